@@ -1,0 +1,280 @@
+"""Host-side mirror of flarellm's ComputeBackend decode hooks over the C-ABI.
+
+`HipBackend` is what a flarellm `Model` would hold as `Box<dyn
+ComputeBackend>` (flare-core/src/model.rs:176-618): it owns one fl_ctx
+(one GPU, one HIP stream), the uploaded weights and the KV cache, and exposes
+the decode entry points with the reference's names and argument meaning.
+Per-op methods take torch tensors (device memory plumbing) and call the HIP
+kernels through ctypes; nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import FL_KV_F16, FL_KV_F32, FlareError, ModelConfig, RawWeight, check
+from .synth import ModelSpec, SynthModel
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class Weight:
+    """A RawWeight uploaded to the device (fl_weight)."""
+
+    def __init__(self, backend: "HipBackend", raw: RawWeight):
+        self._b = backend
+        h = C.c_void_p()
+        check(backend.lib.fl_weight_upload(backend.ctx, C.byref(raw), C.byref(h)), backend.ctx)
+        self.handle = h
+        self.format = raw.format
+        self.rows = raw.num_rows
+        self.blocks_per_row = raw.blocks_per_row
+
+    def free(self):
+        if self.handle:
+            self._b.lib.fl_weight_free(self._b.ctx, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipBackend:
+    """ComputeBackend over libflare_hip.so (name(): model.rs:615)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.load()
+        ctx = C.c_void_p()
+        check(self.lib.fl_ctx_create(device, C.byref(ctx)))
+        self.ctx = ctx
+        self.spec: ModelSpec | None = None
+        self._keep = []  # host buffers referenced by the last upload
+
+    # ---- lifecycle ---------------------------------------------------------
+    def name(self) -> str:
+        return self.lib.fl_backend_name().decode()
+
+    def close(self):
+        if self.ctx:
+            self.lib.fl_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return self.lib.fl_ctx_stream(self.ctx)
+
+    def sync(self):
+        check(self.lib.fl_sync(self.ctx), self.ctx)
+
+    def _torch_sync(self):
+        import torch
+
+        torch.cuda.synchronize()
+
+    # ---- per-op entry points (torch tensors on cuda) ------------------------
+    def upload(self, qw) -> Weight:
+        return Weight(self, qw.raw() if hasattr(qw, "raw") else qw)
+
+    def quantize_q8(self, x):
+        """quantize_input_q8_0_into (model.rs:5534-5571) -> (q, scales, sums)."""
+        import torch
+
+        n = x.numel()
+        q = torch.empty(n, dtype=torch.int8, device=x.device)
+        s = torch.empty(n // 32, dtype=torch.float32, device=x.device)
+        su = torch.empty(n // 32, dtype=torch.int32, device=x.device)
+        self._torch_sync()
+        check(self.lib.fl_op_quantize_q8(self.ctx, _ptr(x), n, _ptr(q), _ptr(s), _ptr(su)), self.ctx)
+        self.sync()
+        return q, s, su
+
+    def rmsnorm_quantize_q8(self, x, w, eps: float, order: int = 0):
+        import torch
+
+        n = x.numel()
+        q = torch.empty(n, dtype=torch.int8, device=x.device)
+        s = torch.empty(n // 32, dtype=torch.float32, device=x.device)
+        su = torch.empty(n // 32, dtype=torch.int32, device=x.device)
+        self._torch_sync()
+        check(self.lib.fl_op_rmsnorm_quantize_q8(self.ctx, _ptr(x), _ptr(w), n, eps, order, _ptr(q), _ptr(s),
+                                                 _ptr(su)), self.ctx)
+        self.sync()
+        return q, s, su
+
+    def rmsnorm(self, x, w, eps: float):
+        import torch
+
+        out = torch.empty_like(x)
+        self._torch_sync()
+        check(self.lib.fl_op_rmsnorm(self.ctx, _ptr(x), _ptr(w), x.numel(), eps, _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
+    def matvec_q8in(self, w: Weight, q, s, su):
+        import torch
+
+        out = torch.empty(w.rows, dtype=torch.float32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_matvec_q8in(self.ctx, w.handle, _ptr(q), _ptr(s), _ptr(su), _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
+    def matvec_f32in(self, w: Weight, x):
+        import torch
+
+        out = torch.empty(w.rows, dtype=torch.float32, device=x.device)
+        self._torch_sync()
+        check(self.lib.fl_op_matvec_f32in(self.ctx, w.handle, _ptr(x), _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
+    def block_dots(self, w: Weight, q):
+        import torch
+
+        per_row = w.blocks_per_row * (8 if w.format == _lib.FL_Q4K else 1)
+        out = torch.empty(w.rows * per_row, dtype=torch.int32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_block_dots(self.ctx, w.handle, _ptr(q), _ptr(out)), self.ctx)
+        self.sync()
+        return out.view(w.rows, per_row)
+
+    def dequant(self, w: Weight, cols: int):
+        import torch
+
+        out = torch.empty(w.rows * cols, dtype=torch.float32, device="cuda")
+        self._torch_sync()
+        check(self.lib.fl_op_dequant(self.ctx, w.handle, _ptr(out)), self.ctx)
+        self.sync()
+        return out.view(w.rows, cols)
+
+    def matvec_argmax(self, w: Weight, q=None, s=None, su=None, x=None):
+        import torch
+
+        dev = (q if q is not None else x).device
+        idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        val = torch.zeros(1, dtype=torch.float32, device=dev)
+        self._torch_sync()
+        check(self.lib.fl_op_matvec_argmax(self.ctx, w.handle, _ptr(q), _ptr(s), _ptr(su), _ptr(x), _ptr(idx),
+                                           _ptr(val)), self.ctx)
+        self.sync()
+        return int(idx.item()), float(val.item())
+
+    def rope(self, data, num_heads: int, head_dim: int, pos: int, theta: float):
+        """apply_rope_with_table in place (model.rs:7256-7297)."""
+        self._torch_sync()
+        check(self.lib.fl_op_rope(self.ctx, _ptr(data), num_heads, head_dim, pos, theta), self.ctx)
+        self.sync()
+        return data
+
+    def silu_mul(self, gate, up):
+        import torch
+
+        out = torch.empty_like(gate)
+        self._torch_sync()
+        check(self.lib.fl_op_silu_mul(self.ctx, _ptr(gate), _ptr(up), gate.numel(), _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
+    def attention(self, q, k_cache, v_cache, num_heads: int, num_kv_heads: int, head_dim: int, seq_len: int,
+                  num_splits: int = 0):
+        """grouped_query_attention over a [slots, nkv, hd] cache (model.rs:9849)."""
+        import torch
+
+        fmt = FL_KV_F16 if k_cache.dtype == torch.float16 else FL_KV_F32
+        out = torch.empty(num_heads * head_dim, dtype=torch.float32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_attention(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache), fmt, num_heads,
+                                       num_kv_heads, head_dim, seq_len, num_splits, _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
+    # ---- model decode hooks -------------------------------------------------
+    def init_gpu_kv_cache(self, spec: ModelSpec, kv_format: int = FL_KV_F16):
+        """init_gpu_kv_cache (model.rs:274) with the model config."""
+        cfg = ModelConfig(spec.hidden, spec.layers, spec.heads, spec.kv_heads, spec.head_dim, spec.inter,
+                          spec.vocab, spec.max_seq, spec.eps, spec.theta)
+        check(self.lib.fl_model_init(self.ctx, C.byref(cfg), kv_format), self.ctx)
+        self.spec = spec
+
+    def upload_weights_to_gpu(self, model: SynthModel):
+        """upload_weights_to_gpu (model.rs:526) from raw GGUF-layout weights."""
+        L = model.spec.layers
+        raws = (RawWeight * (7 * L))()
+        for l, ws in enumerate(model.layers):
+            for j, w in enumerate(ws):
+                raws[7 * l + j] = w.raw()
+        an = (C.c_void_p * L)(*[a.ctypes.data for a in model.attn_norms])
+        fn = (C.c_void_p * L)(*[a.ctypes.data for a in model.ffn_norms])
+        emb = model.embedding.raw()
+        out = model.output.raw() if model.output is not None else None
+        check(self.lib.fl_upload_weights(self.ctx, raws, an, fn, model.output_norm.ctypes.data, C.byref(emb),
+                                         C.byref(out) if out is not None else None), self.ctx)
+
+    def has_gpu_weights(self) -> bool:
+        return bool(self.lib.fl_has_weights(self.ctx))
+
+    def has_gpu_kv_cache(self) -> bool:
+        return bool(self.lib.fl_has_kv_cache(self.ctx))
+
+    def gpu_kv_write(self, layer: int, position: int, key: np.ndarray, value: np.ndarray):
+        key = np.ascontiguousarray(key, np.float32)
+        value = np.ascontiguousarray(value, np.float32)
+        check(self.lib.fl_kv_write(self.ctx, layer, position, key.ctypes.data, value.ctypes.data), self.ctx)
+
+    def reset(self):
+        check(self.lib.fl_reset(self.ctx), self.ctx)
+
+    def forward_greedy(self, token: int, pos: int) -> tuple[int, float]:
+        """Model::forward_greedy (model.rs:1872-1942) on the device."""
+        t = C.c_int32()
+        v = C.c_float()
+        check(self.lib.fl_decode_step(self.ctx, token, pos, None, C.byref(t), C.byref(v)), self.ctx)
+        return t.value, v.value
+
+    def forward_single_token_gpu(self, token: int, pos: int) -> np.ndarray:
+        """forward_single_token_gpu (model.rs:555): full logits."""
+        out = np.empty(self.spec.vocab, np.float32)
+        t = C.c_int32()
+        v = C.c_float()
+        check(self.lib.fl_decode_step(self.ctx, token, pos, out.ctypes.data, C.byref(t), C.byref(v)), self.ctx)
+        return out
+
+    def generate(self, prompt, n_gen: int) -> np.ndarray:
+        """Greedy Generator loop (generate.rs:186-206), device-resident."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(n_gen, np.uint32)
+        check(self.lib.fl_generate(self.ctx, prompt.ctypes.data, prompt.size, n_gen, out.ctypes.data), self.ctx)
+        return out
+
+    def decode_continue(self, n_steps: int):
+        """Enqueue n_steps more device-resident greedy steps (asynchronous)."""
+        check(self.lib.fl_decode_continue(self.ctx, n_steps), self.ctx)
+
+    def read_tokens(self, start: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.uint32)
+        check(self.lib.fl_read_tokens(self.ctx, start, n, out.ctypes.data), self.ctx)
+        return out
+
+    def bench_layer_kernel(self, which: int, iters: int) -> float:
+        b = C.c_double()
+        check(self.lib.fl_bench_layer_kernel(self.ctx, which, iters, C.byref(b)), self.ctx)
+        return b.value
+
+    def bench_kernel_name(self, which: int) -> str:
+        return self.lib.fl_bench_kernel_name(self.ctx, which).decode()
+
+
+__all__ = ["HipBackend", "Weight", "FlareError"]

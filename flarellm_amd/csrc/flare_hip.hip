@@ -1,0 +1,1655 @@
+// flare_hip.hip -- MI355X (gfx950) decode backend for flarellm: kernels and
+// the C-ABI declared in include/flare_hip.h.
+//
+// Decode step = one HIP graph (captured once, replayed per token):
+//   embed      token select (prompt or previous argmax) + embedding row dequant
+//   per layer: qkv      RMSNorm+Q8 quantize prologue, fused [wq;wk;wv] matvec
+//              attn     RoPE(q,k) + KV store + split-K online softmax with a
+//                       last-workgroup merge that also Q8-quantizes the output
+//              wo       matvec + residual add into x
+//              gate_up  RMSNorm+Q8 prologue, [w_gate;w_up] matvec, SiLU*up and
+//                       Q8 quantize epilogue
+//              down     matvec + residual add into x
+//   out        final RMSNorm prologue, output matvec with fused argmax
+// Every kernel reads the token position from device memory, so replays need
+// no host work.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/flare_hip.h"
+#include "kernels.h"
+
+using namespace fl;
+
+// =====================================================================
+// Kernels
+// =====================================================================
+
+__global__ __launch_bounds__(kThreads) void k_quantize(const float *x, int nblk, int8_t *q,
+                                                       float *s, int *sums) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float4 t = ((const float4 *)(x + b * 32))[j];
+        v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+    }
+    quant_block32(v, q + b * 32, s + b, sums + b);
+}
+
+template <int PRO>
+__global__ __launch_bounds__(kThreads) void k_norm_quant(const float *x, const float *w, int n,
+                                                         float eps, int8_t *q, float *s, int *sums) {
+    __shared__ float red[8];
+    stage_q8<PRO>(x, w, eps, n, nullptr, nullptr, nullptr, q, s, sums, red);
+}
+
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const float *w, int n,
+                                                      float eps, float *out) {
+    __shared__ float red[8];
+    const float inv = wg_inv_rms(x, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] * inv) * w[i];
+}
+
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_ARGMAX = 2 };
+
+template <int R>
+__device__ __forceinline__ void group_argmax_commit(const float *acc, int row0, int rows, int gl,
+                                                    unsigned long long *slot,
+                                                    unsigned long long *lred) {
+    // strict '>' over rows in ascending order keeps the first maximum
+    unsigned long long best = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (row0 + r < rows) {
+            unsigned long long k = argmax_key(acc[r], (uint32_t)(row0 + r));
+            best = k > best ? k : best;
+        }
+    }
+    (void)gl;
+    // wave max (all groups of the wave share it; max is order-independent)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned long long t = __shfl_xor(best, o, 64);
+        best = t > best ? t : best;
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lred[w] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = lred[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); i++) b = lred[i] > b ? lred[i] : b;
+        atomicMax(slot, b);
+    }
+}
+
+// Generic Q8-input matvec.  Groups of LPR lanes own R consecutive rows.
+template <int FMT, int LPR, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void k_mv_q8in(WDesc W, const float *x, const float *nw,
+                                                      float eps, const int8_t *gq, const float *gs,
+                                                      const int *gsum, float *out,
+                                                      unsigned long long *slot) {
+    extern __shared__ __align__(16) char smem[];
+    const int K = W.cols;
+    int8_t *lq = (int8_t *)smem;
+    float *ls = (float *)(smem + K);
+    int *lsum = (int *)(ls + (K >> 5));
+    float *red = (float *)(lsum + (K >> 5));
+    stage_q8<PRO>(x, nw, eps, K, gq, gs, gsum, lq, ls, lsum, red);
+    constexpr int G = kThreads / LPR;
+    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * G + grp) * R;
+    int rix[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rix[r] = min(row0 + r, W.rows - 1);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    if (row0 < W.rows) rows_q8in<FMT, LPR, R>(W, rix, lq, ls, lsum, gl, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
+    if (EPI == EPI_ARGMAX) {
+        group_argmax_commit<R>(acc, row0, W.rows, gl, slot, (unsigned long long *)red);
+        return;
+    }
+    if (gl < R && row0 + gl < W.rows) {
+        float v = acc[0];
+#pragma unroll
+        for (int r = 1; r < R; r++) v = (gl == r) ? acc[r] : v;
+        if (EPI == EPI_STORE) out[row0 + gl] = v;
+        else out[row0 + gl] += v;
+    }
+}
+
+// Fused gate/up matvec over W = [w_gate; w_up] (F rows each) with the
+// SiLU(gate)*up (model.rs:9788-9795) and quantize_input_q8_0 (5557-5570)
+// epilogue.  Workgroup b produces hidden block b (32 values).
+template <int FMT, int LPR, int PRO>
+__global__ __launch_bounds__(kThreads) void k_gateup(WDesc W, int F, const float *x,
+                                                     const float *nw, float eps, const int8_t *gq,
+                                                     const float *gs, const int *gsum, int8_t *hq,
+                                                     float *hs, int *hsum, float *hout) {
+    extern __shared__ __align__(16) char smem[];
+    const int K = W.cols;
+    int8_t *lq = (int8_t *)smem;
+    float *ls = (float *)(smem + K);
+    int *lsum = (int *)(ls + (K >> 5));
+    float *red = (float *)(lsum + (K >> 5));
+    float *gu = red + 8;  // [64]: gate[32], up[32]
+    stage_q8<PRO>(x, nw, eps, K, gq, gs, gsum, lq, ls, lsum, red);
+    constexpr int G = kThreads / LPR;
+    constexpr int R = 64 / G;
+    constexpr int RH = R / 2;
+    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+    const int i0 = blockIdx.x * 32 + grp * RH;
+    int rix[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rix[r] = (r < RH) ? (i0 + r) : (F + i0 + r - RH);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    rows_q8in<FMT, LPR, R>(W, rix, lq, ls, lsum, gl, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
+    if (gl == 0) {
+#pragma unroll
+        for (int r = 0; r < RH; r++) {
+            gu[grp * RH + r] = acc[r];
+            gu[32 + grp * RH + r] = acc[RH + r];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float h[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float g = gu[j];
+            h[j] = (g / (1.0f + expf(-g))) * gu[32 + j];
+        }
+        if (hout) {
+            for (int j = 0; j < 32; j++) hout[blockIdx.x * 32 + j] = h[j];
+        }
+        quant_block32(h, hq + blockIdx.x * 32, hs + blockIdx.x, hsum + blockIdx.x);
+    }
+}
+
+// f32-input matvec (logits path).  PRO 0: x loaded as is; PRO 1: final
+// rmsnorm_into (model.rs:2553-2558) computed per workgroup.
+template <int FMT, int LPR, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void k_mv_f32in(WDesc W, const float *x, const float *nw,
+                                                       float eps, float *out,
+                                                       unsigned long long *slot) {
+    extern __shared__ __align__(16) char smem[];
+    const int K = W.cols;
+    float *lx = (float *)smem;
+    float *red = lx + K;
+    if (PRO == 1) {
+        const float inv = wg_inv_rms(x, K, eps, red);
+        for (int i = threadIdx.x; i < K; i += blockDim.x) lx[i] = (x[i] * inv) * nw[i];
+    } else {
+        for (int i = threadIdx.x; i < K; i += blockDim.x) lx[i] = x[i];
+    }
+    __syncthreads();
+    constexpr int G = kThreads / LPR;
+    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * G + grp) * R;
+    int rix[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rix[r] = min(row0 + r, W.rows - 1);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    if (row0 < W.rows) rows_f32in<FMT, LPR, R>(W, rix, lx, gl, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
+    if (EPI == EPI_ARGMAX) {
+        group_argmax_commit<R>(acc, row0, W.rows, gl, slot, (unsigned long long *)red);
+        return;
+    }
+    if (gl < R && row0 + gl < W.rows) {
+        float v = acc[0];
+#pragma unroll
+        for (int r = 1; r < R; r++) v = (gl == r) ? acc[r] : v;
+        out[row0 + gl] = v;
+    }
+}
+
+// Per-block integer dots (parity surface).  One thread per unit.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_block_dots(WDesc W, const int8_t *xq, int *dots) {
+    if (FMT == F_Q8_0) {
+        const int bpr = W.cols >> 5;
+        const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= (long long)W.rows * bpr) return;
+        const int row = (int)(i / bpr), b = (int)(i % bpr);
+        const int4 *p = (const int4 *)(W.q + (size_t)row * W.cols + b * 32);
+        const int4 *xp = (const int4 *)(xq + b * 32);
+        dots[i] = dot16(p[1], xp[1], dot16(p[0], xp[0], 0));
+    } else {
+        const int nsb = W.cols >> 8;
+        const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= (long long)W.rows * nsb * 4) return;
+        const int sub = (int)(i & 3);
+        const long long rs = i >> 2;
+        const int row = (int)(rs / nsb), sb = (int)(rs % nsb);
+        const uint8_t *blk = W.q + ((size_t)row * nsb + sb) * 144;
+        const int4 a = *(const int4 *)(blk + 16 + 32 * sub), c = *(const int4 *)(blk + 32 + 32 * sub);
+        const int blo = sb * 8 + sub, bhi = blo + 4;
+        const int4 *xl = (const int4 *)(xq + blo * 32), *xh = (const int4 *)(xq + bhi * 32);
+        const int4 lo0 = make_int4(a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F);
+        const int4 lo1 = make_int4(c.x & 0x0F0F0F0F, c.y & 0x0F0F0F0F, c.z & 0x0F0F0F0F, c.w & 0x0F0F0F0F);
+        const int4 hi0 = make_int4((a.x >> 4) & 0x0F0F0F0F, (a.y >> 4) & 0x0F0F0F0F,
+                                   (a.z >> 4) & 0x0F0F0F0F, (a.w >> 4) & 0x0F0F0F0F);
+        const int4 hi1 = make_int4((c.x >> 4) & 0x0F0F0F0F, (c.y >> 4) & 0x0F0F0F0F,
+                                   (c.z >> 4) & 0x0F0F0F0F, (c.w >> 4) & 0x0F0F0F0F);
+        dots[rs * 8 + 2 * sub] = dot16(lo1, xl[1], dot16(lo0, xl[0], 0));
+        dots[rs * 8 + 2 * sub + 1] = dot16(hi1, xh[1], dot16(hi0, xh[0], 0));
+    }
+}
+
+// Dequantize (dequantize_tensor, gguf.rs:717-880) one 32-value group per thread.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_dequant(WDesc W, float *out) {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // 32-value group
+    const int gpr = W.cols >> 5;
+    if (g >= (long long)W.rows * gpr) return;
+    const int row = (int)(g / gpr), j = (int)(g % gpr);
+    float *o = out + (size_t)row * W.cols + (size_t)j * 32;
+    if (FMT == F_Q8_0) {
+        const float scale = h2f(W.s[(size_t)row * gpr + j]);
+        const int8_t *q = (const int8_t *)W.q + (size_t)row * W.cols + j * 32;
+        for (int k = 0; k < 32; k++) o[k] = (float)q[k] * scale;
+    } else if (FMT == F_Q4K) {
+        const int sb = j >> 3, sblk = j & 7;
+        const uint8_t *blk = W.q + ((size_t)row * (W.cols >> 8) + sb) * 144;
+        const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
+        const uint8_t *s = blk + 4;
+        const int i = sblk & 3;
+        uint32_t sc, mn;
+        if (sblk < 4) {
+            sc = s[i] & 63;
+            mn = s[i + 4] & 63;
+        } else {
+            sc = (s[i] >> 6) | ((s[i + 8] & 0xF) << 2);
+            mn = (s[i + 4] >> 6) | ((s[i + 8] >> 4) << 2);
+        }
+        const uint8_t *qs = blk + 16 + 32 * i;
+        for (int k = 0; k < 32; k++) {
+            const float v = (float)(sblk < 4 ? (qs[k] & 0xF) : (qs[k] >> 4));
+            o[k] = d * (float)sc * v - dmin * (float)mn;
+        }
+    } else if (FMT == F_Q6K) {
+        const int nsb = W.cols >> 8, sb = j >> 3, e0 = (j & 7) * 32;
+        const uint8_t *body = W.q + ((size_t)row * nsb + sb) * 208;
+        const float d = h2f(W.s[(size_t)row * nsb + sb]);
+        for (int k = 0; k < 32; k++) {
+            const int e = e0 + k, hf = e >> 7, r = e & 127, grp = r >> 5, l = r & 31;
+            const uint8_t la = body[64 * hf + l], lb = body[64 * hf + 32 + l], hh = body[128 + 32 * hf + l];
+            int q;
+            switch (grp) {
+            case 0: q = (int)((la & 0xF) | ((hh & 3) << 4)) - 32; break;
+            case 1: q = (int)((lb & 0xF) | (((hh >> 2) & 3) << 4)) - 32; break;
+            case 2: q = (int)((la >> 4) | (((hh >> 4) & 3) << 4)) - 32; break;
+            default: q = (int)((lb >> 4) | (((hh >> 6) & 3) << 4)) - 32; break;
+            }
+            const float sc = (float)(int8_t)body[192 + hf * 8 + (l >> 4) + 2 * grp];
+            o[k] = d * sc * (float)q;
+        }
+    } else {
+        const float *src = (const float *)W.q + (size_t)row * W.cols + j * 32;
+        for (int k = 0; k < 32; k++) o[k] = src[k];
+    }
+}
+
+// apply_rope_with_table, x86 branch (model.rs:7283-7296).
+__global__ __launch_bounds__(kThreads) void k_rope(float *data, int num_heads, int head_dim,
+                                                   const float *cs, const float *sn) {
+    const int half = head_dim / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= num_heads * half) return;
+    const int h = i / half, d = i % half;
+    float *p = data + h * head_dim;
+    const float c = cs[d], s = sn[d], x0 = p[d], x1 = p[d + half];
+    p[d] = x0 * c - x1 * s;
+    p[d + half] = x0 * s + x1 * c;
+}
+
+__global__ __launch_bounds__(kThreads) void k_silu_mul(const float *g, const float *u, int n,
+                                                       float *out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    out[i] = (gv / (1.0f + expf(-gv))) * u[i];
+}
+
+// ---------------------------------------------------------------------------
+// Split-K GQA decode attention (cpu_grouped_query_attention_into semantics,
+// model.rs:9849-9966).  Grid (nsplit, num_kv_heads); workgroup (s, kvh)
+// handles the G query heads sharing kv head kvh over token chunk s, then the
+// last workgroup of each kv head merges the chunk partials (flash-decode
+// rescale) and writes the f32 output plus its Q8_0 quantization.
+// When `knew` is set, q/k arrive un-rotated (QKV matvec output): RoPE is
+// applied here and the chunk holding slot `pos` stores the new K/V.
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+    const float *q;      // [nh*D]
+    const float *knew;   // [nkv*D] un-rotated new key (or null)
+    const float *vnew;   // [nkv*D]
+    const float *rope;   // rope table base: cos [maxpos][D/2] then sin at +sin_off
+    long long sin_off;
+    void *kc, *vc;       // cache for this layer: [slots][nkv][D]
+    const int *posp;     // attends slots 0..*posp
+    int nkv, nsplit, chmax;
+    float *part;         // [nkv][nsplit][G][D+2]
+    int *counters;       // [nkv]
+    float *out;          // [nh*D]
+    int8_t *oq;          // optional Q8 output
+    float *os;
+    int *osum;
+};
+
+template <typename KT>
+__device__ __forceinline__ void load8(const KT *p, float *v);
+template <>
+__device__ __forceinline__ void load8<__half>(const __half *p, float *v) {
+    const int4 t = *(const int4 *)p;
+    const uint32_t w[4] = {(uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = h2f((uint16_t)(w[i] & 0xFFFF));
+        v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+    }
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float *p, float *v) {
+    const float4 a = ((const float4 *)p)[0], b = ((const float4 *)p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ float kv_round(float v, const __half *) { return h2f(f2h(v)); }
+__device__ __forceinline__ float kv_round(float v, const float *) { return v; }
+__device__ __forceinline__ void kv_store(__half *p, float v) { *p = __ushort_as_half(f2h(v)); }
+__device__ __forceinline__ void kv_store(float *p, float v) { *p = v; }
+
+template <typename KT, int D, int G>
+__global__ __launch_bounds__(kThreads) void k_attn(AttnArgs a) {
+    constexpr int EPL = 8;              // elements per lane per token row
+    constexpr int LPT = D / EPL;        // lanes per token row (8 or 16)
+    constexpr int TPP = kThreads / LPT; // tokens per pass
+    extern __shared__ __align__(16) float sm[];
+    float *qs = sm;                     // [G][D]
+    float *kn = qs + G * D;             // [D]
+    float *vn = kn + D;                 // [D]
+    float *sc = vn + D;                 // [G][chmax]
+    float *red = sc + G * a.chmax;      // [waves][G][D] (PV partials) / scratch
+    __shared__ float mls[2 * G];
+    __shared__ int is_last;
+
+    const int kvh = blockIdx.y, s = blockIdx.x, tid = threadIdx.x;
+    const int pos = *a.posp;
+    const int T = pos + 1;
+    const int CH = (T + a.nsplit - 1) / a.nsplit;
+    const int t0 = s * CH, t1 = min(T, t0 + CH);
+    const int nact = (T + CH - 1) / CH;
+    if (t0 >= T) return;
+    const int half = D / 2;
+    const bool rot = a.knew != nullptr;
+    const float *cs = a.rope + (size_t)pos * half;
+    const float *sn = cs + a.sin_off;
+    for (int i = tid; i < G * D; i += kThreads) {
+        const int g = i / D, d = i % D;
+        const float *qh = a.q + (size_t)(kvh * G + g) * D;
+        float v;
+        if (rot) {
+            if (d < half) v = qh[d] * cs[d] - qh[d + half] * sn[d];
+            else v = qh[d - half] * sn[d - half] + qh[d] * cs[d - half];
+        } else {
+            v = qh[d];
+        }
+        qs[i] = v;
+    }
+    const bool has_new = rot && (t1 == T);
+    KT *kc = (KT *)a.kc, *vc = (KT *)a.vc;
+    if (has_new) {
+        const float *kh = a.knew + (size_t)kvh * D, *vh = a.vnew + (size_t)kvh * D;
+        for (int d = tid; d < D; d += kThreads) {
+            float kr;
+            if (d < half) kr = kh[d] * cs[d] - kh[d + half] * sn[d];
+            else kr = kh[d - half] * sn[d - half] + kh[d] * cs[d - half];
+            kr = kv_round(kr, (const KT *)nullptr);
+            const float vr = kv_round(vh[d], (const KT *)nullptr);
+            kn[d] = kr;
+            vn[d] = vr;
+            kv_store(kc + ((size_t)pos * a.nkv + kvh) * D + d, kr);
+            kv_store(vc + ((size_t)pos * a.nkv + kvh) * D + d, vr);
+        }
+    }
+    __syncthreads();
+
+    const float scale = 1.0f / sqrtf((float)D);
+    const int tk = tid / LPT, c = tid % LPT;
+    float qr[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qr[g][e] = qs[g * D + c * EPL + e];
+    for (int t = t0 + tk; t < t1; t += TPP) {
+        float kv[EPL];
+        if (has_new && t == pos) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) kv[e] = kn[c * EPL + e];
+        } else {
+            load8<KT>(kc + ((size_t)t * a.nkv + kvh) * D + c * EPL, kv);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float p = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) p += qr[g][e] * kv[e];
+            p = group_sum<LPT>(p);
+            if (c == 0) sc[g * a.chmax + (t - t0)] = p * scale;
+        }
+    }
+    __syncthreads();
+    // chunk softmax statistics, one wave per head
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = t1 - t0;
+    for (int g = wave; g < G; g += kThreads / 64) {
+        float m = -INFINITY;
+        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * a.chmax + i]);
+        m = group_max<64>(m);
+        float l = 0.0f;
+        for (int i = lane; i < n; i += 64) {
+            const float p = expf(sc[g * a.chmax + i] - m);
+            sc[g * a.chmax + i] = p;
+            l += p;
+        }
+        l = group_sum<64>(l);
+        if (lane == 0) { mls[2 * g] = m; mls[2 * g + 1] = l; }
+    }
+    __syncthreads();
+    float acc[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
+    for (int t = t0 + tk; t < t1; t += TPP) {
+        float vv[EPL];
+        if (has_new && t == pos) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) vv[e] = vn[c * EPL + e];
+        } else {
+            load8<KT>(vc + ((size_t)t * a.nkv + kvh) * D + c * EPL, vv);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float p = sc[g * a.chmax + (t - t0)];
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[g][e] += p * vv[e];
+        }
+    }
+    // reduce the token groups of a wave with shuffles, then the 4 waves in LDS
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            float v = acc[g][e];
+#pragma unroll
+            for (int o = LPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+            acc[g][e] = v;
+        }
+    if (lane < LPT) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int e = 0; e < EPL; e++) red[(wave * G + g) * D + c * EPL + e] = acc[g][e];
+    }
+    __syncthreads();
+    const int P = G * (D + 2);
+    float *mypart = a.part + ((size_t)kvh * a.nsplit + s) * P;
+    for (int i = tid; i < G * D; i += kThreads) {
+        float o = 0.0f;
+        for (int j = 0; j < kThreads / 64; j++) o += red[j * G * D + i];
+        mypart[i] = o;
+    }
+    if (tid < G) {
+        mypart[G * D + 2 * tid] = mls[2 * tid];
+        mypart[G * D + 2 * tid + 1] = mls[2 * tid + 1];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const int old = atomicAdd(&a.counters[kvh], 1);
+        is_last = (old == nact - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    // merge the nact chunk partials of this kv head
+    float *mo = red;  // [G][D]
+    for (int i = tid; i < G * D; i += kThreads) {
+        const int g = i / D;
+        float M = -INFINITY;
+        for (int j = 0; j < nact; j++) {
+            const float *pj = a.part + ((size_t)kvh * a.nsplit + j) * P;
+            M = fmaxf(M, __builtin_nontemporal_load(pj + G * D + 2 * g));
+        }
+        float L = 0.0f, O = 0.0f;
+        for (int j = 0; j < nact; j++) {
+            const float *pj = a.part + ((size_t)kvh * a.nsplit + j) * P;
+            const float f = expf(__builtin_nontemporal_load(pj + G * D + 2 * g) - M);
+            L += __builtin_nontemporal_load(pj + G * D + 2 * g + 1) * f;
+            O += __builtin_nontemporal_load(pj + i) * f;
+        }
+        const float inv = 1.0f / L;
+        const float v = O * inv;
+        mo[i] = v;
+        a.out[(size_t)kvh * G * D + i] = v;
+    }
+    __syncthreads();
+    if (tid == 0) a.counters[kvh] = 0;
+    if (a.oq) {
+        const int nb = G * D / 32;
+        for (int b = tid; b < nb; b += kThreads) {
+            const int gb = kvh * nb + b;
+            quant_block32(mo + b * 32, a.oq + gb * 32, a.os + gb, a.osum + gb);
+        }
+    }
+}
+
+// Decode-step head: choose the token (prompt slot or previous argmax) and
+// dequantize its embedding row into x (token_embedding lookup, model.rs:1964).
+struct DevState {
+    int step;     // next step to run
+    int pos;      // position of the step in flight
+    int n_prompt; // steps < n_prompt read tokens[step]
+    int pad;
+    unsigned long long argmax;
+};
+
+__device__ __forceinline__ uint32_t key_index(unsigned long long k) {
+    return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x) {
+    __shared__ int tok_s, step_s;
+    if (threadIdx.x == 0) {
+        const int s = st->step;
+        int tok;
+        if (s < st->n_prompt) {
+            tok = tokens[s];
+        } else {
+            tok = (int)key_index(st->argmax);
+            tokens[s] = tok;
+        }
+        tok = min(max(tok, 0), E.rows - 1);
+        tok_s = tok;
+        step_s = s;
+    }
+    __syncthreads();
+    const int row = tok_s, H = E.cols;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v;
+        if (FMT == F_Q8_0) {
+            v = (float)((const int8_t *)E.q)[(size_t)row * H + i] * h2f(E.s[(size_t)row * (H >> 5) + (i >> 5)]);
+        } else if (FMT == F_Q6K) {
+            const int nsb = H >> 8, sb = i >> 8, e = i & 255, hf = e >> 7, r = e & 127, grp = r >> 5, l = r & 31;
+            const uint8_t *body = E.q + ((size_t)row * nsb + sb) * 208;
+            const uint8_t la = body[64 * hf + l], lb = body[64 * hf + 32 + l], hh = body[128 + 32 * hf + l];
+            int q;
+            switch (grp) {
+            case 0: q = (int)((la & 0xF) | ((hh & 3) << 4)) - 32; break;
+            case 1: q = (int)((lb & 0xF) | (((hh >> 2) & 3) << 4)) - 32; break;
+            case 2: q = (int)((la >> 4) | (((hh >> 4) & 3) << 4)) - 32; break;
+            default: q = (int)((lb >> 4) | (((hh >> 6) & 3) << 4)) - 32; break;
+            }
+            const float sc = (float)(int8_t)body[192 + hf * 8 + (l >> 4) + 2 * grp];
+            v = h2f(E.s[(size_t)row * nsb + sb]) * sc * (float)q;
+        } else if (FMT == F_Q4K) {
+            const int nsb = H >> 8, sb = i >> 8, e = i & 255, sblk = e >> 5, k = e & 31, ii = sblk & 3;
+            const uint8_t *blk = E.q + ((size_t)row * nsb + sb) * 144;
+            const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
+            const uint8_t *s = blk + 4;
+            uint32_t sc, mn;
+            if (sblk < 4) { sc = s[ii] & 63; mn = s[ii + 4] & 63; }
+            else { sc = (s[ii] >> 6) | ((s[ii + 8] & 0xF) << 2); mn = (s[ii + 4] >> 6) | ((s[ii + 8] >> 4) << 2); }
+            const uint8_t qb = blk[16 + 32 * ii + k];
+            v = d * (float)sc * (float)(sblk < 4 ? (qb & 0xF) : (qb >> 4)) - dmin * (float)mn;
+        } else {
+            v = ((const float *)E.q)[(size_t)row * H + i];
+        }
+        x[i] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st->pos = step_s;
+        st->step = step_s + 1;
+        st->argmax = 0ull;
+    }
+}
+
+// =====================================================================
+// Host side
+// =====================================================================
+
+struct fl_weight {
+    int format = 0, rows = 0, cols = 0;
+    void *q = nullptr;      // device
+    void *s = nullptr;      // device (Q8_0 / Q6_K)
+    size_t gguf_bytes = 0;  // algorithmic bytes (GGUF size)
+    WDesc desc() const {
+        WDesc d;
+        d.q = (const uint8_t *)q;
+        d.s = (const uint16_t *)s;
+        d.rows = rows;
+        d.cols = cols;
+        return d;
+    }
+};
+
+struct Layer {
+    fl_weight qkv, wo, gu, down;
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+struct fl_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // op scratch
+    int *d_pos = nullptr;
+    float *d_rope_row = nullptr;  // [2*256]
+    float *d_part = nullptr;
+    size_t part_cap = 0;
+    int *d_counters = nullptr;    // [1024]
+    unsigned long long *d_slot = nullptr;
+    // model
+    bool have_cfg = false, have_weights = false;
+    fl_model_config cfg{};
+    int kv_format = FL_KV_F16;
+    int layer_fmt = FL_Q8_0;
+    std::vector<Layer> layers;
+    fl_weight embed, output;
+    bool tied = true;
+    float *out_norm = nullptr;
+    void *kcache = nullptr, *vcache = nullptr;
+    size_t kv_layer_elems = 0;
+    float *rope = nullptr;
+    int nsplit = 1, chmax = 1;
+    // activations
+    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
+    int8_t *aq = nullptr, *hq = nullptr;
+    float *as = nullptr, *hs = nullptr;
+    int *asum = nullptr, *hsum = nullptr;
+    DevState *st = nullptr;
+    int *tokens = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+};
+
+static std::string g_err;
+static thread_local char g_errbuf[512];
+
+static int fail(fl_ctx *ctx, int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_errbuf, sizeof g_errbuf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = g_errbuf;
+    g_err = g_errbuf;
+    return code;
+}
+
+#define HIPCHK(ctx, expr)                                                                   \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail((ctx), FL_E_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                        __FILE__, __LINE__);                                                \
+    } while (0)
+
+static int dev_alloc(fl_ctx *ctx, void **p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return fail(ctx, FL_E_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    return 0;
+}
+#define ALLOC(ctx, ptr, bytes)                                            \
+    do {                                                                  \
+        int rc_ = dev_alloc((ctx), (void **)&(ptr), (bytes));             \
+        if (rc_) return rc_;                                              \
+    } while (0)
+
+static void weight_release(fl_weight &w) {
+    if (w.q) (void)hipFree(w.q);
+    if (w.s) (void)hipFree(w.s);
+    w.q = w.s = nullptr;
+}
+
+static size_t row_bytes(int fmt, int cols) { return fl_format_row_bytes(fmt, (size_t)cols); }
+
+static int weight_cols(const fl_raw_weight *w) {
+    switch (w->format) {
+    case FL_F32: return w->blocks_per_row;
+    case FL_Q8_0: return w->blocks_per_row * 32;
+    case FL_Q4K:
+    case FL_Q6K: return w->blocks_per_row * 256;
+    }
+    return 0;
+}
+
+// Upload `n` RawWeights sharing format and cols as one row-concatenated
+// device weight (Model::set_raw_weights fusion, model.rs:1411-1452).
+static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws, int n, fl_weight &out) {
+    const int fmt = ws[0]->format, cols = weight_cols(ws[0]);
+    int rows = 0;
+    for (int i = 0; i < n; i++) {
+        if (!ws[i] || !ws[i]->data) return fail(ctx, FL_E_INVALID, "null weight");
+        if (ws[i]->format != fmt || weight_cols(ws[i]) != cols)
+            return fail(ctx, FL_E_INVALID, "fused weights must share format and columns");
+        const size_t need = row_bytes(fmt, cols) * (size_t)ws[i]->num_rows;
+        if (need == 0 || ws[i]->nbytes < need)
+            return fail(ctx, FL_E_INVALID, "weight bytes %zu < rows*row_bytes %zu (format %d, cols %d)",
+                        ws[i]->nbytes, need, fmt, cols);
+        rows += ws[i]->num_rows;
+    }
+    if (fmt != FL_Q8_0 && fmt != FL_Q4K && fmt != FL_Q6K && fmt != FL_F32)
+        return fail(ctx, FL_E_UNSUPPORTED, "weight format %d not supported", fmt);
+    if (fmt == FL_F32 && cols % 4) return fail(ctx, FL_E_INVALID, "f32 cols must be a multiple of 4");
+    out.format = fmt;
+    out.rows = rows;
+    out.cols = cols;
+    out.gguf_bytes = row_bytes(fmt, cols) * (size_t)rows;
+    const size_t R = (size_t)rows;
+    if (fmt == FL_Q4K || fmt == FL_F32) {
+        ALLOC(ctx, out.q, out.gguf_bytes);
+        size_t off = 0;
+        for (int i = 0; i < n; i++) {
+            const size_t b = row_bytes(fmt, cols) * (size_t)ws[i]->num_rows;
+            HIPCHK(ctx, hipMemcpy((uint8_t *)out.q + off, ws[i]->data, b, hipMemcpyHostToDevice));
+            off += b;
+        }
+        return 0;
+    }
+    // Q8_0 -> int8 quants [rows][cols] + f16 scales [rows][cols/32];
+    // Q6_K -> 208-byte bodies [rows][nsb] + f16 d [rows][nsb].
+    const bool q8 = fmt == FL_Q8_0;
+    const size_t nblk = q8 ? (size_t)cols / 32 : (size_t)cols / 256;
+    const size_t body = q8 ? 32 : 208, bsz = q8 ? 34 : 210, doff = q8 ? 0 : 208, boff = q8 ? 2 : 0;
+    ALLOC(ctx, out.q, R * nblk * body);
+    ALLOC(ctx, out.s, R * nblk * 2);
+    std::vector<uint8_t> hq, hs;
+    size_t row_base = 0;
+    for (int i = 0; i < n; i++) {
+        const size_t r = (size_t)ws[i]->num_rows;
+        hq.resize(r * nblk * body);
+        hs.resize(r * nblk * 2);
+        const uint8_t *src = (const uint8_t *)ws[i]->data;
+#pragma omp parallel for schedule(static)
+        for (long long k = 0; k < (long long)(r * nblk); k++) {
+            const uint8_t *b = src + (size_t)k * bsz;
+            std::memcpy(&hq[(size_t)k * body], b + boff, body);
+            hs[(size_t)k * 2] = b[doff];
+            hs[(size_t)k * 2 + 1] = b[doff + 1];
+        }
+        HIPCHK(ctx, hipMemcpy((uint8_t *)out.q + row_base * nblk * body, hq.data(), hq.size(), hipMemcpyHostToDevice));
+        HIPCHK(ctx, hipMemcpy((uint8_t *)out.s + row_base * nblk * 2, hs.data(), hs.size(), hipMemcpyHostToDevice));
+        row_base += r;
+    }
+    return 0;
+}
+
+// ---- launch plans ----------------------------------------------------------
+
+static int units_per_row(int fmt, int cols) {
+    switch (fmt) {
+    case FL_Q8_0: return cols / 32;
+    case FL_Q4K:
+    case FL_Q6K: return cols / 64;
+    default: return cols / 4;
+    }
+}
+static int pick_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
+static int pick_r(int rows, int groups) {
+    for (int r : {8, 4, 2}) {
+        if ((rows + groups * r - 1) / (groups * r) >= 512) return r;
+    }
+    return 1;
+}
+static size_t q8_lds(int K) { return (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64; }
+
+typedef void (*q8in_fn)(WDesc, const float *, const float *, float, const int8_t *, const float *,
+                        const int *, float *, unsigned long long *);
+typedef void (*f32in_fn)(WDesc, const float *, const float *, float, float *, unsigned long long *);
+typedef void (*gu_fn)(WDesc, int, const float *, const float *, float, const int8_t *, const float *,
+                      const int *, int8_t *, float *, int *, float *);
+
+template <int FMT, int PRO, int EPI>
+static q8in_fn q8in_pick(int lpr, int r) {
+#define Q8C(L, RR) \
+    if (lpr == L && r == RR) return k_mv_q8in<FMT, L, RR, PRO, EPI>;
+    Q8C(64, 1) Q8C(64, 2) Q8C(64, 4) Q8C(64, 8)
+    Q8C(32, 1) Q8C(32, 2) Q8C(32, 4) Q8C(32, 8)
+    Q8C(16, 1) Q8C(16, 2) Q8C(16, 4) Q8C(16, 8)
+#undef Q8C
+    return nullptr;
+}
+template <int FMT>
+static q8in_fn q8in_pick_any(int pro, int epi, int lpr, int r) {
+    if (pro == PRO_LOADQ && epi == EPI_STORE) return q8in_pick<FMT, PRO_LOADQ, EPI_STORE>(lpr, r);
+    if (pro == PRO_LOADQ && epi == EPI_ADD) return q8in_pick<FMT, PRO_LOADQ, EPI_ADD>(lpr, r);
+    if (pro == PRO_LOADQ && epi == EPI_ARGMAX) return q8in_pick<FMT, PRO_LOADQ, EPI_ARGMAX>(lpr, r);
+    if (pro == PRO_NORMQ0 && epi == EPI_STORE) return q8in_pick<FMT, PRO_NORMQ0, EPI_STORE>(lpr, r);
+    if (pro == PRO_NORMQ1 && epi == EPI_STORE) return q8in_pick<FMT, PRO_NORMQ1, EPI_STORE>(lpr, r);
+    if (pro == PRO_NORMQ1 && epi == EPI_ARGMAX) return q8in_pick<FMT, PRO_NORMQ1, EPI_ARGMAX>(lpr, r);
+    return nullptr;
+}
+
+template <int FMT, int PRO, int EPI>
+static f32in_fn f32in_pick(int lpr, int r) {
+#define FC(L, RR) \
+    if (lpr == L && r == RR) return k_mv_f32in<FMT, L, RR, PRO, EPI>;
+    FC(64, 1) FC(64, 2) FC(64, 4) FC(64, 8)
+    FC(32, 1) FC(32, 2) FC(32, 4) FC(32, 8)
+    FC(16, 1) FC(16, 2) FC(16, 4) FC(16, 8)
+#undef FC
+    return nullptr;
+}
+template <int FMT>
+static f32in_fn f32in_pick_any(int pro, int epi, int lpr, int r) {
+    if (pro == 0 && epi == EPI_STORE) return f32in_pick<FMT, 0, EPI_STORE>(lpr, r);
+    if (pro == 0 && epi == EPI_ARGMAX) return f32in_pick<FMT, 0, EPI_ARGMAX>(lpr, r);
+    if (pro == 1 && epi == EPI_STORE) return f32in_pick<FMT, 1, EPI_STORE>(lpr, r);
+    if (pro == 1 && epi == EPI_ARGMAX) return f32in_pick<FMT, 1, EPI_ARGMAX>(lpr, r);
+    return nullptr;
+}
+
+struct Plan {
+    int lpr = 64, r = 1, grid = 1;
+    size_t lds = 0;
+};
+
+static Plan plan_for(int fmt, int rows, int cols, bool f32in) {
+    Plan p;
+    p.lpr = pick_lpr(units_per_row(fmt, cols));
+    const int groups = kThreads / p.lpr;
+    p.r = pick_r(rows, groups);
+    p.grid = (rows + groups * p.r - 1) / (groups * p.r);
+    p.lds = f32in ? (size_t)cols * 4 + 64 * 4 : q8_lds(cols);
+    return p;
+}
+
+// Launch a Q8-input matvec with prologue `pro` and epilogue `epi`.
+static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
+                       const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
+                       float *out, unsigned long long *slot, const char **name = nullptr) {
+    const Plan p = plan_for(w.format, w.rows, w.cols, false);
+    q8in_fn fn = nullptr;
+    if (w.format == FL_Q8_0) fn = q8in_pick_any<F_Q8_0>(pro, epi, p.lpr, p.r);
+    else if (w.format == FL_Q4K) fn = q8in_pick_any<F_Q4K>(pro, epi, p.lpr, p.r);
+    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no Q8-input kernel for format %d", w.format);
+    if (name) *name = w.format == FL_Q8_0 ? "k_mv_q8in<Q8_0>" : "k_mv_q8in<Q4_K>";
+    hipLaunchKernelGGL(fn, dim3(p.grid), dim3(kThreads), p.lds, ctx->stream, w.desc(), x, nw, eps, q, s,
+                       sums, out, slot);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+static int launch_f32in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
+                        const float *nw, float eps, float *out, unsigned long long *slot) {
+    const Plan p = plan_for(w.format, w.rows, w.cols, true);
+    f32in_fn fn = nullptr;
+    if (w.format == FL_Q8_0) fn = f32in_pick_any<F_Q8_0>(pro, epi, p.lpr, p.r);
+    else if (w.format == FL_Q6K) fn = f32in_pick_any<F_Q6K>(pro, epi, p.lpr, p.r);
+    else if (w.format == FL_F32) fn = f32in_pick_any<F_F32>(pro, epi, p.lpr, p.r);
+    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no f32-input kernel for format %d", w.format);
+    hipLaunchKernelGGL(fn, dim3(p.grid), dim3(kThreads), p.lds, ctx->stream, w.desc(), x, nw, eps, out, slot);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *x, const float *nw,
+                         float eps, const int8_t *q, const float *s, const int *sums, int8_t *hq,
+                         float *hs, int *hsum, float *hout) {
+    const int F = w.rows / 2;
+    if (w.rows % 2 || F % 32) return fail(ctx, FL_E_INVALID, "gate_up rows %d must be 2*32k", w.rows);
+    const int lpr = pick_lpr(units_per_row(w.format, w.cols));
+    gu_fn fn = nullptr;
+#define GUC(FM, L, P) \
+    if (lpr == L && pro == P) fn = k_gateup<FM, L, P>;
+    if (w.format == FL_Q8_0) {
+        GUC(F_Q8_0, 64, PRO_NORMQ0) GUC(F_Q8_0, 32, PRO_NORMQ0) GUC(F_Q8_0, 16, PRO_NORMQ0)
+        GUC(F_Q8_0, 64, PRO_NORMQ1) GUC(F_Q8_0, 32, PRO_NORMQ1) GUC(F_Q8_0, 16, PRO_NORMQ1)
+        GUC(F_Q8_0, 64, PRO_LOADQ) GUC(F_Q8_0, 32, PRO_LOADQ) GUC(F_Q8_0, 16, PRO_LOADQ)
+    } else if (w.format == FL_Q4K) {
+        GUC(F_Q4K, 64, PRO_NORMQ0) GUC(F_Q4K, 32, PRO_NORMQ0) GUC(F_Q4K, 16, PRO_NORMQ0)
+        GUC(F_Q4K, 64, PRO_NORMQ1) GUC(F_Q4K, 32, PRO_NORMQ1) GUC(F_Q4K, 16, PRO_NORMQ1)
+        GUC(F_Q4K, 64, PRO_LOADQ) GUC(F_Q4K, 32, PRO_LOADQ) GUC(F_Q4K, 16, PRO_LOADQ)
+    }
+#undef GUC
+    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel for format %d", w.format);
+    const size_t lds = q8_lds(w.cols) + 80 * 4;
+    hipLaunchKernelGGL(fn, dim3(F / 32), dim3(kThreads), lds, ctx->stream, w.desc(), F, x, nw, eps, q,
+                       s, sums, hq, hs, hsum, hout);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+typedef void (*attn_fn)(AttnArgs);
+template <typename KT>
+static attn_fn attn_pick(int D, int G) {
+#define AC(DD, GG) \
+    if (D == DD && G == GG) return k_attn<KT, DD, GG>;
+    AC(64, 1) AC(64, 2) AC(64, 3) AC(64, 4) AC(64, 8)
+    AC(128, 1) AC(128, 2) AC(128, 3) AC(128, 4) AC(128, 8)
+#undef AC
+    return nullptr;
+}
+static size_t attn_lds(int D, int G, int chmax) {
+    return (size_t)(G * D + 2 * D + G * chmax + (kThreads / 64) * G * D) * 4;
+}
+
+static int launch_attn(fl_ctx *ctx, int kv_format, int D, int G, AttnArgs &a) {
+    attn_fn fn = kv_format == FL_KV_F16 ? attn_pick<__half>(D, G) : attn_pick<float>(D, G);
+    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "attention: head_dim %d / group %d not supported", D, G);
+    hipLaunchKernelGGL(fn, dim3(a.nsplit, a.nkv), dim3(kThreads), attn_lds(D, G, a.chmax), ctx->stream, a);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+static void choose_splits(int max_seq, int nkv, int &nsplit, int &chmax) {
+    // enough workgroups to cover the chip at long context, chunks <= 512
+    int ns = (max_seq + 63) / 64;
+    ns = std::max(1, std::min(ns, 256));
+    if (ns * nkv < 64) ns = std::min((max_seq + 15) / 16, std::max(ns, 64 / std::max(nkv, 1)));
+    ns = std::max(1, ns);
+    nsplit = ns;
+    chmax = (max_seq + ns - 1) / ns;
+}
+
+static int ensure_part(fl_ctx *ctx, size_t floats) {
+    if (ctx->part_cap >= floats) return 0;
+    if (ctx->d_part) (void)hipFree(ctx->d_part);
+    ctx->d_part = nullptr;
+    ctx->part_cap = 0;
+    ALLOC(ctx, ctx->d_part, floats * 4);
+    ctx->part_cap = floats;
+    return 0;
+}
+
+// =====================================================================
+// C-ABI
+// =====================================================================
+extern "C" {
+
+int fl_abi_version(void) { return FL_ABI_VERSION; }
+const char *fl_backend_name(void) { return "flare-hip (MI355X gfx950)"; }
+
+const char *fl_last_error(const fl_ctx *ctx) { return ctx ? ctx->err.c_str() : g_err.c_str(); }
+
+int fl_ctx_create(int device, fl_ctx **out) {
+    if (!out) return fail(nullptr, FL_E_INVALID, "out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, FL_E_HIP, "no HIP device available");
+    if (device < 0 || device >= n) return fail(nullptr, FL_E_INVALID, "device %d out of range", device);
+    fl_ctx *c = new fl_ctx();
+    c->device = device;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(nullptr, FL_E_HIP, "stream creation failed: %s", hipGetErrorString(e));
+    }
+    int rc = dev_alloc(c, (void **)&c->d_pos, 64);
+    if (!rc) rc = dev_alloc(c, (void **)&c->d_rope_row, 2 * 512 * 4);
+    if (!rc) rc = dev_alloc(c, (void **)&c->d_counters, 1024 * 4);
+    if (!rc) rc = dev_alloc(c, (void **)&c->d_slot, 64);
+    if (rc) {
+        fl_ctx_destroy(c);
+        return rc;
+    }
+    (void)hipMemset(c->d_counters, 0, 1024 * 4);
+    *out = c;
+    return 0;
+}
+
+static void model_release(fl_ctx *c) {
+    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->gexec = nullptr;
+    c->graph = nullptr;
+    for (auto &l : c->layers) {
+        weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
+        if (l.attn_norm) (void)hipFree(l.attn_norm);
+        if (l.ffn_norm) (void)hipFree(l.ffn_norm);
+    }
+    c->layers.clear();
+    weight_release(c->embed);
+    weight_release(c->output);
+    void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits,
+                    c->aq, c->hq, c->as, c->hs, c->asum, c->hsum, c->st, c->tokens};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
+    c->attn = c->logits = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
+    c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
+    c->have_cfg = c->have_weights = false;
+}
+
+void fl_ctx_destroy(fl_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    model_release(ctx);
+    void *ptrs[] = {ctx->d_pos, ctx->d_rope_row, ctx->d_part, ctx->d_counters, ctx->d_slot};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+void *fl_ctx_stream(fl_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int fl_sync(fl_ctx *ctx) {
+    if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int fl_weight_upload(fl_ctx *ctx, const fl_raw_weight *w, fl_weight **out) {
+    if (!ctx || !w || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    *out = nullptr;
+    if (w->num_rows <= 0 || w->blocks_per_row <= 0) return fail(ctx, FL_E_INVALID, "empty weight");
+    fl_weight *fw = new fl_weight();
+    const fl_raw_weight *arr[1] = {w};
+    int rc = upload_concat(ctx, arr, 1, *fw);
+    if (rc) {
+        weight_release(*fw);
+        delete fw;
+        return rc;
+    }
+    *out = fw;
+    return 0;
+}
+
+void fl_weight_free(fl_ctx *ctx, fl_weight *w) {
+    (void)ctx;
+    if (!w) return;
+    weight_release(*w);
+    delete w;
+}
+
+int fl_op_quantize_q8(fl_ctx *ctx, const float *x, int n, int8_t *q, float *scales, int32_t *sums) {
+    if (!ctx || !x || !q || !scales || !sums) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n <= 0 || n % 32) return fail(ctx, FL_E_INVALID, "n=%d must be a positive multiple of 32", n);
+    const int nb = n / 32;
+    hipLaunchKernelGGL(k_quantize, dim3((nb + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream, x,
+                       nb, q, scales, (int *)sums);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_rmsnorm_quantize_q8(fl_ctx *ctx, const float *x, const float *w, int n, float eps, int order,
+                              int8_t *q, float *scales, int32_t *sums) {
+    if (!ctx || !x || !w || !q || !scales || !sums) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n <= 0 || n % 32) return fail(ctx, FL_E_INVALID, "n=%d must be a positive multiple of 32", n);
+    if (order == 0)
+        hipLaunchKernelGGL(k_norm_quant<PRO_NORMQ0>, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, q,
+                           scales, (int *)sums);
+    else
+        hipLaunchKernelGGL(k_norm_quant<PRO_NORMQ1>, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, q,
+                           scales, (int *)sums);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_rmsnorm(fl_ctx *ctx, const float *x, const float *w, int n, float eps, float *out) {
+    if (!ctx || !x || !w || !out || n <= 0) return fail(ctx, FL_E_INVALID, "bad argument");
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
+                      const int32_t *sums, float *out) {
+    if (!ctx || !w || !q || !scales || !sums || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    return launch_q8in(ctx, *w, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, q, scales, (const int *)sums, out,
+                       nullptr);
+}
+
+int fl_op_matvec_f32in(fl_ctx *ctx, const fl_weight *w, const float *x, float *out) {
+    if (!ctx || !w || !x || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    return launch_f32in(ctx, *w, 0, EPI_STORE, x, nullptr, 0.f, out, nullptr);
+}
+
+int fl_op_block_dots(fl_ctx *ctx, const fl_weight *w, const int8_t *q, int32_t *dots) {
+    if (!ctx || !w || !q || !dots) return fail(ctx, FL_E_INVALID, "null argument");
+    long long n;
+    if (w->format == FL_Q8_0) {
+        n = (long long)w->rows * (w->cols / 32);
+        hipLaunchKernelGGL(k_block_dots<F_Q8_0>, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads),
+                           0, ctx->stream, w->desc(), q, (int *)dots);
+    } else if (w->format == FL_Q4K) {
+        n = (long long)w->rows * (w->cols / 256) * 4;
+        hipLaunchKernelGGL(k_block_dots<F_Q4K>, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads),
+                           0, ctx->stream, w->desc(), q, (int *)dots);
+    } else {
+        return fail(ctx, FL_E_UNSUPPORTED, "block dots need Q8_0 or Q4_K");
+    }
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_dequant(fl_ctx *ctx, const fl_weight *w, float *out) {
+    if (!ctx || !w || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    const long long n = (long long)w->rows * (w->cols / 32);
+    const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+    switch (w->format) {
+    case FL_Q8_0: hipLaunchKernelGGL(k_dequant<F_Q8_0>, grid, dim3(kThreads), 0, ctx->stream, w->desc(), out); break;
+    case FL_Q4K: hipLaunchKernelGGL(k_dequant<F_Q4K>, grid, dim3(kThreads), 0, ctx->stream, w->desc(), out); break;
+    case FL_Q6K: hipLaunchKernelGGL(k_dequant<F_Q6K>, grid, dim3(kThreads), 0, ctx->stream, w->desc(), out); break;
+    case FL_F32: hipLaunchKernelGGL(k_dequant<F_F32>, grid, dim3(kThreads), 0, ctx->stream, w->desc(), out); break;
+    default: return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
+    }
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_matvec_argmax(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
+                        const int32_t *sums, const float *x, int64_t *out_idx, float *out_val) {
+    if (!ctx || !w || !out_idx || !out_val) return fail(ctx, FL_E_INVALID, "null argument");
+    HIPCHK(ctx, hipMemsetAsync(ctx->d_slot, 0, 8, ctx->stream));
+    int rc;
+    if (q) {
+        if (!scales || !sums) return fail(ctx, FL_E_INVALID, "quantized input needs scales and sums");
+        rc = launch_q8in(ctx, *w, PRO_LOADQ, EPI_ARGMAX, nullptr, nullptr, 0.f, q, scales, (const int *)sums,
+                         nullptr, ctx->d_slot);
+    } else {
+        if (!x) return fail(ctx, FL_E_INVALID, "need q or x");
+        rc = launch_f32in(ctx, *w, 0, EPI_ARGMAX, x, nullptr, 0.f, nullptr, ctx->d_slot);
+    }
+    if (rc) return rc;
+    unsigned long long key = 0;
+    HIPCHK(ctx, hipMemcpyAsync(&key, ctx->d_slot, 8, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    const int64_t idx = (int64_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+    uint32_t u = (uint32_t)(key >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    float v;
+    std::memcpy(&v, &u, 4);
+    HIPCHK(ctx, hipMemcpyAsync(out_idx, &idx, 8, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(out_val, &v, 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// Host RoPE table row with the formula of RopeTable::new (model.rs:7197-7204).
+static void rope_row_host(int head_dim, int pos, float theta, float *c, float *s) {
+    const int half = head_dim / 2;
+    for (int d = 0; d < half; d++) {
+        const float freq = 1.0f / powf(theta, 2.0f * (float)d / (float)head_dim);
+        const float angle = (float)pos * freq;
+        s[d] = sinf(angle);
+        c[d] = cosf(angle);
+    }
+}
+
+int fl_op_rope(fl_ctx *ctx, float *data, int num_heads, int head_dim, int pos, float theta) {
+    if (!ctx || !data || num_heads <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 512 || pos < 0)
+        return fail(ctx, FL_E_INVALID, "bad rope argument");
+    std::vector<float> cs(512), sn(512);
+    rope_row_host(head_dim, pos, theta, cs.data(), sn.data());
+    HIPCHK(ctx, hipMemcpyAsync(ctx->d_rope_row, cs.data(), 512 * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->d_rope_row + 512, sn.data(), 512 * 4, hipMemcpyHostToDevice, ctx->stream));
+    const int n = num_heads * head_dim / 2;
+    hipLaunchKernelGGL(k_rope, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream, data, num_heads,
+                       head_dim, ctx->d_rope_row, ctx->d_rope_row + 512);
+    HIPCHK(ctx, hipGetLastError());
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // host staging buffers go out of scope
+    return 0;
+}
+
+int fl_op_silu_mul(fl_ctx *ctx, const float *gate, const float *up, int n, float *out) {
+    if (!ctx || !gate || !up || !out || n <= 0) return fail(ctx, FL_E_INVALID, "bad argument");
+    hipLaunchKernelGGL(k_silu_mul, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream, gate, up,
+                       n, out);
+    HIPCHK(ctx, hipGetLastError());
+    return 0;
+}
+
+int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void *v_cache, int kv_format,
+                    int num_heads, int num_kv_heads, int head_dim, int seq_len, int num_splits, float *out) {
+    if (!ctx || !q || !k_cache || !v_cache || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (num_kv_heads <= 0 || num_heads % num_kv_heads || seq_len <= 0)
+        return fail(ctx, FL_E_INVALID, "bad attention shape");
+    if (num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads");
+    if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format");
+    const int G = num_heads / num_kv_heads;
+    int ns, ch;
+    choose_splits(seq_len, num_kv_heads, ns, ch);
+    if (num_splits > 0) {
+        ns = std::min(num_splits, seq_len);
+        ch = (seq_len + ns - 1) / ns;
+    }
+    const size_t need = (size_t)num_kv_heads * ns * G * (head_dim + 2);
+    int rc = ensure_part(ctx, need);
+    if (rc) return rc;
+    const int pos = seq_len - 1;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->d_pos, &pos, 4, hipMemcpyHostToDevice, ctx->stream));
+    AttnArgs a{};
+    a.q = q;
+    a.kc = (void *)k_cache;
+    a.vc = (void *)v_cache;
+    a.posp = ctx->d_pos;
+    a.nkv = num_kv_heads;
+    a.nsplit = ns;
+    a.chmax = ch;
+    a.part = ctx->d_part;
+    a.counters = ctx->d_counters;
+    a.out = out;
+    rc = launch_attn(ctx, kv_format, head_dim, G, a);
+    if (rc) return rc;
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // pos staged from the host stack
+    return 0;
+}
+
+// ---- model -------------------------------------------------------------------
+
+int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
+    if (!ctx || !cfg) return fail(ctx, FL_E_INVALID, "null argument");
+    const fl_model_config &c = *cfg;
+    if (c.hidden_dim <= 0 || c.hidden_dim % 32 || c.num_layers <= 0 || c.num_heads <= 0 ||
+        c.num_kv_heads <= 0 || c.num_heads % c.num_kv_heads || (c.head_dim != 64 && c.head_dim != 128) ||
+        c.intermediate_dim % 32 || c.vocab_size <= 0 || c.max_seq_len <= 0)
+        return fail(ctx, FL_E_INVALID,
+                    "unsupported config (hidden %% 32, head_dim 64/128, inter %% 32 required)");
+    if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format %d", kv_format);
+    if (!attn_pick<float>(c.head_dim, c.num_heads / c.num_kv_heads))
+        return fail(ctx, FL_E_UNSUPPORTED, "heads per kv group %d", c.num_heads / c.num_kv_heads);
+    model_release(ctx);
+    ctx->cfg = c;
+    ctx->kv_format = kv_format;
+    const size_t H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
+    const size_t F = c.intermediate_dim, S = c.max_seq_len, L = c.num_layers;
+    const size_t esz = kv_format == FL_KV_F16 ? 2 : 4;
+    ctx->kv_layer_elems = S * kvd;
+    ALLOC(ctx, ctx->kcache, L * S * kvd * esz);
+    ALLOC(ctx, ctx->vcache, L * S * kvd * esz);
+    HIPCHK(ctx, hipMemset(ctx->kcache, 0, L * S * kvd * esz));
+    HIPCHK(ctx, hipMemset(ctx->vcache, 0, L * S * kvd * esz));
+    // RoPE table for every position (RopeTable::new formula, host libm)
+    const int half = c.head_dim / 2;
+    std::vector<float> tab(2 * S * half);
+#pragma omp parallel for schedule(static)
+    for (long long p = 0; p < (long long)S; p++)
+        rope_row_host(c.head_dim, (int)p, c.rope_theta, &tab[p * half], &tab[S * half + p * half]);
+    ALLOC(ctx, ctx->rope, tab.size() * 4);
+    HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+    choose_splits(c.max_seq_len, c.num_kv_heads, ctx->nsplit, ctx->chmax);
+    const int G = c.num_heads / c.num_kv_heads;
+    int rc = ensure_part(ctx, (size_t)c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    if (rc) return rc;
+    ALLOC(ctx, ctx->x, H * 4);
+    ALLOC(ctx, ctx->qkv, (qd + 2 * kvd) * 4);
+    ALLOC(ctx, ctx->attn, qd * 4);
+    ALLOC(ctx, ctx->aq, qd);
+    ALLOC(ctx, ctx->as, qd / 32 * 4);
+    ALLOC(ctx, ctx->asum, qd / 32 * 4);
+    ALLOC(ctx, ctx->hq, F);
+    ALLOC(ctx, ctx->hs, F / 32 * 4);
+    ALLOC(ctx, ctx->hsum, F / 32 * 4);
+    ALLOC(ctx, ctx->logits, (size_t)c.vocab_size * 4);
+    ALLOC(ctx, ctx->st, sizeof(DevState));
+    ALLOC(ctx, ctx->tokens, S * 4);
+    HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
+    HIPCHK(ctx, hipMemset(ctx->tokens, 0, S * 4));
+    HIPCHK(ctx, hipMemset(ctx->d_counters, 0, 1024 * 4));
+    ctx->have_cfg = true;
+    return 0;
+}
+
+int fl_has_weights(const fl_ctx *ctx) { return ctx && ctx->have_weights ? 1 : 0; }
+int fl_has_kv_cache(const fl_ctx *ctx) { return ctx && ctx->have_cfg ? 1 : 0; }
+
+int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *const *attn_norms,
+                      const float *const *ffn_norms, const float *output_norm, const fl_raw_weight *embedding,
+                      const fl_raw_weight *output) {
+    if (!ctx || !layers || !attn_norms || !ffn_norms || !output_norm || !embedding)
+        return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_cfg) return fail(ctx, FL_E_STATE, "fl_model_init must precede fl_upload_weights");
+    const fl_model_config &c = ctx->cfg;
+    const int H = c.hidden_dim, qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    const int F = c.intermediate_dim;
+    const int fmt = layers[0].format;
+    if (fmt != FL_Q8_0 && fmt != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "layer format %d (need Q8_0/Q4_K)", fmt);
+    if (fmt == FL_Q4K && (H % 256 || F % 256 || qd % 256))
+        return fail(ctx, FL_E_INVALID, "Q4_K needs dims multiple of 256");
+    const int exp_rows[7] = {qd, kvd, kvd, H, F, F, H};
+    const int exp_cols[7] = {H, H, H, qd, H, H, F};
+    for (int l = 0; l < c.num_layers; l++)
+        for (int j = 0; j < 7; j++) {
+            const fl_raw_weight &w = layers[l * 7 + j];
+            if (w.format != fmt) return fail(ctx, FL_E_INVALID, "layer %d weight %d: mixed formats", l, j);
+            if (w.num_rows != exp_rows[j] || weight_cols(&w) != exp_cols[j])
+                return fail(ctx, FL_E_INVALID, "layer %d weight %d: shape %dx%d, expected %dx%d", l, j, w.num_rows,
+                            weight_cols(&w), exp_rows[j], exp_cols[j]);
+        }
+    if (weight_cols(embedding) != H || embedding->num_rows != c.vocab_size)
+        return fail(ctx, FL_E_INVALID, "embedding shape");
+    if (output && (weight_cols(output) != H || output->num_rows != c.vocab_size))
+        return fail(ctx, FL_E_INVALID, "output shape");
+    ctx->have_weights = false;
+    if (ctx->gexec) { (void)hipGraphExecDestroy(ctx->gexec); ctx->gexec = nullptr; }
+    if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
+    for (auto &l : ctx->layers) {
+        weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
+        if (l.attn_norm) (void)hipFree(l.attn_norm);
+        if (l.ffn_norm) (void)hipFree(l.ffn_norm);
+    }
+    ctx->layers.assign(c.num_layers, Layer());
+    ctx->layer_fmt = fmt;
+    for (int l = 0; l < c.num_layers; l++) {
+        const fl_raw_weight *w = &layers[l * 7];
+        const fl_raw_weight *qkv[3] = {&w[0], &w[1], &w[2]};
+        const fl_raw_weight *wo[1] = {&w[3]};
+        const fl_raw_weight *gu[2] = {&w[4], &w[5]};
+        const fl_raw_weight *dn[1] = {&w[6]};
+        Layer &L = ctx->layers[l];
+        int rc = upload_concat(ctx, qkv, 3, L.qkv);
+        if (!rc) rc = upload_concat(ctx, wo, 1, L.wo);
+        if (!rc) rc = upload_concat(ctx, gu, 2, L.gu);
+        if (!rc) rc = upload_concat(ctx, dn, 1, L.down);
+        if (rc) return rc;
+        ALLOC(ctx, L.attn_norm, (size_t)H * 4);
+        ALLOC(ctx, L.ffn_norm, (size_t)H * 4);
+        HIPCHK(ctx, hipMemcpy(L.attn_norm, attn_norms[l], (size_t)H * 4, hipMemcpyHostToDevice));
+        HIPCHK(ctx, hipMemcpy(L.ffn_norm, ffn_norms[l], (size_t)H * 4, hipMemcpyHostToDevice));
+    }
+    weight_release(ctx->embed);
+    weight_release(ctx->output);
+    const fl_raw_weight *e1[1] = {embedding};
+    int rc = upload_concat(ctx, e1, 1, ctx->embed);
+    if (rc) return rc;
+    ctx->tied = output == nullptr;
+    if (!ctx->tied) {
+        const fl_raw_weight *o1[1] = {output};
+        rc = upload_concat(ctx, o1, 1, ctx->output);
+        if (rc) return rc;
+    }
+    if (!ctx->out_norm) ALLOC(ctx, ctx->out_norm, (size_t)H * 4);
+    HIPCHK(ctx, hipMemcpy(ctx->out_norm, output_norm, (size_t)H * 4, hipMemcpyHostToDevice));
+    ctx->have_weights = true;
+    return 0;
+}
+
+int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const float *value) {
+    if (!ctx || !key || !value) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_cfg) return fail(ctx, FL_E_STATE, "no kv cache");
+    const fl_model_config &c = ctx->cfg;
+    if (layer < 0 || layer >= c.num_layers) return fail(ctx, FL_E_INVALID, "layer %d", layer);
+    const int slot = position % c.max_seq_len;  // ring write (GpuKvCache::write)
+    const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
+    const size_t off = (size_t)layer * ctx->kv_layer_elems + (size_t)slot * kvd;
+    if (ctx->kv_format == FL_KV_F32) {
+        HIPCHK(ctx, hipMemcpy((float *)ctx->kcache + off, key, kvd * 4, hipMemcpyHostToDevice));
+        HIPCHK(ctx, hipMemcpy((float *)ctx->vcache + off, value, kvd * 4, hipMemcpyHostToDevice));
+    } else {
+        std::vector<__half> hk(kvd), hv(kvd);
+        for (size_t i = 0; i < kvd; i++) {
+            hk[i] = __float2half(key[i]);
+            hv[i] = __float2half(value[i]);
+        }
+        HIPCHK(ctx, hipMemcpy((__half *)ctx->kcache + off, hk.data(), kvd * 2, hipMemcpyHostToDevice));
+        HIPCHK(ctx, hipMemcpy((__half *)ctx->vcache + off, hv.data(), kvd * 2, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+int fl_reset(fl_ctx *ctx) {
+    if (!ctx || !ctx->have_cfg) return fail(ctx, FL_E_STATE, "no model");
+    const fl_model_config &c = ctx->cfg;
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+    const size_t bytes = (size_t)c.num_layers * ctx->kv_layer_elems * esz;
+    HIPCHK(ctx, hipMemsetAsync(ctx->kcache, 0, bytes, ctx->stream));
+    HIPCHK(ctx, hipMemsetAsync(ctx->vcache, 0, bytes, ctx->stream));
+    HIPCHK(ctx, hipMemsetAsync(ctx->st, 0, sizeof(DevState), ctx->stream));
+    HIPCHK(ctx, hipMemsetAsync(ctx->d_counters, 0, 1024 * 4, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// Enqueue one decode step (kernels only; no host synchronisation).
+static int enqueue_step(fl_ctx *ctx, bool want_logits) {
+    const fl_model_config &c = ctx->cfg;
+    const int H = c.hidden_dim, hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads;
+    const int qd = nh * hd, kvd = nkv * hd, G = nh / nkv;
+    const float eps = c.rms_norm_eps;
+    const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
+    switch (ctx->embed.format) {
+    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
+    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
+    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
+    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
+    }
+    HIPCHK(ctx, hipGetLastError());
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+    for (int l = 0; l < c.num_layers; l++) {
+        Layer &L = ctx->layers[l];
+        int rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
+                             ctx->qkv, nullptr);
+        if (rc) return rc;
+        AttnArgs a{};
+        a.q = ctx->qkv;
+        a.knew = ctx->qkv + qd;
+        a.vnew = ctx->qkv + qd + kvd;
+        a.rope = ctx->rope;
+        a.sin_off = (long long)c.max_seq_len * (hd / 2);
+        a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
+        a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
+        a.posp = &ctx->st->pos;
+        a.nkv = nkv;
+        a.nsplit = ctx->nsplit;
+        a.chmax = ctx->chmax;
+        a.part = ctx->d_part;
+        a.counters = ctx->d_counters;
+        a.out = ctx->attn;
+        a.oq = ctx->aq;
+        a.os = ctx->as;
+        a.osum = ctx->asum;
+        rc = launch_attn(ctx, ctx->kv_format, hd, G, a);
+        if (rc) return rc;
+        rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
+                         nullptr);
+        if (rc) return rc;
+        rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs,
+                           ctx->hsum, nullptr);
+        if (rc) return rc;
+        rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->x,
+                         nullptr);
+        if (rc) return rc;
+    }
+    // output projection (forward_greedy, model.rs:1898-1932)
+    const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
+    const bool q8out = !ctx->tied && ((O.format == FL_Q8_0 && ctx->layer_fmt == FL_Q8_0) ||
+                                      (O.format == FL_Q4K && ctx->layer_fmt == FL_Q4K));
+    int rc;
+    if (q8out) {
+        rc = launch_q8in(ctx, O, PRO_NORMQ1, want_logits ? EPI_STORE : EPI_ARGMAX, ctx->x, ctx->out_norm, eps,
+                         nullptr, nullptr, nullptr, ctx->logits, &ctx->st->argmax);
+    } else {
+        if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
+        rc = launch_f32in(ctx, O, 1, want_logits ? EPI_STORE : EPI_ARGMAX, ctx->x, ctx->out_norm, eps, ctx->logits,
+                          &ctx->st->argmax);
+    }
+    return rc;
+}
+
+static int ensure_graph(fl_ctx *ctx) {
+    if (ctx->gexec) return 0;
+    HIPCHK(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(ctx, false);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(ctx, FL_E_HIP, "graph capture failed: %s", hipGetErrorString(e));
+    ctx->graph = g;
+    HIPCHK(ctx, hipGraphInstantiate(&ctx->gexec, g, nullptr, nullptr, 0));
+    return 0;
+}
+
+int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int32_t *out_token, float *out_val) {
+    if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    if (pos < 0 || pos >= c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "pos %d outside the KV cache (max_seq_len %d)", pos, c.max_seq_len);
+    if ((int)token >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", token);
+    const int tok = (int)token;
+    DevState hs{};
+    hs.step = pos;
+    hs.pos = pos;
+    hs.n_prompt = pos + 1;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + pos, &tok, 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
+    if (out_logits) {
+        int rc = enqueue_step(ctx, true);
+        if (rc) return rc;
+    } else {
+        int rc = ensure_graph(ctx);
+        if (rc) return rc;
+        HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    }
+    DevState out{};
+    HIPCHK(ctx, hipMemcpyAsync(&out, ctx->st, sizeof out, hipMemcpyDeviceToHost, ctx->stream));
+    if (out_logits)
+        HIPCHK(ctx, hipMemcpyAsync(out_logits, ctx->logits, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    if (out_logits) {
+        int bi = 0;
+        float bv = -INFINITY;
+        for (int i = 0; i < c.vocab_size; i++)
+            if (out_logits[i] > bv) { bv = out_logits[i]; bi = i; }
+        if (out_token) *out_token = bi;
+        if (out_val) *out_val = bv;
+    } else {
+        const unsigned long long k = out.argmax;
+        if (out_token) *out_token = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+        uint32_t u = (uint32_t)(k >> 32);
+        u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+        float v;
+        std::memcpy(&v, &u, 4);
+        if (out_val) *out_val = v;
+    }
+    return 0;
+}
+
+int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen, uint32_t *out_tokens) {
+    if (!ctx || !prompt || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    if (n_prompt <= 0 || n_gen <= 0) return fail(ctx, FL_E_INVALID, "n_prompt and n_gen must be positive");
+    const int steps = n_prompt + n_gen - 1;
+    if (steps > c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "prompt+generation (%d) exceeds max_seq_len %d", steps, c.max_seq_len);
+    for (int i = 0; i < n_prompt; i++)
+        if ((int)prompt[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "prompt token %u >= vocab", prompt[i]);
+    int rc = ensure_graph(ctx);
+    if (rc) return rc;
+    std::vector<int> toks(prompt, prompt + n_prompt);
+    DevState hs{};
+    hs.n_prompt = n_prompt;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->tokens, toks.data(), (size_t)n_prompt * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
+    for (int s = 0; s < steps; s++) HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    std::vector<int> gen((size_t)std::max(n_gen - 1, 1));
+    DevState out{};
+    if (n_gen > 1)
+        HIPCHK(ctx, hipMemcpyAsync(gen.data(), ctx->tokens + n_prompt, (size_t)(n_gen - 1) * 4, hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(&out, ctx->st, sizeof out, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    for (int i = 0; i < n_gen - 1; i++) out_tokens[i] = (uint32_t)gen[i];
+    out_tokens[n_gen - 1] = 0xFFFFFFFFu - (uint32_t)(out.argmax & 0xFFFFFFFFull);
+    return 0;
+}
+
+int fl_decode_continue(fl_ctx *ctx, int n_steps) {
+    if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
+    if (!ctx->gexec) return fail(ctx, FL_E_STATE, "fl_generate must run first");
+    if (n_steps < 0) return fail(ctx, FL_E_INVALID, "n_steps < 0");
+    DevState st{};
+    HIPCHK(ctx, hipMemcpyAsync(&st, ctx->st, sizeof st, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    if (st.step + n_steps > ctx->cfg.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "continuing %d steps from %d exceeds max_seq_len %d", n_steps, st.step,
+                    ctx->cfg.max_seq_len);
+    for (int s = 0; s < n_steps; s++) HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    return 0;
+}
+
+int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out) {
+    if (!ctx || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_cfg || start < 0 || n < 0 || start + n > ctx->cfg.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "token range");
+    HIPCHK(ctx, hipMemcpyAsync(out, ctx->tokens + start, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// Launch `iters` copies of one layer-0 kernel on the context stream.
+int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_launch) {
+    if (!ctx || !ctx->have_weights) return fail(ctx, FL_E_STATE, "no model");
+    const fl_model_config &c = ctx->cfg;
+    Layer &L = ctx->layers[0];
+    const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
+    const fl_weight *w = nullptr;
+    for (int i = 0; i < iters; i++) {
+        int rc = 0;
+        switch (which) {
+        case 0: w = &L.qkv; rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->qkv, nullptr); break;
+        case 1: w = &L.wo; rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->logits, nullptr); break;
+        case 2: w = &L.gu; rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs, ctx->hsum, nullptr); break;
+        case 3: w = &L.down; rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->logits, nullptr); break;
+        case 4: {
+            const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
+            w = &O;
+            const bool q8out = !ctx->tied && (O.format == FL_Q8_0 || O.format == FL_Q4K);
+            if (q8out) rc = launch_q8in(ctx, O, PRO_NORMQ1, EPI_ARGMAX, ctx->x, ctx->out_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, nullptr, ctx->d_slot);
+            else rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, ctx->x, ctx->out_norm, c.rms_norm_eps, nullptr, ctx->d_slot);
+            break;
+        }
+        default: return fail(ctx, FL_E_INVALID, "which=%d", which);
+        }
+        if (rc) return rc;
+    }
+    if (bytes_per_launch && w) *bytes_per_launch = (double)w->gguf_bytes;
+    return 0;
+}
+
+const char *fl_bench_kernel_name(fl_ctx *ctx, int which) {
+    if (!ctx || !ctx->have_weights) return "";
+    switch (which) {
+    case 0: return "k_mv_q8in";
+    case 1: return "k_mv_q8in";
+    case 2: return "k_gateup";
+    case 3: return "k_mv_q8in";
+    case 4: return ctx->tied || ctx->output.format == FL_Q6K ? "k_mv_f32in" : "k_mv_q8in";
+    }
+    return "";
+}
+
+}  // extern "C"

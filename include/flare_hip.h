@@ -1,0 +1,208 @@
+/*
+ * flare_hip.h -- C-ABI of the MI355X decode backend for flarellm.
+ *
+ * This is the drop-in boundary that replaces flarellm's
+ * `flare_core::model::ComputeBackend` decode hooks
+ * (flare-core/src/model.rs:176-618) and the free quantized kernels that
+ * `Model::forward_layers` calls directly on the CPU path
+ * (flare-core/src/model.rs:1955-2561).  Citations are path:line in the
+ * flarellm source tree.
+ *
+ * Conventions
+ *  - Every entry point returns 0 on success or a negative FL_E* code; the
+ *    message is available from fl_last_error(ctx) (ctx may be NULL for
+ *    errors raised before a context exists).  This replaces the reference's
+ *    panics (model.rs:321, 474-477; flare-gpu/src/backend.rs:4907-4910).
+ *  - One context = one GPU + one HIP stream.  A context is not thread-safe,
+ *    like the reference's single `&mut Model`.
+ *  - Weight bytes cross the boundary in GGUF block layout exactly as
+ *    `RawWeight { data, format, num_rows, blocks_per_row }`
+ *    (model.rs:123-130, flare-loader/src/gguf.rs:616-653).  They are host
+ *    pointers and are copied (and, for Q8_0/Q6_K, re-laid-out) on upload.
+ *  - "Op" entry points (fl_op_*) take DEVICE pointers and enqueue on the
+ *    context stream; call fl_sync() before reading results on the host.
+ *  - Activations quantized to Q8_0 are three device arrays: int8 quants[n],
+ *    float scales[n/32] and int32 block sums[n/32] (sum of the 32 quants,
+ *    used by the Q4_K min term).  quants+scales are the reference's
+ *    `QuantizedInput` (model.rs:5468-5472).
+ */
+#ifndef FLARE_HIP_H
+#define FLARE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FL_ABI_VERSION 1
+
+/* status codes */
+#define FL_OK 0
+#define FL_E_INVALID (-1)     /* bad argument / unsupported shape */
+#define FL_E_UNSUPPORTED (-2) /* format or path not implemented */
+#define FL_E_HIP (-3)         /* HIP runtime error */
+#define FL_E_STATE (-4)       /* call order violated (e.g. no weights) */
+#define FL_E_OOM (-5)         /* device allocation failed */
+
+/* WeightFormat subset on the decode hot path (model.rs WeightFormat). */
+#define FL_F32 0
+#define FL_Q8_0 1
+#define FL_Q4K 2
+#define FL_Q6K 3
+
+/* KV cache storage. F32 = flare-core KvCache (kv_cache.rs:431-546);
+ * F16 = flare-gpu GpuKvCache f16 (flare-gpu/src/kv_cache.rs:51-66). */
+#define FL_KV_F32 0
+#define FL_KV_F16 1
+
+typedef struct fl_ctx fl_ctx;
+typedef struct fl_weight fl_weight;
+
+/* RawWeight (model.rs:123-130). */
+typedef struct {
+    const void *data; /* host pointer to GGUF tensor bytes */
+    size_t nbytes;
+    int format;       /* FL_Q8_0 / FL_Q4K / FL_Q6K / FL_F32 */
+    int num_rows;     /* out features (last GGUF dim) */
+    int blocks_per_row;
+} fl_raw_weight;
+
+/* ModelConfig fields used by forward_single_token_gpu (model.rs:555) and
+ * flare-core/src/config.rs:17-54. */
+typedef struct {
+    int hidden_dim, num_layers, num_heads, num_kv_heads, head_dim, intermediate_dim,
+        vocab_size, max_seq_len;
+    float rms_norm_eps, rope_theta;
+} fl_model_config;
+
+/* ---- context ------------------------------------------------------------ */
+int fl_abi_version(void);
+/* Create a context on HIP device `device`.  No reference counterpart: the
+ * reference constructs its backend with WebGpuBackend::new. */
+int fl_ctx_create(int device, fl_ctx **out);
+void fl_ctx_destroy(fl_ctx *ctx);
+const char *fl_last_error(const fl_ctx *ctx);
+/* The hipStream_t all work of this context is enqueued on. */
+void *fl_ctx_stream(fl_ctx *ctx);
+int fl_sync(fl_ctx *ctx);
+/* ComputeBackend::name (model.rs:615). */
+const char *fl_backend_name(void);
+
+/* ---- weights -------------------------------------------------------------- */
+/* Upload one RawWeight for use with the fl_op_matvec* entry points (the
+ * weight argument of ComputeBackend::batched_dequant_matmul, model.rs:468). */
+int fl_weight_upload(fl_ctx *ctx, const fl_raw_weight *w, fl_weight **out);
+void fl_weight_free(fl_ctx *ctx, fl_weight *w);
+
+/* ---- per-op entry points (device pointers) --------------------------------- */
+/* quantize_input_q8_0_into (model.rs:5534-5571). n % 32 == 0. */
+int fl_op_quantize_q8(fl_ctx *ctx, const float *x, int n, int8_t *q, float *scales,
+                      int32_t *sums);
+/* rmsnorm_quantize_q8_0_into (model.rs:5581-5640) when order == 0:
+ * normed = (x*w)*inv_rms; order == 1 is rmsnorm_into followed by
+ * quantize_input_q8_0_into (model.rs:2040-2095, the Q4_K path):
+ * normed = (x*inv_rms)*w. */
+int fl_op_rmsnorm_quantize_q8(fl_ctx *ctx, const float *x, const float *w, int n, float eps,
+                              int order, int8_t *q, float *scales, int32_t *sums);
+/* rmsnorm_into (model.rs:7456-7477). */
+int fl_op_rmsnorm(fl_ctx *ctx, const float *x, const float *w, int n, float eps, float *out);
+/* matvec_q8_0_preq_into (model.rs:7976-8103) / matvec_q4k_q8_into
+ * (model.rs:9672-9779) over a Q8_0-quantized input. */
+int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
+                      const int32_t *sums, float *out);
+/* Dequantized-weight x f32-input matvec (the f32 logits path,
+ * matvec_into model.rs:7549 on dequantize_tensor output, gguf.rs:717). */
+int fl_op_matvec_f32in(fl_ctx *ctx, const fl_weight *w, const float *x, float *out);
+/* Per-block integer dot products of the device dot routine (the bit-exact
+ * parity surface of model.rs:8082-8099 and 8997-9014).  Q8_0: rows*bpr
+ * int32; Q4_K: rows*bpr*8 int32 ordered (sub0 lo, sub0 hi, sub1 lo, ...). */
+int fl_op_block_dots(fl_ctx *ctx, const fl_weight *w, const int8_t *q, int32_t *dots);
+/* Dequantize a whole weight to f32 (dequantize_tensor, gguf.rs:717-880). */
+int fl_op_dequant(fl_ctx *ctx, const fl_weight *w, float *out);
+/* Fused argmax over the output projection: matvec_argmax_q8_0_preq
+ * (model.rs:8450), matvec_argmax_q4k_q8_preq (8569) with a Q8 input;
+ * matvec_argmax_f32 (8668) with an f32 input (x != NULL, q == NULL).
+ * Result: out_idx_val[0] = index (as int64), first maximum on ties;
+ * *out_val = winning value. Both device pointers. */
+int fl_op_matvec_argmax(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
+                        const int32_t *sums, const float *x, int64_t *out_idx, float *out_val);
+/* apply_rope_with_table (model.rs:7256-7297) in place on num_heads*head_dim
+ * floats, using the host-built libm table of RopeTable::new (7190-7212). */
+int fl_op_rope(fl_ctx *ctx, float *data, int num_heads, int head_dim, int pos, float theta);
+/* silu_mul_into (model.rs:9783-9796). */
+int fl_op_silu_mul(fl_ctx *ctx, const float *gate, const float *up, int n, float *out);
+/* cpu_grouped_query_attention_into (model.rs:9849-9966) over a ring cache
+ * laid out [slot][num_kv_heads][head_dim] (kv_cache.rs:431-472), attending to
+ * slots 0..seq_len-1; kv_format FL_KV_F32 or FL_KV_F16. num_splits <= 0 picks
+ * the split count automatically. */
+int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void *v_cache,
+                    int kv_format, int num_heads, int num_kv_heads, int head_dim, int seq_len,
+                    int num_splits, float *out);
+
+/* ---- model: ComputeBackend decode hooks ----------------------------------- */
+/* init_gpu_kv_cache (model.rs:274) + the config forward_single_token_gpu
+ * receives per call (model.rs:555).  Must precede fl_upload_weights. */
+int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format);
+/* upload_weights_to_gpu (model.rs:526) taking raw layers as
+ * Model::set_raw_weights does (model.rs:1411-1452).  layers: 7*num_layers
+ * weights ordered wq, wk, wv, wo, w_gate, w_up, w_down per layer; all seven
+ * share one format (FL_Q8_0 or FL_Q4K).  attn_norms / ffn_norms: num_layers
+ * host pointers to hidden_dim floats.  output: NULL when tied to the
+ * embedding (flare-loader/src/weights.rs:50-51). */
+int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *const *attn_norms,
+                      const float *const *ffn_norms, const float *output_norm,
+                      const fl_raw_weight *embedding, const fl_raw_weight *output);
+/* has_gpu_weights (model.rs:537) / has_gpu_kv_cache (model.rs:299). */
+int fl_has_weights(const fl_ctx *ctx);
+int fl_has_kv_cache(const fl_ctx *ctx);
+/* gpu_kv_write (model.rs:287): store one token's K and V (host floats,
+ * num_kv_heads*head_dim each) at ring slot `position` of `layer`. */
+int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const float *value);
+/* Model::reset / KvCache::clear (model.rs:1591, kv_cache.rs:534-545). */
+int fl_reset(fl_ctx *ctx);
+/* forward_greedy (model.rs:1872-1942) when out_logits == NULL, else
+ * forward_single_token_gpu (model.rs:555) + argmax: writes vocab_size host
+ * floats of logits.  The token is processed at position `pos` (the KV ring
+ * slot), attending to pos+1 slots. */
+int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int32_t *out_token,
+                   float *out_val);
+/* Greedy generation (Generator::step loop, flare-core/src/generate.rs:186-206):
+ * feeds the n_prompt tokens one per step from position 0, then writes n_gen
+ * generated tokens to out_tokens.  Runs device-resident: one HIP graph replay
+ * per token, one host synchronisation at the end. */
+int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen,
+                uint32_t *out_tokens);
+
+/* Enqueue n_steps more device-resident greedy steps after fl_generate (no
+ * host synchronisation; tokens land in the device token buffer). */
+int fl_decode_continue(fl_ctx *ctx, int n_steps);
+/* Copy tokens[start, start+n) of the device token buffer (prompt tokens
+ * followed by generated tokens) to the host. */
+int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out);
+
+/* ---- measurement helpers ---------------------------------------------------- */
+/* Enqueue `iters` launches of the layer matvec kernel for `which`
+ * (0=qkv, 1=wo, 2=gate_up, 3=down, 4=output argmax) of layer 0 on the context
+ * stream, reading the model's live activation buffers.  Writes the
+ * algorithmic weight bytes of one launch to *bytes_per_launch. */
+int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_launch);
+/* Name of the device kernel fl_bench_layer_kernel launches for `which`. */
+const char *fl_bench_kernel_name(fl_ctx *ctx, int which);
+
+/* ---- synthetic model generation (host only; no reference counterpart: the
+ * reference loads real GGUF files) --------------------------------------- */
+/* Fill out[n] with N(mean, std) floats from a counter-based generator keyed
+ * by (seed, index), so any slice is reproducible independently. */
+void fl_synth_normal(uint64_t seed, uint64_t offset, size_t n, float mean, float std, float *out);
+/* Quantize rows x cols f32 into GGUF block bytes of `format`. Returns the
+ * byte count written (0 on bad shape).  Q4_K uses flarellm's layout
+ * (model.rs:8700-8719, quantize.rs:386-423). */
+size_t fl_synth_quantize(const float *src, size_t rows, size_t cols, int format, uint8_t *out);
+size_t fl_format_row_bytes(int format, size_t cols);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
