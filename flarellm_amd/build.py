@@ -33,14 +33,28 @@ def _run(cmd: list[str]) -> None:
     subprocess.run(cmd, check=True)
 
 
+HIP_SOURCES = ["flare_hip.hip", "mv_q8_0.hip", "mv_q4k.hip", "mv_f32in.hip", "attn.hip"]
+
+
 def build(verbose: bool = True) -> str:
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(BUILD, exist_ok=True)
-    hip_obj = os.path.join(BUILD, "flare_hip.o")
+    jobs = []
+    objs = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     syn_obj = os.path.join(BUILD, "synth.o")
-    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "flare_hip.hip"), "-o", hip_obj])
-    _run(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "synth.cpp"), "-o", syn_obj])
+    jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "synth.cpp"), "-o", syn_obj])
+    objs.append(syn_obj)
+    workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(workers) as ex:
+        for f in [ex.submit(_run, j) for j in jobs]:
+            f.result()
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", hip_obj, syn_obj, "-lgomp", "-o", tmp])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lgomp", "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
 

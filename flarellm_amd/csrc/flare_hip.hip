@@ -25,6 +25,7 @@
 
 #include "../../include/flare_hip.h"
 #include "kernels.h"
+#include "launch.h"
 
 using namespace fl;
 
@@ -57,169 +58,6 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const floa
     __shared__ float red[8];
     const float inv = wg_inv_rms(x, n, eps, red);
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] * inv) * w[i];
-}
-
-enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_ARGMAX = 2 };
-
-template <int R>
-__device__ __forceinline__ void group_argmax_commit(const float *acc, int row0, int rows, int gl,
-                                                    unsigned long long *slot,
-                                                    unsigned long long *lred) {
-    // strict '>' over rows in ascending order keeps the first maximum
-    unsigned long long best = 0;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (row0 + r < rows) {
-            unsigned long long k = argmax_key(acc[r], (uint32_t)(row0 + r));
-            best = k > best ? k : best;
-        }
-    }
-    (void)gl;
-    // wave max (all groups of the wave share it; max is order-independent)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned long long t = __shfl_xor(best, o, 64);
-        best = t > best ? t : best;
-    }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) lred[w] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long b = lred[0];
-        for (int i = 1; i < (int)(blockDim.x >> 6); i++) b = lred[i] > b ? lred[i] : b;
-        atomicMax(slot, b);
-    }
-}
-
-// Generic Q8-input matvec.  Groups of LPR lanes own R consecutive rows.
-template <int FMT, int LPR, int R, int PRO, int EPI>
-__global__ __launch_bounds__(kThreads) void k_mv_q8in(WDesc W, const float *x, const float *nw,
-                                                      float eps, const int8_t *gq, const float *gs,
-                                                      const int *gsum, float *out,
-                                                      unsigned long long *slot) {
-    extern __shared__ __align__(16) char smem[];
-    const int K = W.cols;
-    int8_t *lq = (int8_t *)smem;
-    float *ls = (float *)(smem + K);
-    int *lsum = (int *)(ls + (K >> 5));
-    float *red = (float *)(lsum + (K >> 5));
-    stage_q8<PRO>(x, nw, eps, K, gq, gs, gsum, lq, ls, lsum, red);
-    constexpr int G = kThreads / LPR;
-    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
-    const int row0 = (blockIdx.x * G + grp) * R;
-    int rix[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) rix[r] = min(row0 + r, W.rows - 1);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
-    if (row0 < W.rows) rows_q8in<FMT, LPR, R>(W, rix, lq, ls, lsum, gl, acc);
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
-    if (EPI == EPI_ARGMAX) {
-        group_argmax_commit<R>(acc, row0, W.rows, gl, slot, (unsigned long long *)red);
-        return;
-    }
-    if (gl < R && row0 + gl < W.rows) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < R; r++) v = (gl == r) ? acc[r] : v;
-        if (EPI == EPI_STORE) out[row0 + gl] = v;
-        else out[row0 + gl] += v;
-    }
-}
-
-// Fused gate/up matvec over W = [w_gate; w_up] (F rows each) with the
-// SiLU(gate)*up (model.rs:9788-9795) and quantize_input_q8_0 (5557-5570)
-// epilogue.  Workgroup b produces hidden block b (32 values).
-template <int FMT, int LPR, int PRO>
-__global__ __launch_bounds__(kThreads) void k_gateup(WDesc W, int F, const float *x,
-                                                     const float *nw, float eps, const int8_t *gq,
-                                                     const float *gs, const int *gsum, int8_t *hq,
-                                                     float *hs, int *hsum, float *hout) {
-    extern __shared__ __align__(16) char smem[];
-    const int K = W.cols;
-    int8_t *lq = (int8_t *)smem;
-    float *ls = (float *)(smem + K);
-    int *lsum = (int *)(ls + (K >> 5));
-    float *red = (float *)(lsum + (K >> 5));
-    float *gu = red + 8;  // [64]: gate[32], up[32]
-    stage_q8<PRO>(x, nw, eps, K, gq, gs, gsum, lq, ls, lsum, red);
-    constexpr int G = kThreads / LPR;
-    constexpr int R = 64 / G;
-    constexpr int RH = R / 2;
-    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
-    const int i0 = blockIdx.x * 32 + grp * RH;
-    int rix[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) rix[r] = (r < RH) ? (i0 + r) : (F + i0 + r - RH);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
-    rows_q8in<FMT, LPR, R>(W, rix, lq, ls, lsum, gl, acc);
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
-    if (gl == 0) {
-#pragma unroll
-        for (int r = 0; r < RH; r++) {
-            gu[grp * RH + r] = acc[r];
-            gu[32 + grp * RH + r] = acc[RH + r];
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float h[32];
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-            const float g = gu[j];
-            h[j] = (g / (1.0f + expf(-g))) * gu[32 + j];
-        }
-        if (hout) {
-            for (int j = 0; j < 32; j++) hout[blockIdx.x * 32 + j] = h[j];
-        }
-        quant_block32(h, hq + blockIdx.x * 32, hs + blockIdx.x, hsum + blockIdx.x);
-    }
-}
-
-// f32-input matvec (logits path).  PRO 0: x loaded as is; PRO 1: final
-// rmsnorm_into (model.rs:2553-2558) computed per workgroup.
-template <int FMT, int LPR, int R, int PRO, int EPI>
-__global__ __launch_bounds__(kThreads) void k_mv_f32in(WDesc W, const float *x, const float *nw,
-                                                       float eps, float *out,
-                                                       unsigned long long *slot) {
-    extern __shared__ __align__(16) char smem[];
-    const int K = W.cols;
-    float *lx = (float *)smem;
-    float *red = lx + K;
-    if (PRO == 1) {
-        const float inv = wg_inv_rms(x, K, eps, red);
-        for (int i = threadIdx.x; i < K; i += blockDim.x) lx[i] = (x[i] * inv) * nw[i];
-    } else {
-        for (int i = threadIdx.x; i < K; i += blockDim.x) lx[i] = x[i];
-    }
-    __syncthreads();
-    constexpr int G = kThreads / LPR;
-    const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
-    const int row0 = (blockIdx.x * G + grp) * R;
-    int rix[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) rix[r] = min(row0 + r, W.rows - 1);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
-    if (row0 < W.rows) rows_f32in<FMT, LPR, R>(W, rix, lx, gl, acc);
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
-    if (EPI == EPI_ARGMAX) {
-        group_argmax_commit<R>(acc, row0, W.rows, gl, slot, (unsigned long long *)red);
-        return;
-    }
-    if (gl < R && row0 + gl < W.rows) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < R; r++) v = (gl == r) ? acc[r] : v;
-        out[row0 + gl] = v;
-    }
 }
 
 // Per-block integer dots (parity surface).  One thread per unit.
@@ -328,240 +166,6 @@ __global__ __launch_bounds__(kThreads) void k_silu_mul(const float *g, const flo
     if (i >= n) return;
     const float gv = g[i];
     out[i] = (gv / (1.0f + expf(-gv))) * u[i];
-}
-
-// ---------------------------------------------------------------------------
-// Split-K GQA decode attention (cpu_grouped_query_attention_into semantics,
-// model.rs:9849-9966).  Grid (nsplit, num_kv_heads); workgroup (s, kvh)
-// handles the G query heads sharing kv head kvh over token chunk s, then the
-// last workgroup of each kv head merges the chunk partials (flash-decode
-// rescale) and writes the f32 output plus its Q8_0 quantization.
-// When `knew` is set, q/k arrive un-rotated (QKV matvec output): RoPE is
-// applied here and the chunk holding slot `pos` stores the new K/V.
-// ---------------------------------------------------------------------------
-struct AttnArgs {
-    const float *q;      // [nh*D]
-    const float *knew;   // [nkv*D] un-rotated new key (or null)
-    const float *vnew;   // [nkv*D]
-    const float *rope;   // rope table base: cos [maxpos][D/2] then sin at +sin_off
-    long long sin_off;
-    void *kc, *vc;       // cache for this layer: [slots][nkv][D]
-    const int *posp;     // attends slots 0..*posp
-    int nkv, nsplit, chmax;
-    float *part;         // [nkv][nsplit][G][D+2]
-    int *counters;       // [nkv]
-    float *out;          // [nh*D]
-    int8_t *oq;          // optional Q8 output
-    float *os;
-    int *osum;
-};
-
-template <typename KT>
-__device__ __forceinline__ void load8(const KT *p, float *v);
-template <>
-__device__ __forceinline__ void load8<__half>(const __half *p, float *v) {
-    const int4 t = *(const int4 *)p;
-    const uint32_t w[4] = {(uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[2 * i] = h2f((uint16_t)(w[i] & 0xFFFF));
-        v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
-    }
-}
-template <>
-__device__ __forceinline__ void load8<float>(const float *p, float *v) {
-    const float4 a = ((const float4 *)p)[0], b = ((const float4 *)p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-__device__ __forceinline__ float kv_round(float v, const __half *) { return h2f(f2h(v)); }
-__device__ __forceinline__ float kv_round(float v, const float *) { return v; }
-__device__ __forceinline__ void kv_store(__half *p, float v) { *p = __ushort_as_half(f2h(v)); }
-__device__ __forceinline__ void kv_store(float *p, float v) { *p = v; }
-
-template <typename KT, int D, int G>
-__global__ __launch_bounds__(kThreads) void k_attn(AttnArgs a) {
-    constexpr int EPL = 8;              // elements per lane per token row
-    constexpr int LPT = D / EPL;        // lanes per token row (8 or 16)
-    constexpr int TPP = kThreads / LPT; // tokens per pass
-    extern __shared__ __align__(16) float sm[];
-    float *qs = sm;                     // [G][D]
-    float *kn = qs + G * D;             // [D]
-    float *vn = kn + D;                 // [D]
-    float *sc = vn + D;                 // [G][chmax]
-    float *red = sc + G * a.chmax;      // [waves][G][D] (PV partials) / scratch
-    __shared__ float mls[2 * G];
-    __shared__ int is_last;
-
-    const int kvh = blockIdx.y, s = blockIdx.x, tid = threadIdx.x;
-    const int pos = *a.posp;
-    const int T = pos + 1;
-    const int CH = (T + a.nsplit - 1) / a.nsplit;
-    const int t0 = s * CH, t1 = min(T, t0 + CH);
-    const int nact = (T + CH - 1) / CH;
-    if (t0 >= T) return;
-    const int half = D / 2;
-    const bool rot = a.knew != nullptr;
-    const float *cs = a.rope + (size_t)pos * half;
-    const float *sn = cs + a.sin_off;
-    for (int i = tid; i < G * D; i += kThreads) {
-        const int g = i / D, d = i % D;
-        const float *qh = a.q + (size_t)(kvh * G + g) * D;
-        float v;
-        if (rot) {
-            if (d < half) v = qh[d] * cs[d] - qh[d + half] * sn[d];
-            else v = qh[d - half] * sn[d - half] + qh[d] * cs[d - half];
-        } else {
-            v = qh[d];
-        }
-        qs[i] = v;
-    }
-    const bool has_new = rot && (t1 == T);
-    KT *kc = (KT *)a.kc, *vc = (KT *)a.vc;
-    if (has_new) {
-        const float *kh = a.knew + (size_t)kvh * D, *vh = a.vnew + (size_t)kvh * D;
-        for (int d = tid; d < D; d += kThreads) {
-            float kr;
-            if (d < half) kr = kh[d] * cs[d] - kh[d + half] * sn[d];
-            else kr = kh[d - half] * sn[d - half] + kh[d] * cs[d - half];
-            kr = kv_round(kr, (const KT *)nullptr);
-            const float vr = kv_round(vh[d], (const KT *)nullptr);
-            kn[d] = kr;
-            vn[d] = vr;
-            kv_store(kc + ((size_t)pos * a.nkv + kvh) * D + d, kr);
-            kv_store(vc + ((size_t)pos * a.nkv + kvh) * D + d, vr);
-        }
-    }
-    __syncthreads();
-
-    const float scale = 1.0f / sqrtf((float)D);
-    const int tk = tid / LPT, c = tid % LPT;
-    float qr[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qr[g][e] = qs[g * D + c * EPL + e];
-    for (int t = t0 + tk; t < t1; t += TPP) {
-        float kv[EPL];
-        if (has_new && t == pos) {
-#pragma unroll
-            for (int e = 0; e < EPL; e++) kv[e] = kn[c * EPL + e];
-        } else {
-            load8<KT>(kc + ((size_t)t * a.nkv + kvh) * D + c * EPL, kv);
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float p = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) p += qr[g][e] * kv[e];
-            p = group_sum<LPT>(p);
-            if (c == 0) sc[g * a.chmax + (t - t0)] = p * scale;
-        }
-    }
-    __syncthreads();
-    // chunk softmax statistics, one wave per head
-    const int wave = tid >> 6, lane = tid & 63;
-    const int n = t1 - t0;
-    for (int g = wave; g < G; g += kThreads / 64) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * a.chmax + i]);
-        m = group_max<64>(m);
-        float l = 0.0f;
-        for (int i = lane; i < n; i += 64) {
-            const float p = expf(sc[g * a.chmax + i] - m);
-            sc[g * a.chmax + i] = p;
-            l += p;
-        }
-        l = group_sum<64>(l);
-        if (lane == 0) { mls[2 * g] = m; mls[2 * g + 1] = l; }
-    }
-    __syncthreads();
-    float acc[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
-    for (int t = t0 + tk; t < t1; t += TPP) {
-        float vv[EPL];
-        if (has_new && t == pos) {
-#pragma unroll
-            for (int e = 0; e < EPL; e++) vv[e] = vn[c * EPL + e];
-        } else {
-            load8<KT>(vc + ((size_t)t * a.nkv + kvh) * D + c * EPL, vv);
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float p = sc[g * a.chmax + (t - t0)];
-#pragma unroll
-            for (int e = 0; e < EPL; e++) acc[g][e] += p * vv[e];
-        }
-    }
-    // reduce the token groups of a wave with shuffles, then the 4 waves in LDS
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            float v = acc[g][e];
-#pragma unroll
-            for (int o = LPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-            acc[g][e] = v;
-        }
-    if (lane < LPT) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < EPL; e++) red[(wave * G + g) * D + c * EPL + e] = acc[g][e];
-    }
-    __syncthreads();
-    const int P = G * (D + 2);
-    float *mypart = a.part + ((size_t)kvh * a.nsplit + s) * P;
-    for (int i = tid; i < G * D; i += kThreads) {
-        float o = 0.0f;
-        for (int j = 0; j < kThreads / 64; j++) o += red[j * G * D + i];
-        mypart[i] = o;
-    }
-    if (tid < G) {
-        mypart[G * D + 2 * tid] = mls[2 * tid];
-        mypart[G * D + 2 * tid + 1] = mls[2 * tid + 1];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int old = atomicAdd(&a.counters[kvh], 1);
-        is_last = (old == nact - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    // merge the nact chunk partials of this kv head
-    float *mo = red;  // [G][D]
-    for (int i = tid; i < G * D; i += kThreads) {
-        const int g = i / D;
-        float M = -INFINITY;
-        for (int j = 0; j < nact; j++) {
-            const float *pj = a.part + ((size_t)kvh * a.nsplit + j) * P;
-            M = fmaxf(M, __builtin_nontemporal_load(pj + G * D + 2 * g));
-        }
-        float L = 0.0f, O = 0.0f;
-        for (int j = 0; j < nact; j++) {
-            const float *pj = a.part + ((size_t)kvh * a.nsplit + j) * P;
-            const float f = expf(__builtin_nontemporal_load(pj + G * D + 2 * g) - M);
-            L += __builtin_nontemporal_load(pj + G * D + 2 * g + 1) * f;
-            O += __builtin_nontemporal_load(pj + i) * f;
-        }
-        const float inv = 1.0f / L;
-        const float v = O * inv;
-        mo[i] = v;
-        a.out[(size_t)kvh * G * D + i] = v;
-    }
-    __syncthreads();
-    if (tid == 0) a.counters[kvh] = 0;
-    if (a.oq) {
-        const int nb = G * D / 32;
-        for (int b = tid; b < nb; b += kThreads) {
-            const int gb = kvh * nb + b;
-            quant_block32(mo + b * 32, a.oq + gb * 32, a.os + gb, a.osum + gb);
-        }
-    }
 }
 
 // Decode-step head: choose the token (prompt slot or previous argmax) and
@@ -683,9 +287,11 @@ struct fl_ctx {
     void *kcache = nullptr, *vcache = nullptr;
     size_t kv_layer_elems = 0;
     float *rope = nullptr;
-    int nsplit = 1, chmax = 1;
+    int nsplit = 1, chmax = 1, chmin = 1;
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
+    float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
+    long long *bench_trace = nullptr;  // attention phase timestamps (FLARE_ATTN_TRACE builds)
     int8_t *aq = nullptr, *hq = nullptr;
     float *as = nullptr, *hs = nullptr;
     int *asum = nullptr, *hsum = nullptr;
@@ -807,111 +413,34 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws, int n, fl_
     return 0;
 }
 
-// ---- launch plans ----------------------------------------------------------
+// ---- launches ---------------------------------------------------------------
 
-static int units_per_row(int fmt, int cols) {
-    switch (fmt) {
-    case FL_Q8_0: return cols / 32;
-    case FL_Q4K:
-    case FL_Q6K: return cols / 64;
-    default: return cols / 4;
-    }
-}
-static int pick_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
-static int pick_r(int rows, int groups) {
-    for (int r : {8, 4, 2}) {
-        if ((rows + groups * r - 1) / (groups * r) >= 512) return r;
-    }
-    return 1;
-}
-static size_t q8_lds(int K) { return (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64; }
-
-typedef void (*q8in_fn)(WDesc, const float *, const float *, float, const int8_t *, const float *,
-                        const int *, float *, unsigned long long *);
-typedef void (*f32in_fn)(WDesc, const float *, const float *, float, float *, unsigned long long *);
-typedef void (*gu_fn)(WDesc, int, const float *, const float *, float, const int8_t *, const float *,
-                      const int *, int8_t *, float *, int *, float *);
-
-template <int FMT, int PRO, int EPI>
-static q8in_fn q8in_pick(int lpr, int r) {
-#define Q8C(L, RR) \
-    if (lpr == L && r == RR) return k_mv_q8in<FMT, L, RR, PRO, EPI>;
-    Q8C(64, 1) Q8C(64, 2) Q8C(64, 4) Q8C(64, 8)
-    Q8C(32, 1) Q8C(32, 2) Q8C(32, 4) Q8C(32, 8)
-    Q8C(16, 1) Q8C(16, 2) Q8C(16, 4) Q8C(16, 8)
-#undef Q8C
-    return nullptr;
-}
-template <int FMT>
-static q8in_fn q8in_pick_any(int pro, int epi, int lpr, int r) {
-    if (pro == PRO_LOADQ && epi == EPI_STORE) return q8in_pick<FMT, PRO_LOADQ, EPI_STORE>(lpr, r);
-    if (pro == PRO_LOADQ && epi == EPI_ADD) return q8in_pick<FMT, PRO_LOADQ, EPI_ADD>(lpr, r);
-    if (pro == PRO_LOADQ && epi == EPI_ARGMAX) return q8in_pick<FMT, PRO_LOADQ, EPI_ARGMAX>(lpr, r);
-    if (pro == PRO_NORMQ0 && epi == EPI_STORE) return q8in_pick<FMT, PRO_NORMQ0, EPI_STORE>(lpr, r);
-    if (pro == PRO_NORMQ1 && epi == EPI_STORE) return q8in_pick<FMT, PRO_NORMQ1, EPI_STORE>(lpr, r);
-    if (pro == PRO_NORMQ1 && epi == EPI_ARGMAX) return q8in_pick<FMT, PRO_NORMQ1, EPI_ARGMAX>(lpr, r);
-    return nullptr;
-}
-
-template <int FMT, int PRO, int EPI>
-static f32in_fn f32in_pick(int lpr, int r) {
-#define FC(L, RR) \
-    if (lpr == L && r == RR) return k_mv_f32in<FMT, L, RR, PRO, EPI>;
-    FC(64, 1) FC(64, 2) FC(64, 4) FC(64, 8)
-    FC(32, 1) FC(32, 2) FC(32, 4) FC(32, 8)
-    FC(16, 1) FC(16, 2) FC(16, 4) FC(16, 8)
-#undef FC
-    return nullptr;
-}
-template <int FMT>
-static f32in_fn f32in_pick_any(int pro, int epi, int lpr, int r) {
-    if (pro == 0 && epi == EPI_STORE) return f32in_pick<FMT, 0, EPI_STORE>(lpr, r);
-    if (pro == 0 && epi == EPI_ARGMAX) return f32in_pick<FMT, 0, EPI_ARGMAX>(lpr, r);
-    if (pro == 1 && epi == EPI_STORE) return f32in_pick<FMT, 1, EPI_STORE>(lpr, r);
-    if (pro == 1 && epi == EPI_ARGMAX) return f32in_pick<FMT, 1, EPI_ARGMAX>(lpr, r);
-    return nullptr;
-}
-
-struct Plan {
-    int lpr = 64, r = 1, grid = 1;
-    size_t lds = 0;
-};
-
-static Plan plan_for(int fmt, int rows, int cols, bool f32in) {
-    Plan p;
-    p.lpr = pick_lpr(units_per_row(fmt, cols));
-    const int groups = kThreads / p.lpr;
-    p.r = pick_r(rows, groups);
-    p.grid = (rows + groups * p.r - 1) / (groups * p.r);
-    p.lds = f32in ? (size_t)cols * 4 + 64 * 4 : q8_lds(cols);
-    return p;
-}
-
-// Launch a Q8-input matvec with prologue `pro` and epilogue `epi`.
 static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                        const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
-                       float *out, unsigned long long *slot, const char **name = nullptr) {
-    const Plan p = plan_for(w.format, w.rows, w.cols, false);
-    q8in_fn fn = nullptr;
-    if (w.format == FL_Q8_0) fn = q8in_pick_any<F_Q8_0>(pro, epi, p.lpr, p.r);
-    else if (w.format == FL_Q4K) fn = q8in_pick_any<F_Q4K>(pro, epi, p.lpr, p.r);
-    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no Q8-input kernel for format %d", w.format);
-    if (name) *name = w.format == FL_Q8_0 ? "k_mv_q8in<Q8_0>" : "k_mv_q8in<Q4_K>";
-    hipLaunchKernelGGL(fn, dim3(p.grid), dim3(kThreads), p.lds, ctx->stream, w.desc(), x, nw, eps, q, s,
-                       sums, out, slot);
+                       float *out, unsigned long long *slot) {
+    const MvPlan p = mv_plan(w.format, w.rows, w.cols, false);
+    Q8inArgs a{w.desc(), pro, epi, x, nw, eps, q, s, sums, out, slot};
+    hipError_t e;
+    if (w.format == FL_Q8_0) e = launch_mv_q8in_q8_0(p, ctx->stream, a);
+    else if (w.format == FL_Q4K) e = launch_mv_q8in_q4k(p, ctx->stream, a);
+    else return fail(ctx, FL_E_UNSUPPORTED, "no Q8-input matvec for format %d", w.format);
+    if (e == hipErrorNotSupported)
+        return fail(ctx, FL_E_UNSUPPORTED, "no kernel for plan lpr=%d r=%d u=%d", p.lpr, p.r, p.u);
+    HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
 
 static int launch_f32in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                         const float *nw, float eps, float *out, unsigned long long *slot) {
-    const Plan p = plan_for(w.format, w.rows, w.cols, true);
-    f32in_fn fn = nullptr;
-    if (w.format == FL_Q8_0) fn = f32in_pick_any<F_Q8_0>(pro, epi, p.lpr, p.r);
-    else if (w.format == FL_Q6K) fn = f32in_pick_any<F_Q6K>(pro, epi, p.lpr, p.r);
-    else if (w.format == FL_F32) fn = f32in_pick_any<F_F32>(pro, epi, p.lpr, p.r);
-    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no f32-input kernel for format %d", w.format);
-    hipLaunchKernelGGL(fn, dim3(p.grid), dim3(kThreads), p.lds, ctx->stream, w.desc(), x, nw, eps, out, slot);
+    if (w.format != FL_Q8_0 && w.format != FL_Q6K && w.format != FL_F32)
+        return fail(ctx, FL_E_UNSUPPORTED, "no f32-input matvec for format %d", w.format);
+    const MvPlan p = mv_plan(w.format, w.rows, w.cols, true);
+    F32Args a{w.desc(), pro, epi, x, nw, eps, out, slot};
+    const hipError_t e = launch_mv_f32in(w.format, p, ctx->stream, a);
+    if (e == hipErrorNotSupported)
+        return fail(ctx, FL_E_UNSUPPORTED, "no kernel for plan lpr=%d r=%d u=%d", p.lpr, p.r, p.u);
+    HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
@@ -921,58 +450,25 @@ static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *
                          float *hs, int *hsum, float *hout) {
     const int F = w.rows / 2;
     if (w.rows % 2 || F % 32) return fail(ctx, FL_E_INVALID, "gate_up rows %d must be 2*32k", w.rows);
-    const int lpr = pick_lpr(units_per_row(w.format, w.cols));
-    gu_fn fn = nullptr;
-#define GUC(FM, L, P) \
-    if (lpr == L && pro == P) fn = k_gateup<FM, L, P>;
-    if (w.format == FL_Q8_0) {
-        GUC(F_Q8_0, 64, PRO_NORMQ0) GUC(F_Q8_0, 32, PRO_NORMQ0) GUC(F_Q8_0, 16, PRO_NORMQ0)
-        GUC(F_Q8_0, 64, PRO_NORMQ1) GUC(F_Q8_0, 32, PRO_NORMQ1) GUC(F_Q8_0, 16, PRO_NORMQ1)
-        GUC(F_Q8_0, 64, PRO_LOADQ) GUC(F_Q8_0, 32, PRO_LOADQ) GUC(F_Q8_0, 16, PRO_LOADQ)
-    } else if (w.format == FL_Q4K) {
-        GUC(F_Q4K, 64, PRO_NORMQ0) GUC(F_Q4K, 32, PRO_NORMQ0) GUC(F_Q4K, 16, PRO_NORMQ0)
-        GUC(F_Q4K, 64, PRO_NORMQ1) GUC(F_Q4K, 32, PRO_NORMQ1) GUC(F_Q4K, 16, PRO_NORMQ1)
-        GUC(F_Q4K, 64, PRO_LOADQ) GUC(F_Q4K, 32, PRO_LOADQ) GUC(F_Q4K, 16, PRO_LOADQ)
-    }
-#undef GUC
-    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel for format %d", w.format);
-    const size_t lds = q8_lds(w.cols) + 80 * 4;
-    hipLaunchKernelGGL(fn, dim3(F / 32), dim3(kThreads), lds, ctx->stream, w.desc(), F, x, nw, eps, q,
-                       s, sums, hq, hs, hsum, hout);
+    GuArgs a{w.desc(), F, pro, x, nw, eps, q, s, sums, hq, hs, hsum, hout};
+    const GuPlan p = gu_plan(w.format, w.cols);
+    hipError_t e;
+    if (w.format == FL_Q8_0) e = launch_gateup_q8_0(p, F / 32, ctx->stream, a);
+    else if (w.format == FL_Q4K) e = launch_gateup_q4k(p, F / 32, ctx->stream, a);
+    else return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel for format %d", w.format);
+    if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel lpr=%d u=%d", p.lpr, p.u);
+    HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
 
-typedef void (*attn_fn)(AttnArgs);
-template <typename KT>
-static attn_fn attn_pick(int D, int G) {
-#define AC(DD, GG) \
-    if (D == DD && G == GG) return k_attn<KT, DD, GG>;
-    AC(64, 1) AC(64, 2) AC(64, 3) AC(64, 4) AC(64, 8)
-    AC(128, 1) AC(128, 2) AC(128, 3) AC(128, 4) AC(128, 8)
-#undef AC
-    return nullptr;
-}
-static size_t attn_lds(int D, int G, int chmax) {
-    return (size_t)(G * D + 2 * D + G * chmax + (kThreads / 64) * G * D) * 4;
-}
-
-static int launch_attn(fl_ctx *ctx, int kv_format, int D, int G, AttnArgs &a) {
-    attn_fn fn = kv_format == FL_KV_F16 ? attn_pick<__half>(D, G) : attn_pick<float>(D, G);
-    if (!fn) return fail(ctx, FL_E_UNSUPPORTED, "attention: head_dim %d / group %d not supported", D, G);
-    hipLaunchKernelGGL(fn, dim3(a.nsplit, a.nkv), dim3(kThreads), attn_lds(D, G, a.chmax), ctx->stream, a);
+static int launch_attention(fl_ctx *ctx, int kv_format, int D, int G, AttnArgs &a) {
+    const hipError_t e = launch_attn(kv_format == FL_KV_F16, D, G, ctx->stream, a);
+    if (e == hipErrorNotSupported)
+        return fail(ctx, FL_E_UNSUPPORTED, "attention: head_dim %d / group %d not supported", D, G);
+    HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
-}
-
-static void choose_splits(int max_seq, int nkv, int &nsplit, int &chmax) {
-    // enough workgroups to cover the chip at long context, chunks <= 512
-    int ns = (max_seq + 63) / 64;
-    ns = std::max(1, std::min(ns, 256));
-    if (ns * nkv < 64) ns = std::min((max_seq + 15) / 16, std::max(ns, 64 / std::max(nkv, 1)));
-    ns = std::max(1, ns);
-    nsplit = ns;
-    chmax = (max_seq + ns - 1) / ns;
 }
 
 static int ensure_part(fl_ctx *ctx, size_t floats) {
@@ -1036,12 +532,13 @@ static void model_release(fl_ctx *c) {
     c->layers.clear();
     weight_release(c->embed);
     weight_release(c->output);
-    void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits,
+    void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits, c->bench_out,
+                    c->bench_trace,
                     c->aq, c->hq, c->as, c->hs, c->asum, c->hsum, c->st, c->tokens};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
-    c->attn = c->logits = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
+    c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
     c->have_cfg = c->have_weights = false;
 }
@@ -1236,9 +733,9 @@ int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void
     if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format");
     const int G = num_heads / num_kv_heads;
     int ns, ch;
-    choose_splits(seq_len, num_kv_heads, ns, ch);
+    choose_splits(seq_len, num_kv_heads, head_dim, ns, ch);
     if (num_splits > 0) {
-        ns = std::min(num_splits, seq_len);
+        ns = std::min(num_splits, 1024);
         ch = (seq_len + ns - 1) / ns;
     }
     const size_t need = (size_t)num_kv_heads * ns * G * (head_dim + 2);
@@ -1250,14 +747,17 @@ int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void
     a.q = q;
     a.kc = (void *)k_cache;
     a.vc = (void *)v_cache;
+    a.tok_stride = (long long)num_kv_heads * head_dim;  // [slot][kv_head][head_dim]
+    a.head_stride = head_dim;
     a.posp = ctx->d_pos;
     a.nkv = num_kv_heads;
     a.nsplit = ns;
     a.chmax = ch;
+    a.chmin = num_splits > 0 ? 1 : attn_chmin(head_dim);
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = out;
-    rc = launch_attn(ctx, kv_format, head_dim, G, a);
+    rc = launch_attention(ctx, kv_format, head_dim, G, a);
     if (rc) return rc;
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // pos staged from the host stack
     return 0;
@@ -1274,7 +774,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         return fail(ctx, FL_E_INVALID,
                     "unsupported config (hidden %% 32, head_dim 64/128, inter %% 32 required)");
     if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format %d", kv_format);
-    if (!attn_pick<float>(c.head_dim, c.num_heads / c.num_kv_heads))
+    if (!attn_supported(c.head_dim, c.num_heads / c.num_kv_heads))
         return fail(ctx, FL_E_UNSUPPORTED, "heads per kv group %d", c.num_heads / c.num_kv_heads);
     model_release(ctx);
     ctx->cfg = c;
@@ -1295,7 +795,16 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         rope_row_host(c.head_dim, (int)p, c.rope_theta, &tab[p * half], &tab[S * half + p * half]);
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
-    choose_splits(c.max_seq_len, c.num_kv_heads, ctx->nsplit, ctx->chmax);
+    choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmax);
+    ctx->chmin = attn_chmin(c.head_dim);
+    if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
+    if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
+        const int ns = atoi(ev);
+        if (ns > 0 && ns <= 1024) {
+            ctx->nsplit = ns;
+            ctx->chmax = (c.max_seq_len + ns - 1) / ns;
+        }
+    }
     const int G = c.num_heads / c.num_kv_heads;
     int rc = ensure_part(ctx, (size_t)c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
     if (rc) return rc;
@@ -1309,6 +818,8 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->hs, F / 32 * 4);
     ALLOC(ctx, ctx->hsum, F / 32 * 4);
     ALLOC(ctx, ctx->logits, (size_t)c.vocab_size * 4);
+    ALLOC(ctx, ctx->bench_out, std::max({(size_t)c.vocab_size, H, qd + 2 * kvd, 2 * F}) * 4);
+    ALLOC(ctx, ctx->bench_trace, 64 * 8);
     ALLOC(ctx, ctx->st, sizeof(DevState));
     ALLOC(ctx, ctx->tokens, S * 4);
     HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
@@ -1398,19 +909,22 @@ int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const fl
     const fl_model_config &c = ctx->cfg;
     if (layer < 0 || layer >= c.num_layers) return fail(ctx, FL_E_INVALID, "layer %d", layer);
     const int slot = position % c.max_seq_len;  // ring write (GpuKvCache::write)
-    const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
-    const size_t off = (size_t)layer * ctx->kv_layer_elems + (size_t)slot * kvd;
-    if (ctx->kv_format == FL_KV_F32) {
-        HIPCHK(ctx, hipMemcpy((float *)ctx->kcache + off, key, kvd * 4, hipMemcpyHostToDevice));
-        HIPCHK(ctx, hipMemcpy((float *)ctx->vcache + off, value, kvd * 4, hipMemcpyHostToDevice));
-    } else {
-        std::vector<__half> hk(kvd), hv(kvd);
-        for (size_t i = 0; i < kvd; i++) {
-            hk[i] = __float2half(key[i]);
-            hv[i] = __float2half(value[i]);
+    const size_t hd = (size_t)c.head_dim;
+    // device layout is head-major: [layer][kv_head][slot][head_dim]
+    for (int h = 0; h < c.num_kv_heads; h++) {
+        const size_t off = (size_t)layer * ctx->kv_layer_elems + ((size_t)h * c.max_seq_len + slot) * hd;
+        if (ctx->kv_format == FL_KV_F32) {
+            HIPCHK(ctx, hipMemcpy((float *)ctx->kcache + off, key + h * hd, hd * 4, hipMemcpyHostToDevice));
+            HIPCHK(ctx, hipMemcpy((float *)ctx->vcache + off, value + h * hd, hd * 4, hipMemcpyHostToDevice));
+        } else {
+            std::vector<__half> hk(hd), hv(hd);
+            for (size_t i = 0; i < hd; i++) {
+                hk[i] = __float2half(key[h * hd + i]);
+                hv[i] = __float2half(value[h * hd + i]);
+            }
+            HIPCHK(ctx, hipMemcpy((__half *)ctx->kcache + off, hk.data(), hd * 2, hipMemcpyHostToDevice));
+            HIPCHK(ctx, hipMemcpy((__half *)ctx->vcache + off, hv.data(), hd * 2, hipMemcpyHostToDevice));
         }
-        HIPCHK(ctx, hipMemcpy((__half *)ctx->kcache + off, hk.data(), kvd * 2, hipMemcpyHostToDevice));
-        HIPCHK(ctx, hipMemcpy((__half *)ctx->vcache + off, hv.data(), kvd * 2, hipMemcpyHostToDevice));
     }
     return 0;
 }
@@ -1457,16 +971,19 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
         a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
         a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
         a.posp = &ctx->st->pos;
+        a.tok_stride = hd;  // head-major cache: [kv_head][slot][head_dim]
+        a.head_stride = (long long)c.max_seq_len * hd;
         a.nkv = nkv;
         a.nsplit = ctx->nsplit;
         a.chmax = ctx->chmax;
+        a.chmin = ctx->chmin;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = ctx->attn;
         a.oq = ctx->aq;
         a.os = ctx->as;
         a.osum = ctx->asum;
-        rc = launch_attn(ctx, ctx->kv_format, hd, G, a);
+        rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
         if (rc) return rc;
         rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
                          nullptr);
@@ -1610,20 +1127,23 @@ int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out) {
     return 0;
 }
 
-// Launch `iters` copies of one layer-0 kernel on the context stream.
+// Launch `iters` copies of one layer kernel on the context stream, cycling
+// through the layers.
 int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_launch) {
     if (!ctx || !ctx->have_weights) return fail(ctx, FL_E_STATE, "no model");
     const fl_model_config &c = ctx->cfg;
-    Layer &L = ctx->layers[0];
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
     const fl_weight *w = nullptr;
     for (int i = 0; i < iters; i++) {
+        // cycle through the layers so repeated launches stream distinct
+        // weights from HBM instead of re-reading a cache-resident matrix
+        Layer &L = ctx->layers[i % c.num_layers];
         int rc = 0;
         switch (which) {
-        case 0: w = &L.qkv; rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->qkv, nullptr); break;
-        case 1: w = &L.wo; rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->logits, nullptr); break;
+        case 0: w = &L.qkv; rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->bench_out, nullptr); break;
+        case 1: w = &L.wo; rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->bench_out, nullptr); break;
         case 2: w = &L.gu; rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs, ctx->hsum, nullptr); break;
-        case 3: w = &L.down; rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->logits, nullptr); break;
+        case 3: w = &L.down; rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->bench_out, nullptr); break;
         case 4: {
             const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
             w = &O;
@@ -1632,11 +1152,61 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_l
             else rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, ctx->x, ctx->out_norm, c.rms_norm_eps, nullptr, ctx->d_slot);
             break;
         }
+        case 5: {  // attention of layer i % L at the current position
+            const int hd = c.head_dim, nkv = c.num_kv_heads, qd = c.num_heads * hd, kvd = nkv * hd;
+            const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+            const int l = i % c.num_layers;
+            AttnArgs a{};
+            a.q = ctx->qkv;
+            a.knew = ctx->qkv + qd;
+            a.vnew = ctx->qkv + qd + kvd;
+            a.rope = ctx->rope;
+            a.sin_off = (long long)c.max_seq_len * (hd / 2);
+            a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
+            a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
+            a.posp = &ctx->st->pos;
+            a.tok_stride = hd;
+            a.head_stride = (long long)c.max_seq_len * hd;
+        a.tok_stride = hd;  // head-major cache: [kv_head][slot][head_dim]
+        a.head_stride = (long long)c.max_seq_len * hd;
+            a.nkv = nkv;
+            a.nsplit = ctx->nsplit;
+            a.chmax = ctx->chmax;
+            a.chmin = ctx->chmin;
+        a.chmin = ctx->chmin;
+            a.part = ctx->d_part;
+            a.counters = ctx->d_counters;
+            a.out = ctx->attn;
+            a.oq = ctx->aq;
+            a.os = ctx->as;
+            a.osum = ctx->asum;
+            a.skip_merge = getenv("FLARE_ATTN_SKIP_MERGE") != nullptr;
+            a.trace = ctx->bench_trace;
+            rc = launch_attention(ctx, ctx->kv_format, hd, c.num_heads / nkv, a);
+            break;
+        }
         default: return fail(ctx, FL_E_INVALID, "which=%d", which);
         }
         if (rc) return rc;
     }
-    if (bytes_per_launch && w) *bytes_per_launch = (double)w->gguf_bytes;
+    if (which == 5 && getenv("FLARE_ATTN_TRACE_PRINT")) {
+        long long tr[24] = {0};
+        HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+        HIPCHK(ctx, hipMemcpy(tr, ctx->bench_trace, sizeof tr, hipMemcpyDeviceToHost));
+        fprintf(stderr, "attn trace (10ns ticks from start):");
+        for (int i = 1; i < 9; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        fprintf(stderr, " | batch0:");
+        for (int i = 10; i < 18; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        fprintf(stderr, "\n");
+    }
+    if (bytes_per_launch && which == 5) {
+        DevState st{};
+        HIPCHK(ctx, hipMemcpy(&st, ctx->st, sizeof st, hipMemcpyDeviceToHost));
+        const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+        *bytes_per_launch = 2.0 * (st.pos + 1) * c.num_kv_heads * c.head_dim * esz;
+    } else if (bytes_per_launch && w) {
+        *bytes_per_launch = (double)w->gguf_bytes;
+    }
     return 0;
 }
 
@@ -1648,6 +1218,7 @@ const char *fl_bench_kernel_name(fl_ctx *ctx, int which) {
     case 2: return "k_gateup";
     case 3: return "k_mv_q8in";
     case 4: return ctx->tied || ctx->output.format == FL_Q6K ? "k_mv_f32in" : "k_mv_q8in";
+    case 5: return "k_attn";
     }
     return "";
 }

@@ -208,3 +208,22 @@ def test_attention(backend, oracle, nh, nkv, hd, T, dt, splits):
     got = backend.attention(_t(q), kt, vt, nh, nkv, hd, T, splits).cpu().numpy()
     want = oracle.gqa_attention(q, kt.float().cpu().numpy(), vt.float().cpu().numpy(), nh, nkv, hd, T)
     _close(got, want)
+
+
+@pytest.mark.parametrize("T,splits", [(8192, 0), (3000, 17), (700, 0)])
+def test_attention_split_merge_repeatable(backend, oracle, T, splits):
+    """Cross-workgroup split merge: repeated launches agree bit-for-bit."""
+    import torch
+
+    nh, nkv, hd = 32, 8, 128
+    print(f"[attention-merge] T={T} splits={splits}", flush=True)
+    q = _act(61, nh * hd)
+    k = _act(67, T * nkv * hd).reshape(T, nkv, hd)
+    v = _act(71, T * nkv * hd).reshape(T, nkv, hd)
+    kt = torch.from_numpy(k).half().cuda()
+    vt = torch.from_numpy(v).half().cuda()
+    outs = [backend.attention(_t(q), kt, vt, nh, nkv, hd, T, splits).cpu().numpy() for _ in range(20)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    want = oracle.gqa_attention(q, kt.float().cpu().numpy(), vt.float().cpu().numpy(), nh, nkv, hd, T)
+    _close(outs[0], want)
