@@ -74,6 +74,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=6)
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the decode path "
@@ -153,6 +155,16 @@ def main() -> int:
                 "frac": round(d["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
                 "kernel": f"{dom} ({d['kernel']})", "bytes_per_launch": d["bytes"]}
     b.close()
+    if args.calibrate_copy:
+        # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE
+        # counters calibrate the per-kernel HBM traffic readings
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {src.numel() * 4} bytes read, {dst.numel() * 4} bytes written")
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -299,6 +299,7 @@ struct fl_ctx {
     int *tokens = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
+    bool graph_ready = false;
 };
 
 static std::string g_err;
@@ -418,6 +419,8 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws, int n, fl_
 static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                        const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
                        float *out, unsigned long long *slot) {
+    if (pro == PRO_LOADQ && w.cols > 4 * 16 * kThreads)
+        return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
     const MvPlan p = mv_plan(w.format, w.rows, w.cols, false);
     Q8inArgs a{w.desc(), pro, epi, x, nw, eps, q, s, sums, out, slot};
     hipError_t e;
@@ -450,11 +453,12 @@ static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *
                          float *hs, int *hsum, float *hout) {
     const int F = w.rows / 2;
     if (w.rows % 2 || F % 32) return fail(ctx, FL_E_INVALID, "gate_up rows %d must be 2*32k", w.rows);
-    GuArgs a{w.desc(), F, pro, x, nw, eps, q, s, sums, hq, hs, hsum, hout};
-    const GuPlan p = gu_plan(w.format, w.cols);
+    GuArgs a{w.desc(), F, pro, x, nw, eps, q, s, sums, hq, hs, hsum, hout, ctx->bench_trace};
+    const GuPlan p = gu_plan(w.format, w.cols, F);
+    if (p.u == 0) return fail(ctx, FL_E_UNSUPPORTED, "gate_up input of %d columns is too wide", w.cols);
     hipError_t e;
-    if (w.format == FL_Q8_0) e = launch_gateup_q8_0(p, F / 32, ctx->stream, a);
-    else if (w.format == FL_Q4K) e = launch_gateup_q4k(p, F / 32, ctx->stream, a);
+    if (w.format == FL_Q8_0) e = launch_gateup_q8_0(p, ctx->stream, a);
+    else if (w.format == FL_Q4K) e = launch_gateup_q4k(p, ctx->stream, a);
     else return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel for format %d", w.format);
     if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel lpr=%d u=%d", p.lpr, p.u);
     HIPCHK(ctx, e);
@@ -524,6 +528,7 @@ static void model_release(fl_ctx *c) {
     if (c->graph) (void)hipGraphDestroy(c->graph);
     c->gexec = nullptr;
     c->graph = nullptr;
+    c->graph_ready = false;
     for (auto &l : c->layers) {
         weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
         if (l.attn_norm) (void)hipFree(l.attn_norm);
@@ -862,6 +867,7 @@ int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *con
     ctx->have_weights = false;
     if (ctx->gexec) { (void)hipGraphExecDestroy(ctx->gexec); ctx->gexec = nullptr; }
     if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
+    ctx->graph_ready = false;
     for (auto &l : ctx->layers) {
         weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
         if (l.attn_norm) (void)hipFree(l.attn_norm);
@@ -1011,7 +1017,24 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     return rc;
 }
 
+// FLARE_NO_GRAPH=1: enqueue the step's kernels directly instead of replaying a
+// HIP graph (identical kernels; for profilers that cannot follow graphs).
+static bool use_graph() {
+    static const bool g = getenv("FLARE_NO_GRAPH") == nullptr;
+    return g;
+}
+
+static int launch_step(fl_ctx *ctx) {
+    if (!use_graph()) return enqueue_step(ctx, false);
+    HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    return 0;
+}
+
 static int ensure_graph(fl_ctx *ctx) {
+    if (!use_graph()) {
+        ctx->graph_ready = true;
+        return 0;
+    }
     if (ctx->gexec) return 0;
     HIPCHK(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_step(ctx, false);
@@ -1024,6 +1047,7 @@ static int ensure_graph(fl_ctx *ctx) {
     if (e != hipSuccess) return fail(ctx, FL_E_HIP, "graph capture failed: %s", hipGetErrorString(e));
     ctx->graph = g;
     HIPCHK(ctx, hipGraphInstantiate(&ctx->gexec, g, nullptr, nullptr, 0));
+    ctx->graph_ready = true;
     return 0;
 }
 
@@ -1046,8 +1070,8 @@ int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int3
         if (rc) return rc;
     } else {
         int rc = ensure_graph(ctx);
+        if (!rc) rc = launch_step(ctx);
         if (rc) return rc;
-        HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
     }
     DevState out{};
     HIPCHK(ctx, hipMemcpyAsync(&out, ctx->st, sizeof out, hipMemcpyDeviceToHost, ctx->stream));
@@ -1091,7 +1115,10 @@ int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen, ui
     hs.n_prompt = n_prompt;
     HIPCHK(ctx, hipMemcpyAsync(ctx->tokens, toks.data(), (size_t)n_prompt * 4, hipMemcpyHostToDevice, ctx->stream));
     HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
-    for (int s = 0; s < steps; s++) HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    for (int s = 0; s < steps; s++) {
+        rc = launch_step(ctx);
+        if (rc) return rc;
+    }
     std::vector<int> gen((size_t)std::max(n_gen - 1, 1));
     DevState out{};
     if (n_gen > 1)
@@ -1106,7 +1133,7 @@ int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen, ui
 
 int fl_decode_continue(fl_ctx *ctx, int n_steps) {
     if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
-    if (!ctx->gexec) return fail(ctx, FL_E_STATE, "fl_generate must run first");
+    if (!ctx->graph_ready) return fail(ctx, FL_E_STATE, "fl_generate must run first");
     if (n_steps < 0) return fail(ctx, FL_E_INVALID, "n_steps < 0");
     DevState st{};
     HIPCHK(ctx, hipMemcpyAsync(&st, ctx->st, sizeof st, hipMemcpyDeviceToHost, ctx->stream));
@@ -1114,7 +1141,10 @@ int fl_decode_continue(fl_ctx *ctx, int n_steps) {
     if (st.step + n_steps > ctx->cfg.max_seq_len)
         return fail(ctx, FL_E_INVALID, "continuing %d steps from %d exceeds max_seq_len %d", n_steps, st.step,
                     ctx->cfg.max_seq_len);
-    for (int s = 0; s < n_steps; s++) HIPCHK(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+    for (int s = 0; s < n_steps; s++) {
+        const int rc = launch_step(ctx);
+        if (rc) return rc;
+    }
     return 0;
 }
 
@@ -1188,6 +1218,14 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_l
         default: return fail(ctx, FL_E_INVALID, "which=%d", which);
         }
         if (rc) return rc;
+    }
+    if (which == 2 && getenv("FLARE_MV_TRACE_PRINT")) {
+        long long tr[8] = {0};
+        HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+        HIPCHK(ctx, hipMemcpy(tr, ctx->bench_trace, sizeof tr, hipMemcpyDeviceToHost));
+        fprintf(stderr, "gate_up trace (10ns ticks from start):");
+        for (int i = 1; i < 6; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        fprintf(stderr, "\n");
     }
     if (which == 5 && getenv("FLARE_ATTN_TRACE_PRINT")) {
         long long tr[24] = {0};

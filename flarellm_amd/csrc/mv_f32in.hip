@@ -5,14 +5,14 @@ namespace fl {
 
 template <int FMT>
 static hipError_t launch_f32in_fmt(const MvPlan &p, hipStream_t st, const F32Args &a) {
-#define C(L, RR, UU)                                                                                \
-    if (p.lpr == L && p.r == RR && p.u == UU) {                                                     \
-        hipLaunchKernelGGL((k_mv_f32in<FMT, L, RR, UU>), dim3(p.grid), dim3(kThreads), p.lds, st, a); \
-        return hipSuccess;                                                                          \
+#define C(L, UU, RR)                                                                                 \
+    if (p.lpr == L && p.u == UU && p.r == RR) {                                                      \
+        hipLaunchKernelGGL((k_mv_f32in<FMT, L, UU, RR>), dim3(p.grid), dim3(kThreads), p.lds, st, a); \
+        return hipSuccess;                                                                           \
     }
-    C(64, 1, 1) C(64, 2, 1) C(64, 4, 1) C(64, 8, 1) C(64, 1, 2) C(64, 2, 2) C(64, 4, 2) C(64, 1, 4) C(64, 2, 4)
-    C(32, 1, 1) C(32, 2, 1) C(32, 4, 1) C(32, 8, 1) C(32, 1, 2) C(32, 2, 2) C(32, 4, 2)
-    C(16, 1, 1) C(16, 2, 1) C(16, 4, 1) C(16, 8, 1) C(16, 1, 2) C(16, 2, 2) C(16, 4, 2)
+#define CL(L) C(L, 1, 8) C(L, 1, 4) C(L, 1, 2) C(L, 1, 1) C(L, 2, 4) C(L, 2, 2) C(L, 2, 1) C(L, 4, 2) C(L, 4, 1)
+    CL(64) CL(32) CL(16)
+#undef CL
 #undef C
     return hipErrorNotSupported;
 }
