@@ -35,7 +35,24 @@ WORKLOADS = {
     "c1": dict(spec="SmolLM2-135M", prompt=32, kv="f32",
                desc="SmolLM2-135M arch, Q8_0 tied, greedy decode after a 32-token prompt"),
 }
-KERNEL_NAMES = {0: "qkv", 1: "wo", 2: "gate_up", 3: "down", 4: "output+argmax"}
+KERNEL_NAMES = {0: "qkv", 1: "wo", 2: "gate_up", 3: "down", 4: "output+argmax", 5: "attention"}
+# Calibrated HBM traffic per launch, from rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE runs of this script (summaries committed under profiles/):
+# lines "traffic <config> <kernel> <bytes>".
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+
+
+def measured_traffic(config: str) -> dict:
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                p = line.strip().strip("`").split()
+                if len(p) == 4 and p[0] == "traffic" and p[1] == config:
+                    out[p[2]] = int(float(p[3]))
+    except OSError:
+        pass
+    return out
 
 
 def log(*a):
@@ -72,7 +89,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--cpu-tokens", type=int, default=40)
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
@@ -128,7 +145,9 @@ def main() -> int:
     log(f"[bench] {args.steps} steps: {ms_total:.2f} ms (wall {wall * 1e3:.2f} ms) -> {tok_s:.1f} tok/s; "
         f"first tokens {toks.tolist()}")
 
-    # per-kernel HBM bandwidth, HIP events on the context stream
+    # per-kernel HBM bandwidth: HIP events on the context stream around
+    # back-to-back launches; launch i uses layer i % L, so consecutive
+    # launches stream distinct weights from HBM
     kernels = {}
     for which, name in KERNEL_NAMES.items():
         b.bench_layer_kernel(which, 3)  # warm
@@ -147,13 +166,15 @@ def main() -> int:
         log(f"[bench] {k:14s} {v['kernel']:12s} {v['us']:8.2f} us  {v['bytes'] / 1e6:8.2f} MB  {v['GB_s']:7.1f} GB/s")
     # dominant kernel: largest total time per token
     per_token = {"qkv": spec.layers, "wo": spec.layers, "gate_up": spec.layers, "down": spec.layers,
-                 "output+argmax": 1}
+                 "output+argmax": 1, "attention": spec.layers}
     dom = max(kernels, key=lambda k: kernels[k]["us"] * per_token[k])
     d = kernels[dom]
     bytes_per_token = spec.weight_bytes_per_token()
+    traffic = measured_traffic(args.config).get(dom)
     roofline = {"bound": "hbm", "achieved": d["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"{dom} ({d['kernel']})", "bytes_per_launch": d["bytes"]}
+                "frac": round(d["GB_s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": f"{dom} ({d['kernel']})", "bytes_per_launch": d["bytes"],
+                "avg_launch_us": d["us"]}
     b.close()
     if args.calibrate_copy:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE

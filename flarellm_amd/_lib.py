@@ -84,7 +84,7 @@ SIGNATURES = {
     "fl_generate": (i32, [vp, vp, i32, i32, vp]),
     "fl_decode_continue": (i32, [vp, i32]),
     "fl_read_tokens": (i32, [vp, i32, i32, vp]),
-    "fl_bench_layer_kernel": (i32, [vp, i32, i32, C.POINTER(C.c_double)]),
+    "fl_bench_layer_kernel": (i32, [vp, i32, i32, i32, C.POINTER(C.c_double)]),
     "fl_bench_kernel_name": (C.c_char_p, [vp, i32]),
     "fl_synth_normal": (None, [C.c_uint64, C.c_uint64, sz, f32, f32, vp]),
     "fl_synth_quantize": (sz, [vp, sz, sz, i32, vp]),

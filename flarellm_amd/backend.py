@@ -268,9 +268,9 @@ class HipBackend:
         check(self.lib.fl_read_tokens(self.ctx, start, n, out.ctypes.data), self.ctx)
         return out
 
-    def bench_layer_kernel(self, which: int, iters: int) -> float:
+    def bench_layer_kernel(self, which: int, iters: int, first_layer: int = 0) -> float:
         b = C.c_double()
-        check(self.lib.fl_bench_layer_kernel(self.ctx, which, iters, C.byref(b)), self.ctx)
+        check(self.lib.fl_bench_layer_kernel(self.ctx, which, first_layer, iters, C.byref(b)), self.ctx)
         return b.value
 
     def bench_kernel_name(self, which: int) -> str:

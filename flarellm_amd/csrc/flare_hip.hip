@@ -40,7 +40,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float *x, int nblk,
     float v[32];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        float4 t = ((const float4 *)(x + b * 32))[j];
+        v4f_t t = ((const v4f_t *)(x + b * 32))[j];
         v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
     }
     quant_block32(v, q + b * 32, s + b, sums + b);
@@ -68,8 +68,8 @@ __global__ __launch_bounds__(kThreads) void k_block_dots(WDesc W, const int8_t *
         const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
         if (i >= (long long)W.rows * bpr) return;
         const int row = (int)(i / bpr), b = (int)(i % bpr);
-        const int4 *p = (const int4 *)(W.q + (size_t)row * W.cols + b * 32);
-        const int4 *xp = (const int4 *)(xq + b * 32);
+        const v4i_t *p = (const v4i_t *)(W.q + (size_t)row * W.cols + b * 32);
+        const v4i_t *xp = (const v4i_t *)(xq + b * 32);
         dots[i] = dot16(p[1], xp[1], dot16(p[0], xp[0], 0));
     } else {
         const int nsb = W.cols >> 8;
@@ -79,15 +79,15 @@ __global__ __launch_bounds__(kThreads) void k_block_dots(WDesc W, const int8_t *
         const long long rs = i >> 2;
         const int row = (int)(rs / nsb), sb = (int)(rs % nsb);
         const uint8_t *blk = W.q + ((size_t)row * nsb + sb) * 144;
-        const int4 a = *(const int4 *)(blk + 16 + 32 * sub), c = *(const int4 *)(blk + 32 + 32 * sub);
+        const v4i_t a = *(const v4i_t *)(blk + 16 + 32 * sub), c = *(const v4i_t *)(blk + 32 + 32 * sub);
         const int blo = sb * 8 + sub, bhi = blo + 4;
-        const int4 *xl = (const int4 *)(xq + blo * 32), *xh = (const int4 *)(xq + bhi * 32);
-        const int4 lo0 = make_int4(a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F);
-        const int4 lo1 = make_int4(c.x & 0x0F0F0F0F, c.y & 0x0F0F0F0F, c.z & 0x0F0F0F0F, c.w & 0x0F0F0F0F);
-        const int4 hi0 = make_int4((a.x >> 4) & 0x0F0F0F0F, (a.y >> 4) & 0x0F0F0F0F,
-                                   (a.z >> 4) & 0x0F0F0F0F, (a.w >> 4) & 0x0F0F0F0F);
-        const int4 hi1 = make_int4((c.x >> 4) & 0x0F0F0F0F, (c.y >> 4) & 0x0F0F0F0F,
-                                   (c.z >> 4) & 0x0F0F0F0F, (c.w >> 4) & 0x0F0F0F0F);
+        const v4i_t *xl = (const v4i_t *)(xq + blo * 32), *xh = (const v4i_t *)(xq + bhi * 32);
+        const v4i_t lo0 = v4i_t{a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F};
+        const v4i_t lo1 = v4i_t{c.x & 0x0F0F0F0F, c.y & 0x0F0F0F0F, c.z & 0x0F0F0F0F, c.w & 0x0F0F0F0F};
+        const v4i_t hi0 = v4i_t{(a.x >> 4) & 0x0F0F0F0F, (a.y >> 4) & 0x0F0F0F0F,
+                                   (a.z >> 4) & 0x0F0F0F0F, (a.w >> 4) & 0x0F0F0F0F};
+        const v4i_t hi1 = v4i_t{(c.x >> 4) & 0x0F0F0F0F, (c.y >> 4) & 0x0F0F0F0F,
+                                   (c.z >> 4) & 0x0F0F0F0F, (c.w >> 4) & 0x0F0F0F0F};
         dots[rs * 8 + 2 * sub] = dot16(lo1, xl[1], dot16(lo0, xl[0], 0));
         dots[rs * 8 + 2 * sub + 1] = dot16(hi1, xh[1], dot16(hi0, xh[0], 0));
     }
@@ -287,7 +287,7 @@ struct fl_ctx {
     void *kcache = nullptr, *vcache = nullptr;
     size_t kv_layer_elems = 0;
     float *rope = nullptr;
-    int nsplit = 1, chmax = 1, chmin = 1;
+    int nsplit = 1, chmin = 1;
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
     float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
@@ -355,7 +355,40 @@ static int weight_cols(const fl_raw_weight *w) {
 
 // Upload `n` RawWeights sharing format and cols as one row-concatenated
 // device weight (Model::set_raw_weights fusion, model.rs:1411-1452).
-static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws, int n, fl_weight &out) {
+// Pair-interleave the rows of each head (row 2i <- row i, row 2i+1 <- row
+// i + D/2) so the rotate-half pairs of RoPE are adjacent rows (EPI_QKV).
+static std::vector<uint8_t> pair_rows(const fl_raw_weight &w, int hd) {
+    const size_t rb = row_bytes(w.format, weight_cols(&w)), rows = (size_t)w.num_rows, half = hd / 2;
+    std::vector<uint8_t> out(rows * rb);
+    const uint8_t *src = (const uint8_t *)w.data;
+    for (size_t r = 0; r < rows; r++) {
+        const size_t h = r / hd, j = r % hd;
+        const size_t dst = h * hd + (j < half ? 2 * j : 2 * (j - half) + 1);
+        std::memcpy(&out[dst * rb], src + r * rb, rb);
+    }
+    return out;
+}
+
+static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws_in, int n, fl_weight &out, int npair = 0,
+                         int hd = 0) {
+    // the first npair weights get their head rows pair-interleaved
+    std::vector<std::vector<uint8_t>> keep;
+    fl_raw_weight tmp[8];
+    const fl_raw_weight *ws[8];
+    if (n > 8) return fail(ctx, FL_E_INVALID, "too many fused weights");
+    for (int i = 0; i < n; i++) {
+        ws[i] = ws_in[i];
+        if (i < npair && ws_in[i] && ws_in[i]->data) {
+            if (ws_in[i]->num_rows % hd) return fail(ctx, FL_E_INVALID, "q/k rows not a multiple of head_dim");
+            const size_t rb = row_bytes(ws_in[i]->format, weight_cols(ws_in[i]));
+            if (rb == 0 || ws_in[i]->nbytes < rb * (size_t)ws_in[i]->num_rows)
+                return fail(ctx, FL_E_INVALID, "weight bytes %zu < rows*row_bytes", ws_in[i]->nbytes);
+            keep.push_back(pair_rows(*ws_in[i], hd));
+            tmp[i] = *ws_in[i];
+            tmp[i].data = keep.back().data();
+            ws[i] = &tmp[i];
+        }
+    }
     const int fmt = ws[0]->format, cols = weight_cols(ws[0]);
     int rows = 0;
     for (int i = 0; i < n; i++) {
@@ -418,11 +451,18 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws, int n, fl_
 
 static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                        const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
-                       float *out, unsigned long long *slot) {
+                       float *out, unsigned long long *slot, const QkvEpi *qe = nullptr) {
     if (pro == PRO_LOADQ && w.cols > 4 * 16 * kThreads)
         return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
-    const MvPlan p = mv_plan(w.format, w.rows, w.cols, false);
-    Q8inArgs a{w.desc(), pro, epi, x, nw, eps, q, s, sums, out, slot};
+    MvPlan p = mv_plan(w.format, w.rows, w.cols, false);
+    Q8inArgs a{w.desc(), pro, epi, x, nw, eps, q, s, sums, out, slot, QkvEpi{}};
+    if (epi == EPI_QKV) {
+        if (!qe) return fail(ctx, FL_E_INVALID, "EPI_QKV without its arguments");
+        if (w.rows != qe->nq + 2 * qe->nk || qe->nq % qe->hd || qe->nk % qe->hd)
+            return fail(ctx, FL_E_INVALID, "fused QKV rows %d do not match the heads", w.rows);
+        a.qkv = *qe;
+        p = mv_plan_even(p, w.format, w.rows, w.cols);
+    }
     hipError_t e;
     if (w.format == FL_Q8_0) e = launch_mv_q8in_q8_0(p, ctx->stream, a);
     else if (w.format == FL_Q4K) e = launch_mv_q8in_q4k(p, ctx->stream, a);
@@ -737,11 +777,11 @@ int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void
     if (num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads");
     if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format");
     const int G = num_heads / num_kv_heads;
-    int ns, ch;
-    choose_splits(seq_len, num_kv_heads, head_dim, ns, ch);
+    int ns, chmin;
+    choose_splits(seq_len, num_kv_heads, head_dim, ns, chmin);
     if (num_splits > 0) {
-        ns = std::min(num_splits, 1024);
-        ch = (seq_len + ns - 1) / ns;
+        ns = std::min(num_splits, kAttnMaxSplit);
+        chmin = 1;
     }
     const size_t need = (size_t)num_kv_heads * ns * G * (head_dim + 2);
     int rc = ensure_part(ctx, need);
@@ -757,8 +797,7 @@ int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void
     a.posp = ctx->d_pos;
     a.nkv = num_kv_heads;
     a.nsplit = ns;
-    a.chmax = ch;
-    a.chmin = num_splits > 0 ? 1 : attn_chmin(head_dim);
+    a.chmin = chmin;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = out;
@@ -800,15 +839,11 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         rope_row_host(c.head_dim, (int)p, c.rope_theta, &tab[p * half], &tab[S * half + p * half]);
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
-    choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmax);
-    ctx->chmin = attn_chmin(c.head_dim);
+    choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
     if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
     if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
         const int ns = atoi(ev);
-        if (ns > 0 && ns <= 1024) {
-            ctx->nsplit = ns;
-            ctx->chmax = (c.max_seq_len + ns - 1) / ns;
-        }
+        if (ns > 0 && ns <= kAttnMaxSplit) ctx->nsplit = ns;
     }
     const int G = c.num_heads / c.num_kv_heads;
     int rc = ensure_part(ctx, (size_t)c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
@@ -882,7 +917,7 @@ int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *con
         const fl_raw_weight *gu[2] = {&w[4], &w[5]};
         const fl_raw_weight *dn[1] = {&w[6]};
         Layer &L = ctx->layers[l];
-        int rc = upload_concat(ctx, qkv, 3, L.qkv);
+        int rc = upload_concat(ctx, qkv, 3, L.qkv, 2, c.head_dim);
         if (!rc) rc = upload_concat(ctx, wo, 1, L.wo);
         if (!rc) rc = upload_concat(ctx, gu, 2, L.gu);
         if (!rc) rc = upload_concat(ctx, dn, 1, L.down);
@@ -949,10 +984,52 @@ int fl_reset(fl_ctx *ctx) {
 }
 
 // Enqueue one decode step (kernels only; no host synchronisation).
+// Attention of layer l over the head-major cache [kv_head][slot][head_dim]
+// (q from the fused QKV output, RoPE already applied by its epilogue).
+static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
+    const fl_model_config &c = ctx->cfg;
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+    AttnArgs a{};
+    a.q = ctx->qkv;
+    a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
+    a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
+    a.tok_stride = c.head_dim;
+    a.head_stride = (long long)c.max_seq_len * c.head_dim;
+    a.posp = &ctx->st->pos;
+    a.nkv = c.num_kv_heads;
+    a.nsplit = ctx->nsplit;
+    a.chmin = ctx->chmin;
+    a.part = ctx->d_part;
+    a.counters = ctx->d_counters;
+    a.out = nullptr;  // the wo matvec reads the Q8_0 copy only
+    a.oq = ctx->aq;
+    a.os = ctx->as;
+    a.osum = ctx->asum;
+    return a;
+}
+
+// EPI_QKV arguments of layer l: RoPE at the live position, K/V rows into
+// this layer's cache slot.
+static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
+    const fl_model_config &c = ctx->cfg;
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+    QkvEpi e{};
+    e.rope = ctx->rope;
+    e.sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
+    e.posp = &ctx->st->pos;
+    e.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
+    e.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
+    e.head_stride = (long long)c.max_seq_len * c.head_dim;
+    e.nq = c.num_heads * c.head_dim;
+    e.nk = c.num_kv_heads * c.head_dim;
+    e.hd = c.head_dim;
+    e.kv_f16 = ctx->kv_format == FL_KV_F16;
+    return e;
+}
+
 static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     const fl_model_config &c = ctx->cfg;
-    const int H = c.hidden_dim, hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads;
-    const int qd = nh * hd, kvd = nkv * hd, G = nh / nkv;
+    const int hd = c.head_dim, G = c.num_heads / c.num_kv_heads;
     const float eps = c.rms_norm_eps;
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
     switch (ctx->embed.format) {
@@ -962,33 +1039,13 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
     }
     HIPCHK(ctx, hipGetLastError());
-    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
     for (int l = 0; l < c.num_layers; l++) {
         Layer &L = ctx->layers[l];
-        int rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
-                             ctx->qkv, nullptr);
+        const QkvEpi qe = layer_qkv_epi(ctx, l);
+        int rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
+                             ctx->qkv, nullptr, &qe);
         if (rc) return rc;
-        AttnArgs a{};
-        a.q = ctx->qkv;
-        a.knew = ctx->qkv + qd;
-        a.vnew = ctx->qkv + qd + kvd;
-        a.rope = ctx->rope;
-        a.sin_off = (long long)c.max_seq_len * (hd / 2);
-        a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
-        a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
-        a.posp = &ctx->st->pos;
-        a.tok_stride = hd;  // head-major cache: [kv_head][slot][head_dim]
-        a.head_stride = (long long)c.max_seq_len * hd;
-        a.nkv = nkv;
-        a.nsplit = ctx->nsplit;
-        a.chmax = ctx->chmax;
-        a.chmin = ctx->chmin;
-        a.part = ctx->d_part;
-        a.counters = ctx->d_counters;
-        a.out = ctx->attn;
-        a.oq = ctx->aq;
-        a.os = ctx->as;
-        a.osum = ctx->asum;
+        AttnArgs a = layer_attn_args(ctx, l);
         rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
         if (rc) return rc;
         rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
@@ -1159,7 +1216,7 @@ int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out) {
 
 // Launch `iters` copies of one layer kernel on the context stream, cycling
 // through the layers.
-int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_launch) {
+int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, double *bytes_per_launch) {
     if (!ctx || !ctx->have_weights) return fail(ctx, FL_E_STATE, "no model");
     const fl_model_config &c = ctx->cfg;
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
@@ -1167,10 +1224,19 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_l
     for (int i = 0; i < iters; i++) {
         // cycle through the layers so repeated launches stream distinct
         // weights from HBM instead of re-reading a cache-resident matrix
-        Layer &L = ctx->layers[i % c.num_layers];
+        const int li = (first_layer + i) % c.num_layers;
+        Layer &L = ctx->layers[li];
         int rc = 0;
         switch (which) {
-        case 0: w = &L.qkv; rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_STORE, ctx->x, L.attn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->bench_out, nullptr); break;
+        case 0: {
+            // writes q to the bench buffer and K/V into the cache slot of the
+            // current position (the next decode step rewrites that slot)
+            w = &L.qkv;
+            const QkvEpi qe = layer_qkv_epi(ctx, li);
+            rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, c.rms_norm_eps, nullptr, nullptr,
+                             nullptr, ctx->bench_out, nullptr, &qe);
+            break;
+        }
         case 1: w = &L.wo; rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->bench_out, nullptr); break;
         case 2: w = &L.gu; rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, c.rms_norm_eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs, ctx->hsum, nullptr); break;
         case 3: w = &L.down; rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_STORE, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->bench_out, nullptr); break;
@@ -1182,37 +1248,10 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_l
             else rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, ctx->x, ctx->out_norm, c.rms_norm_eps, nullptr, ctx->d_slot);
             break;
         }
-        case 5: {  // attention of layer i % L at the current position
-            const int hd = c.head_dim, nkv = c.num_kv_heads, qd = c.num_heads * hd, kvd = nkv * hd;
-            const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
-            const int l = i % c.num_layers;
-            AttnArgs a{};
-            a.q = ctx->qkv;
-            a.knew = ctx->qkv + qd;
-            a.vnew = ctx->qkv + qd + kvd;
-            a.rope = ctx->rope;
-            a.sin_off = (long long)c.max_seq_len * (hd / 2);
-            a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
-            a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
-            a.posp = &ctx->st->pos;
-            a.tok_stride = hd;
-            a.head_stride = (long long)c.max_seq_len * hd;
-        a.tok_stride = hd;  // head-major cache: [kv_head][slot][head_dim]
-        a.head_stride = (long long)c.max_seq_len * hd;
-            a.nkv = nkv;
-            a.nsplit = ctx->nsplit;
-            a.chmax = ctx->chmax;
-            a.chmin = ctx->chmin;
-        a.chmin = ctx->chmin;
-            a.part = ctx->d_part;
-            a.counters = ctx->d_counters;
-            a.out = ctx->attn;
-            a.oq = ctx->aq;
-            a.os = ctx->as;
-            a.osum = ctx->asum;
-            a.skip_merge = getenv("FLARE_ATTN_SKIP_MERGE") != nullptr;
+        case 5: {  // attention of layer li at the current position
+            AttnArgs a = layer_attn_args(ctx, li);
             a.trace = ctx->bench_trace;
-            rc = launch_attention(ctx, ctx->kv_format, hd, c.num_heads / nkv, a);
+            rc = launch_attention(ctx, ctx->kv_format, c.head_dim, c.num_heads / c.num_kv_heads, a);
             break;
         }
         default: return fail(ctx, FL_E_INVALID, "which=%d", which);
@@ -1232,9 +1271,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_l
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
         HIPCHK(ctx, hipMemcpy(tr, ctx->bench_trace, sizeof tr, hipMemcpyDeviceToHost));
         fprintf(stderr, "attn trace (10ns ticks from start):");
-        for (int i = 1; i < 9; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
-        fprintf(stderr, " | batch0:");
-        for (int i = 10; i < 18; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        for (int i = 1; i < 10; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
         fprintf(stderr, "\n");
     }
     if (bytes_per_launch && which == 5) {

@@ -22,13 +22,20 @@ constexpr int kThreads = 256;  // 4 wave64 per workgroup
 
 enum Fmt { F_F32 = 0, F_Q8_0 = 1, F_Q4K = 2, F_Q6K = 3 };
 
+// Native 16-/8-byte vectors.  HIP's int4/float4 are structs whose copies
+// lower to memcpy through a private alloca (scratch memory); these stay in
+// registers.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+
 // ------------------------------------------------------------------------
 // small helpers
 // ------------------------------------------------------------------------
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half(f)); }
 
-__device__ __forceinline__ int dot16(const int4 &a, const int4 &b, int c) {
+__device__ __forceinline__ int dot16(const v4i_t &a, const v4i_t &b, int c) {
     c = __builtin_amdgcn_sdot4(a.x, b.x, c, false);
     c = __builtin_amdgcn_sdot4(a.y, b.y, c, false);
     c = __builtin_amdgcn_sdot4(a.z, b.z, c, false);
@@ -128,9 +135,9 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *q, float *
         }
         packed[j] = (int)p;
     }
-    int4 *qd = (int4 *)q;
-    qd[0] = make_int4(packed[0], packed[1], packed[2], packed[3]);
-    qd[1] = make_int4(packed[4], packed[5], packed[6], packed[7]);
+    v4i_t *qd = (v4i_t *)q;
+    qd[0] = v4i_t{packed[0], packed[1], packed[2], packed[3]};
+    qd[1] = v4i_t{packed[4], packed[5], packed[6], packed[7]};
     *s = d;
     *sum = acc;
 }
@@ -177,8 +184,8 @@ __device__ __forceinline__ void stage_q8(const float *x, const float *w, float e
                                          int8_t *lq, float *ls, int *lsum, float *red) {
     const int nb = n >> 5;
     if (PRO == PRO_LOADQ) {
-        const int4 *src = (const int4 *)gq;
-        int4 *dst = (int4 *)lq;
+        const v4i_t *src = (const v4i_t *)gq;
+        v4i_t *dst = (v4i_t *)lq;
         for (int i = threadIdx.x; i < (n >> 4); i += blockDim.x) dst[i] = src[i];
         for (int i = threadIdx.x; i < nb; i += blockDim.x) {
             ls[i] = gs[i];
@@ -188,10 +195,10 @@ __device__ __forceinline__ void stage_q8(const float *x, const float *w, float e
         const float inv = wg_inv_rms(x, n, eps, red);
         for (int b = threadIdx.x; b < nb; b += blockDim.x) {
             float v[32];
-            const float4 *xs = (const float4 *)(x + b * 32), *ws = (const float4 *)(w + b * 32);
+            const v4f_t *xs = (const v4f_t *)(x + b * 32), *ws = (const v4f_t *)(w + b * 32);
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                float4 a = xs[j], c = ws[j];
+                v4f_t a = xs[j], c = ws[j];
                 if (PRO == PRO_NORMQ0) {
                     v[4 * j + 0] = a.x * c.x * inv; v[4 * j + 1] = a.y * c.y * inv;
                     v[4 * j + 2] = a.z * c.z * inv; v[4 * j + 3] = a.w * c.w * inv;
@@ -215,16 +222,8 @@ struct WDesc {
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
 // 16-byte streaming loads (weights are read once per token: non-temporal hint)
-typedef int v4i_t __attribute__((ext_vector_type(4)));
-typedef float v4f_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ int4 ld_stream(const void *p) {
-    const v4i_t v = __builtin_nontemporal_load((const v4i_t *)p);
-    return make_int4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ float4 ld_stream_f(const void *p) {
-    const v4f_t v = __builtin_nontemporal_load((const v4f_t *)p);
-    return make_float4(v.x, v.y, v.z, v.w);
-}
+__device__ __forceinline__ v4i_t ld_stream(const void *p) { return __builtin_nontemporal_load((const v4i_t *)p); }
+__device__ __forceinline__ v4f_t ld_stream_f(const void *p) { return __builtin_nontemporal_load((const v4f_t *)p); }
 
 // Packed (value, index) key whose unsigned max is the first maximum:
 // order-preserving float bits in the high word, ~index in the low word.

@@ -61,6 +61,16 @@ inline MvPlan mv_plan(int fmt, int rows, int cols, bool f32in) {
     return p;
 }
 
+// Same plan with an even row count per tile (EPI_QKV stores row pairs).
+inline MvPlan mv_plan_even(MvPlan p, int fmt, int rows, int cols) {
+    if (p.r % 2 == 0) return p;
+    p.r = 2;
+    const int upr = units_per_row(fmt, cols), groups = kThreads / p.lpr;
+    const int nchunk = (upr + p.lpr * p.u - 1) / (p.lpr * p.u);
+    p.grid = std::max(1, std::min(((rows + 1) / 2 * nchunk + groups - 1) / groups, 1024));
+    return p;
+}
+
 struct GuPlan {
     int lpr = 64, u = 1, grid = 1;
     size_t lds = 0;
@@ -78,16 +88,14 @@ inline GuPlan gu_plan(int fmt, int cols, int F) {
     return p;
 }
 
-// Split count for a cache of up to max_seq slots.  The kernel covers the
-// context in chunks of max(chmin, ceil(T / nsplit)) tokens (chmin = one
-// batch), so each workgroup streams at most a few batches and ~T/chmin
-// workgroups per kv head run in parallel (at most 256 splits).
-inline void choose_splits(int max_seq, int nkv, int head_dim, int &nsplit, int &chmax) {
-    const int chmin = attn_chmin(head_dim);
+// Split count for a cache of up to max_seq slots (fixed for the captured
+// decode graph; the kernel derives the chunk from the live position).  A
+// chunk is max(chmin, ceil(T / nsplit)) tokens rounded up to one pass, so
+// about 256 workgroups run once the context is long enough.
+inline void choose_splits(int max_seq, int nkv, int head_dim, int &nsplit, int &chmin) {
+    chmin = attn_round(head_dim) / 2;  // 64 tokens: half a round of loads per thread
     const int cover = (max_seq + chmin - 1) / chmin;
-    nsplit = std::max(1, std::min(cover, 256));
-    chmax = std::max(chmin, (max_seq + nsplit - 1) / nsplit);
-    (void)nkv;
+    nsplit = std::max(1, std::min({cover, std::max(1, 256 / std::max(1, nkv)), kAttnMaxSplit}));
 }
 
 inline bool attn_supported(int D, int G) {

@@ -19,7 +19,23 @@
 
 namespace fl {
 
-enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_ARGMAX = 2 };
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_ARGMAX = 2, EPI_QKV = 3 };
+
+// EPI_QKV: the fused QKV matvec stores q (after RoPE) and writes the new
+// token's K (after RoPE) and V straight into the KV cache.  The weight rows
+// of every q / k head are uploaded pair-interleaved (row 2i = original row i,
+// row 2i+1 = original row i + D/2), so each rotate-half pair of
+// apply_rope_with_table (model.rs:7283-7296) lands in one tile.
+struct QkvEpi {
+    const float *rope;  // cos table [max_pos][D/2]; sin table at rope + sin_off
+    long long sin_off;
+    const int *posp;    // token position (device)
+    void *kc, *vc;      // this layer's head-major cache [kv_head][slot][D]
+    long long head_stride;  // elements between kv heads (max_seq * D)
+    int nq, nk;         // q rows (Nq*D) and k rows (Nkv*D); v rows follow
+    int hd;             // head_dim
+    int kv_f16;         // cache element: 1 = binary16 (RNE), 0 = f32
+};
 
 struct Q8inArgs {
     WDesc W;
@@ -31,6 +47,7 @@ struct Q8inArgs {
     const int *gsum;
     float *out;
     unsigned long long *slot;  // EPI_ARGMAX
+    QkvEpi qkv;                // EPI_QKV
 };
 
 struct F32Args {
@@ -77,38 +94,34 @@ struct GuArgs {
 // ---------------------------------------------------------------------------
 template <int NT>
 struct StageQ8 {
-    int4 qv[4];  // PRO_LOADQ: int8 quants (16 B each), scales, sums
+    v4i_t qv[4];  // PRO_LOADQ: int8 quants (16 B each), scales, sums
     float sv[2];
     int sumv[2];
-    float4 xv[4], wv[4];  // PRO_NORMQ*: x and norm weight
+    v4f_t xv[4], wv[4];  // PRO_NORMQ*: x and norm weight
 
+    // Loads are unconditional (indices clamped into range) so that they stay
+    // in registers and in flight; finish() discards the clamped duplicates.
     __device__ __forceinline__ void issue(int pro, int n, const float *x, const float *w, const int8_t *gq,
                                           const float *gs, const int *gsum) {
         const int t = threadIdx.x;
         if (pro == PRO_LOADQ) {
             const int n16 = n >> 4, nb = n >> 5;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = t + k * NT;
-                if (i < n16) qv[k] = ((const int4 *)gq)[i];
-            }
+            for (int k = 0; k < 4; k++) qv[k] = ((const v4i_t *)gq)[min(t + k * NT, n16 - 1)];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
-                const int j = t + k * NT;
-                if (j < nb) {
-                    sv[k] = gs[j];
-                    sumv[k] = gsum[j];
-                }
+                const int j = min(t + k * NT, nb - 1);
+                sv[k] = gs[j];
+                sumv[k] = gsum[j];
             }
         } else {
             const int E = n / NT;
             if (n == NT * E && (E == 8 || E == 16)) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    if (k * 4 < E) {
-                        xv[k] = ((const float4 *)(x + t * E))[k];
-                        wv[k] = ((const float4 *)(w + t * E))[k];
-                    }
+                    const int o = min(t * E + 4 * k, n - 4);
+                    xv[k] = *(const v4f_t *)(x + o);
+                    wv[k] = *(const v4f_t *)(w + o);
                 }
             }
         }
@@ -122,7 +135,7 @@ struct StageQ8 {
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const int i = t + k * NT;
-                if (i < n16) ((int4 *)lq)[i] = qv[k];
+                if (i < n16) ((v4i_t *)lq)[i] = qv[k];
             }
 #pragma unroll
             for (int k = 0; k < 2; k++) {
@@ -183,7 +196,7 @@ struct StageQ8 {
             }
         }
         if (E == 8) {
-            ((int2 *)lq)[t] = make_int2((int)packed[0], (int)packed[1]);
+            ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
             qsum += __shfl_xor(qsum, 1, 64);
             qsum += __shfl_xor(qsum, 2, 64);
             if ((t & 3) == 0) {
@@ -191,7 +204,7 @@ struct StageQ8 {
                 lsum[t >> 2] = qsum;
             }
         } else {
-            ((int4 *)lq)[t] = make_int4((int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]);
+            ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
             qsum += __shfl_xor(qsum, 1, 64);
             if ((t & 1) == 0) {
                 ls[t >> 1] = d;
@@ -205,16 +218,15 @@ struct StageQ8 {
 // f32 input staging (logits path): pro 0 copies x, pro 1 is rmsnorm_into.
 template <int NT>
 struct StageF32 {
-    float4 xv[4], wv[4];
+    v4f_t xv[4], wv[4];
     __device__ __forceinline__ void issue(int pro, int n, const float *x, const float *w) {
         const int t = threadIdx.x, E = n / NT;
         if (n == NT * E && (E == 8 || E == 16)) {
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                if (k * 4 < E) {
-                    xv[k] = ((const float4 *)(x + t * E))[k];
-                    if (pro == 1) wv[k] = ((const float4 *)(w + t * E))[k];
-                }
+                const int o = min(t * E + 4 * k, n - 4);
+                xv[k] = *(const v4f_t *)(x + o);
+                wv[k] = *(const v4f_t *)((pro == 1 ? w : x) + o);  // w may be null for pro 0
             }
         }
     }
@@ -265,7 +277,7 @@ struct Tile;
 // Q8_0 (re-laid-out): unit = one 32-block; int8 quants [rows][K] + f16 scales.
 template <int LPR, int U, int R>
 struct Tile<F_Q8_0, LPR, U, R> {
-    int4 w0[U][R], w1[U][R];
+    v4i_t w0[U][R], w1[U][R];
     uint16_t sc[U][R];
     __device__ __forceinline__ void load(const WDesc &W, const int *rix, int ubase) {
         const int bpr = W.cols >> 5;
@@ -274,7 +286,7 @@ struct Tile<F_Q8_0, LPR, U, R> {
             const int b = min(ubase + u * LPR, bpr - 1);
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const int4 *p = (const int4 *)(W.q + (size_t)rix[r] * W.cols + b * 32);
+                const v4i_t *p = (const v4i_t *)(W.q + (size_t)rix[r] * W.cols + b * 32);
                 w0[u][r] = ld_stream(p);
                 w1[u][r] = ld_stream(p + 1);
                 sc[u][r] = W.s[(size_t)rix[r] * bpr + b];
@@ -292,7 +304,7 @@ __device__ __forceinline__ void tile_dot_q8(const Tile<F_Q8_0, LPR, U, R> &T, co
     for (int u = 0; u < U; u++) {
         const bool valid = ubase + u * LPR < bpr;
         const int b = valid ? ubase + u * LPR : bpr - 1;
-        const int4 x0 = *(const int4 *)(lq + b * 32), x1 = *(const int4 *)(lq + b * 32 + 16);
+        const v4i_t x0 = *(const v4i_t *)(lq + b * 32), x1 = *(const v4i_t *)(lq + b * 32 + 16);
         const float xs = ls[b];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -312,27 +324,26 @@ __device__ __forceinline__ void tile_dot_f32(const Tile<F_Q8_0, LPR, U, R> &T, c
     for (int u = 0; u < U; u++) {
         const bool valid = ubase + u * LPR < bpr;
         const int b = valid ? ubase + u * LPR : bpr - 1;
-        float xv[32];
+        // dequant_q8_0_block: (q as f32) * scale (quantize.rs:194), then the
+        // f32 dot of matvec_argmax_f32; x is read from LDS one 16-B quarter
+        // at a time (keeps the live register set small)
+        float a[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) a[r] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float4 t = *(const float4 *)(lx + b * 32 + 4 * j);
-            xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
+            const v4f_t xq = *(const v4f_t *)(lx + b * 32 + 4 * j);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float scale = h2f(T.sc[u][r]);
+                const int wj = j < 4 ? T.w0[u][r][j] : T.w1[u][r][j - 4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) a[r] += ((float)(int8_t)(wj >> (8 * k)) * scale) * xq[k];
+            }
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float scale = h2f(T.sc[u][r]);
-            const int ws[8] = {T.w0[u][r].x, T.w0[u][r].y, T.w0[u][r].z, T.w0[u][r].w,
-                               T.w1[u][r].x, T.w1[u][r].y, T.w1[u][r].z, T.w1[u][r].w};
-            float a = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    // dequant_q8_0_block: (q as f32) * scale (quantize.rs:194)
-                    const float wv = (float)(int8_t)(ws[j] >> (8 * k)) * scale;
-                    a += wv * xv[4 * j + k];
-                }
-            acc[r] += valid ? a : 0.0f;
+            acc[r] += valid ? a[r] : 0.0f;
         }
     }
 }
@@ -341,7 +352,7 @@ __device__ __forceinline__ void tile_dot_f32(const Tile<F_Q8_0, LPR, U, R> &T, c
 // nibbles of sub-block `sub` and the high nibbles of sub-block `sub+4`.
 template <int LPR, int U, int R>
 struct Tile<F_Q4K, LPR, U, R> {
-    int4 hd[U][R], q0[U][R], q1[U][R];
+    v4i_t hd[U][R], q0[U][R], q1[U][R];
     __device__ __forceinline__ void load(const WDesc &W, const int *rix, int ubase) {
         const int nsb = W.cols >> 8, units = nsb * 4;
         const size_t rstride = (size_t)nsb * 144;
@@ -371,8 +382,8 @@ __device__ __forceinline__ void tile_dot_q8(const Tile<F_Q4K, LPR, U, R> &T, con
         const int uu = valid ? ubase + u * LPR : units - 1;
         const int sb = uu >> 2, sub = uu & 3;
         const int blo = sb * 8 + sub, bhi = blo + 4;
-        const int4 xl0 = *(const int4 *)(lq + blo * 32), xl1 = *(const int4 *)(lq + blo * 32 + 16);
-        const int4 xh0 = *(const int4 *)(lq + bhi * 32), xh1 = *(const int4 *)(lq + bhi * 32 + 16);
+        const v4i_t xl0 = *(const v4i_t *)(lq + blo * 32), xl1 = *(const v4i_t *)(lq + blo * 32 + 16);
+        const v4i_t xh0 = *(const v4i_t *)(lq + bhi * 32), xh1 = *(const v4i_t *)(lq + bhi * 32 + 16);
         const float s_lo = ls[blo], s_hi = ls[bhi];
         const float qsum_lo = (float)lsum[blo], qsum_hi = (float)lsum[bhi];
 #pragma unroll
@@ -386,13 +397,13 @@ __device__ __forceinline__ void tile_dot_q8(const Tile<F_Q4K, LPR, U, R> &T, con
             const uint32_t sc_lo = s_a & 63, mn_lo = s_b & 63;
             const uint32_t sc_hi = (s_a >> 6) | ((s_c & 0xF) << 2);
             const uint32_t mn_hi = (s_b >> 6) | ((s_c >> 4) << 2);
-            const int4 a = T.q0[u][r], c = T.q1[u][r];
-            const int4 lo0 = make_int4(a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F);
-            const int4 lo1 = make_int4(c.x & 0x0F0F0F0F, c.y & 0x0F0F0F0F, c.z & 0x0F0F0F0F, c.w & 0x0F0F0F0F);
-            const int4 hi0 = make_int4((a.x >> 4) & 0x0F0F0F0F, (a.y >> 4) & 0x0F0F0F0F,
-                                       (a.z >> 4) & 0x0F0F0F0F, (a.w >> 4) & 0x0F0F0F0F);
-            const int4 hi1 = make_int4((c.x >> 4) & 0x0F0F0F0F, (c.y >> 4) & 0x0F0F0F0F,
-                                       (c.z >> 4) & 0x0F0F0F0F, (c.w >> 4) & 0x0F0F0F0F);
+            const v4i_t a = T.q0[u][r], c = T.q1[u][r];
+            const v4i_t lo0 = v4i_t{a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F};
+            const v4i_t lo1 = v4i_t{c.x & 0x0F0F0F0F, c.y & 0x0F0F0F0F, c.z & 0x0F0F0F0F, c.w & 0x0F0F0F0F};
+            const v4i_t hi0 = v4i_t{(a.x >> 4) & 0x0F0F0F0F, (a.y >> 4) & 0x0F0F0F0F,
+                                       (a.z >> 4) & 0x0F0F0F0F, (a.w >> 4) & 0x0F0F0F0F};
+            const v4i_t hi1 = v4i_t{(c.x >> 4) & 0x0F0F0F0F, (c.y >> 4) & 0x0F0F0F0F,
+                                       (c.z >> 4) & 0x0F0F0F0F, (c.w >> 4) & 0x0F0F0F0F};
             const int dl = dot16(lo1, xl1, dot16(lo0, xl0, 0));
             const int dh = dot16(hi1, xh1, dot16(hi0, xh0, 0));
             const float d_sc_lo = d * (float)sc_lo, dmin_mn_lo = dmin * (float)mn_lo;
@@ -409,7 +420,7 @@ __device__ __forceinline__ void tile_dot_q8(const Tile<F_Q4K, LPR, U, R> &T, con
 // l0 in {0,16}) -> 64 weights.
 template <int LPR, int U, int R>
 struct Tile<F_Q6K, LPR, U, R> {
-    int4 qa[U][R], qb[U][R], qh[U][R], scv[U][R];
+    v4i_t qa[U][R], qb[U][R], qh[U][R], scv[U][R];
     uint16_t dd[U][R];
     __device__ __forceinline__ void load(const WDesc &W, const int *rix, int ubase) {
         const int nsb = W.cols >> 8, units = nsb * 4;
@@ -423,7 +434,7 @@ struct Tile<F_Q6K, LPR, U, R> {
                 qa[u][r] = ld_stream(body + 64 * hf + l0);
                 qb[u][r] = ld_stream(body + 64 * hf + 32 + l0);
                 qh[u][r] = ld_stream(body + 128 + 32 * hf + l0);
-                scv[u][r] = *(const int4 *)(body + 192);
+                scv[u][r] = *(const v4i_t *)(body + 192);
                 dd[u][r] = W.s[(size_t)rix[r] * nsb + sb];
             }
         }
@@ -479,7 +490,7 @@ __device__ __forceinline__ void tile_dot_f32(const Tile<F_Q6K, LPR, U, R> &T, co
 // F32: unit = 4 floats.
 template <int LPR, int U, int R>
 struct Tile<F_F32, LPR, U, R> {
-    float4 wv[U][R];
+    v4f_t wv[U][R];
     __device__ __forceinline__ void load(const WDesc &W, const int *rix, int ubase) {
         const int units = W.cols >> 2;
         const float *wf = (const float *)W.q;
@@ -500,10 +511,10 @@ __device__ __forceinline__ void tile_dot_f32(const Tile<F_F32, LPR, U, R> &T, co
     for (int u = 0; u < U; u++) {
         const bool valid = ubase + u * LPR < units;
         const int uu = valid ? ubase + u * LPR : units - 1;
-        const float4 xv = *(const float4 *)(lx + 4 * uu);
+        const v4f_t xv = *(const v4f_t *)(lx + 4 * uu);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float4 w = T.wv[u][r];
+            const v4f_t w = T.wv[u][r];
             const float t = w.x * xv.x + w.y * xv.y + w.z * xv.z + w.w * xv.w;
             acc[r] += valid ? t : 0.0f;
         }
@@ -556,6 +567,55 @@ __device__ __forceinline__ void store_rows(const float *acc, int row0, int rows,
     }
 }
 
+// EPI_QKV store of a finished row group (R even, rows row0.. row0+R-1 in
+// the pair-interleaved order); lane gl < R/2 handles pair gl.
+template <int R>
+__device__ __forceinline__ void store_qkv(const float *acc, int row0, int rows, int gl, const QkvEpi &e, int pos,
+                                          float *q) {
+    static_assert(R % 2 == 0, "EPI_QKV needs row pairs");
+    if (gl >= R / 2) return;
+    const int n = row0 + 2 * gl;  // first row of the pair (even)
+    if (n >= rows) return;
+    float x0 = acc[0], x1 = acc[1];
+#pragma unroll
+    for (int r = 2; r < R; r += 2) {
+        x0 = (gl == r / 2) ? acc[r] : x0;
+        x1 = (gl == r / 2) ? acc[r + 1] : x1;
+    }
+    const int D = e.hd, half = D >> 1;
+    const int j = n % D, i = j >> 1;  // pair index within the head
+    if (n < e.nq + e.nk) {
+        const float c = e.rope[(size_t)pos * half + i], sn = e.rope[e.sin_off + (size_t)pos * half + i];
+        const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+        if (n < e.nq) {
+            const int h = n / D;
+            q[h * D + i] = y0;
+            q[h * D + i + half] = y1;
+        } else {
+            const int kvh = (n - e.nq) / D;
+            const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D;
+            if (e.kv_f16) {
+                ((uint16_t *)e.kc)[off + i] = f2h(y0);
+                ((uint16_t *)e.kc)[off + i + half] = f2h(y1);
+            } else {
+                ((float *)e.kc)[off + i] = y0;
+                ((float *)e.kc)[off + i + half] = y1;
+            }
+        }
+    } else {
+        // v rows keep their original order
+        const int vi = n - e.nq - e.nk, kvh = vi / D, d = vi % D;
+        const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D + d;
+        if (e.kv_f16) {
+            ((uint16_t *)e.vc)[off] = f2h(x0);
+            ((uint16_t *)e.vc)[off + 1] = f2h(x1);
+        } else {
+            ((float *)e.vc)[off] = x0;
+            ((float *)e.vc)[off + 1] = x1;
+        }
+    }
+}
+
 __host__ __device__ inline size_t q8_lds_bytes(int K) { return (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64; }
 
 // ---------------------------------------------------------------------------
@@ -590,6 +650,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 4))
         for (int r = 0; r < R; r++) rix[r] = min(rg * R + r, W.rows - 1);
     };
 
+    const int qpos = a.epi == EPI_QKV ? *a.qkv.posp : 0;
     StageQ8<kThreads> stg;
     stg.issue(a.pro, K, a.x, a.nw, a.gq, a.gs, a.gsum);  // 1. activation loads
     Tile<FMT, LPR, U, R> ta, tb;
@@ -610,7 +671,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 4))
 #pragma unroll
             for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
             if (a.epi == EPI_ARGMAX) best = umax64(best, rows_best<R>(acc, rgc * R, W.rows));
-            else store_rows<R>(acc, rgc * R, W.rows, gl, a.epi, a.out);
+            else if constexpr (R % 2 == 0) {
+                if (a.epi == EPI_QKV) store_qkv<R>(acc, rgc * R, W.rows, gl, a.qkv, qpos, a.out);
+                else store_rows<R>(acc, rgc * R, W.rows, gl, a.epi, a.out);
+            } else store_rows<R>(acc, rgc * R, W.rows, gl, a.epi, a.out);
 #pragma unroll
             for (int r = 0; r < R; r++) acc[r] = 0.0f;
         }

@@ -183,12 +183,13 @@ int fl_decode_continue(fl_ctx *ctx, int n_steps);
 int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out);
 
 /* ---- measurement helpers ---------------------------------------------------- */
-/* Enqueue `iters` launches of the layer matvec kernel for `which`
- * (0=qkv, 1=wo, 2=gate_up, 3=down, 4=output argmax) on the context stream,
- * launch i using layer i % num_layers, reading the model's live activation
- * buffers.  Writes the algorithmic weight bytes of one launch to
- * *bytes_per_launch. */
-int fl_bench_layer_kernel(fl_ctx *ctx, int which, int iters, double *bytes_per_launch);
+/* Enqueue `iters` launches of one decode kernel for `which` (0=qkv, 1=wo,
+ * 2=gate_up, 3=down, 4=output argmax, 5=attention at the current position)
+ * on the context stream, launch i using layer (first_layer + i) % num_layers,
+ * reading the model's live activation buffers.  Writes the algorithmic HBM
+ * bytes of one launch (GGUF weight bytes; K+V bytes for attention) to
+ * *bytes_per_launch.  No counterpart in the reference: measurement only. */
+int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, double *bytes_per_launch);
 /* Name of the device kernel fl_bench_layer_kernel launches for `which`. */
 const char *fl_bench_kernel_name(fl_ctx *ctx, int which);
 
