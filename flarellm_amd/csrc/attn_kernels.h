@@ -30,6 +30,8 @@ struct AttnArgs {
     long long *trace;    // FLARE_ATTN_TRACE builds: per-phase timestamps of workgroup (0,0)
 };
 
+
+
 #ifdef FLARE_ATTN_TRACE
 #define ATTN_TS(i)                                                                          \
     do {                                                                                    \

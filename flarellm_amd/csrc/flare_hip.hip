@@ -78,8 +78,8 @@ __global__ __launch_bounds__(kThreads) void k_block_dots(WDesc W, const int8_t *
         const int sub = (int)(i & 3);
         const long long rs = i >> 2;
         const int row = (int)(rs / nsb), sb = (int)(rs % nsb);
-        const uint8_t *blk = W.q + ((size_t)row * nsb + sb) * 144;
-        const v4i_t a = *(const v4i_t *)(blk + 16 + 32 * sub), c = *(const v4i_t *)(blk + 32 + 32 * sub);
+        const uint8_t *qs = W.q + ((size_t)row * nsb + sb) * 128;
+        const v4i_t a = *(const v4i_t *)(qs + 32 * sub), c = *(const v4i_t *)(qs + 16 + 32 * sub);
         const int blo = sb * 8 + sub, bhi = blo + 4;
         const v4i_t *xl = (const v4i_t *)(xq + blo * 32), *xh = (const v4i_t *)(xq + bhi * 32);
         const v4i_t lo0 = v4i_t{a.x & 0x0F0F0F0F, a.y & 0x0F0F0F0F, a.z & 0x0F0F0F0F, a.w & 0x0F0F0F0F};
@@ -106,41 +106,9 @@ __global__ __launch_bounds__(kThreads) void k_dequant(WDesc W, float *out) {
         const int8_t *q = (const int8_t *)W.q + (size_t)row * W.cols + j * 32;
         for (int k = 0; k < 32; k++) o[k] = (float)q[k] * scale;
     } else if (FMT == F_Q4K) {
-        const int sb = j >> 3, sblk = j & 7;
-        const uint8_t *blk = W.q + ((size_t)row * (W.cols >> 8) + sb) * 144;
-        const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
-        const uint8_t *s = blk + 4;
-        const int i = sblk & 3;
-        uint32_t sc, mn;
-        if (sblk < 4) {
-            sc = s[i] & 63;
-            mn = s[i + 4] & 63;
-        } else {
-            sc = (s[i] >> 6) | ((s[i + 8] & 0xF) << 2);
-            mn = (s[i + 4] >> 6) | ((s[i + 8] >> 4) << 2);
-        }
-        const uint8_t *qs = blk + 16 + 32 * i;
-        for (int k = 0; k < 32; k++) {
-            const float v = (float)(sblk < 4 ? (qs[k] & 0xF) : (qs[k] >> 4));
-            o[k] = d * (float)sc * v - dmin * (float)mn;
-        }
+        for (int k = 0; k < 32; k++) o[k] = q4k_elem(W, row, j * 32 + k);
     } else if (FMT == F_Q6K) {
-        const int nsb = W.cols >> 8, sb = j >> 3, e0 = (j & 7) * 32;
-        const uint8_t *body = W.q + ((size_t)row * nsb + sb) * 208;
-        const float d = h2f(W.s[(size_t)row * nsb + sb]);
-        for (int k = 0; k < 32; k++) {
-            const int e = e0 + k, hf = e >> 7, r = e & 127, grp = r >> 5, l = r & 31;
-            const uint8_t la = body[64 * hf + l], lb = body[64 * hf + 32 + l], hh = body[128 + 32 * hf + l];
-            int q;
-            switch (grp) {
-            case 0: q = (int)((la & 0xF) | ((hh & 3) << 4)) - 32; break;
-            case 1: q = (int)((lb & 0xF) | (((hh >> 2) & 3) << 4)) - 32; break;
-            case 2: q = (int)((la >> 4) | (((hh >> 4) & 3) << 4)) - 32; break;
-            default: q = (int)((lb >> 4) | (((hh >> 6) & 3) << 4)) - 32; break;
-            }
-            const float sc = (float)(int8_t)body[192 + hf * 8 + (l >> 4) + 2 * grp];
-            o[k] = d * sc * (float)q;
-        }
+        for (int k = 0; k < 32; k++) o[k] = q6k_elem(W, row, j * 32 + k);
     } else {
         const float *src = (const float *)W.q + (size_t)row * W.cols + j * 32;
         for (int k = 0; k < 32; k++) o[k] = src[k];
@@ -205,28 +173,9 @@ __global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *
         if (FMT == F_Q8_0) {
             v = (float)((const int8_t *)E.q)[(size_t)row * H + i] * h2f(E.s[(size_t)row * (H >> 5) + (i >> 5)]);
         } else if (FMT == F_Q6K) {
-            const int nsb = H >> 8, sb = i >> 8, e = i & 255, hf = e >> 7, r = e & 127, grp = r >> 5, l = r & 31;
-            const uint8_t *body = E.q + ((size_t)row * nsb + sb) * 208;
-            const uint8_t la = body[64 * hf + l], lb = body[64 * hf + 32 + l], hh = body[128 + 32 * hf + l];
-            int q;
-            switch (grp) {
-            case 0: q = (int)((la & 0xF) | ((hh & 3) << 4)) - 32; break;
-            case 1: q = (int)((lb & 0xF) | (((hh >> 2) & 3) << 4)) - 32; break;
-            case 2: q = (int)((la >> 4) | (((hh >> 4) & 3) << 4)) - 32; break;
-            default: q = (int)((lb >> 4) | (((hh >> 6) & 3) << 4)) - 32; break;
-            }
-            const float sc = (float)(int8_t)body[192 + hf * 8 + (l >> 4) + 2 * grp];
-            v = h2f(E.s[(size_t)row * nsb + sb]) * sc * (float)q;
+            v = q6k_elem(E, row, i);
         } else if (FMT == F_Q4K) {
-            const int nsb = H >> 8, sb = i >> 8, e = i & 255, sblk = e >> 5, k = e & 31, ii = sblk & 3;
-            const uint8_t *blk = E.q + ((size_t)row * nsb + sb) * 144;
-            const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
-            const uint8_t *s = blk + 4;
-            uint32_t sc, mn;
-            if (sblk < 4) { sc = s[ii] & 63; mn = s[ii + 4] & 63; }
-            else { sc = (s[ii] >> 6) | ((s[ii + 8] & 0xF) << 2); mn = (s[ii + 4] >> 6) | ((s[ii + 8] >> 4) << 2); }
-            const uint8_t qb = blk[16 + 32 * ii + k];
-            v = d * (float)sc * (float)(sblk < 4 ? (qb & 0xF) : (qb >> 4)) - dmin * (float)mn;
+            v = q4k_elem(E, row, i);
         } else {
             v = ((const float *)E.q)[(size_t)row * H + i];
         }
@@ -246,13 +195,18 @@ __global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *
 
 struct fl_weight {
     int format = 0, rows = 0, cols = 0;
-    void *q = nullptr;      // device
-    void *s = nullptr;      // device (Q8_0 / Q6_K)
+    void *q = nullptr;      // device planes (see WDesc)
+    void *s = nullptr;
+    void *h = nullptr;
+    void *h2 = nullptr;
+    size_t plane_bytes[4] = {0, 0, 0, 0};  // q, s, h, h2
     size_t gguf_bytes = 0;  // algorithmic bytes (GGUF size)
     WDesc desc() const {
         WDesc d;
         d.q = (const uint8_t *)q;
         d.s = (const uint16_t *)s;
+        d.h = (const uint8_t *)h;
+        d.h2 = (const uint8_t *)h2;
         d.rows = rows;
         d.cols = cols;
         return d;
@@ -336,9 +290,9 @@ static int dev_alloc(fl_ctx *ctx, void **p, size_t bytes) {
     } while (0)
 
 static void weight_release(fl_weight &w) {
-    if (w.q) (void)hipFree(w.q);
-    if (w.s) (void)hipFree(w.s);
-    w.q = w.s = nullptr;
+    for (void *p : {w.q, w.s, w.h, w.h2})
+        if (p) (void)hipFree(p);
+    w.q = w.s = w.h = w.h2 = nullptr;
 }
 
 static size_t row_bytes(int fmt, int cols) { return fl_format_row_bytes(fmt, (size_t)cols); }
@@ -409,39 +363,48 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws_in, int n, 
     out.cols = cols;
     out.gguf_bytes = row_bytes(fmt, cols) * (size_t)rows;
     const size_t R = (size_t)rows;
-    if (fmt == FL_Q4K || fmt == FL_F32) {
-        ALLOC(ctx, out.q, out.gguf_bytes);
-        size_t off = 0;
-        for (int i = 0; i < n; i++) {
-            const size_t b = row_bytes(fmt, cols) * (size_t)ws[i]->num_rows;
-            HIPCHK(ctx, hipMemcpy((uint8_t *)out.q + off, ws[i]->data, b, hipMemcpyHostToDevice));
-            off += b;
-        }
-        return 0;
+    // Split every GGUF block into per-field planes, each [rows][blocks][len]:
+    //   Q8_0 (34 B):  s = f16 scale [0,2), q = quants [2,34)
+    //   Q4_K (144 B): h = d, dmin, scales [0,16), q = qs [16,144)
+    //   Q6_K (210 B): q = ql [0,128), h = qh [128,192), h2 = scales [192,208), s = d [208,210)
+    //   F32:          q = the row
+    struct Seg {
+        void **plane;
+        int off, len;
+    };
+    std::vector<Seg> segs;
+    size_t nblk, bsz;
+    if (fmt == FL_Q8_0) {
+        nblk = (size_t)cols / 32, bsz = 34;
+        segs = {{&out.s, 0, 2}, {&out.q, 2, 32}};
+    } else if (fmt == FL_Q4K) {
+        nblk = (size_t)cols / 256, bsz = 144;
+        segs = {{&out.h, 0, 16}, {&out.q, 16, 128}};
+    } else if (fmt == FL_Q6K) {
+        nblk = (size_t)cols / 256, bsz = 210;
+        segs = {{&out.q, 0, 128}, {&out.h, 128, 64}, {&out.h2, 192, 16}, {&out.s, 208, 2}};
+    } else {
+        nblk = 1, bsz = (size_t)cols * 4;
+        segs = {{&out.q, 0, (int)bsz}};
     }
-    // Q8_0 -> int8 quants [rows][cols] + f16 scales [rows][cols/32];
-    // Q6_K -> 208-byte bodies [rows][nsb] + f16 d [rows][nsb].
-    const bool q8 = fmt == FL_Q8_0;
-    const size_t nblk = q8 ? (size_t)cols / 32 : (size_t)cols / 256;
-    const size_t body = q8 ? 32 : 208, bsz = q8 ? 34 : 210, doff = q8 ? 0 : 208, boff = q8 ? 2 : 0;
-    ALLOC(ctx, out.q, R * nblk * body);
-    ALLOC(ctx, out.s, R * nblk * 2);
-    std::vector<uint8_t> hq, hs;
+    for (const Seg &g : segs) {
+        ALLOC(ctx, *g.plane, R * nblk * (size_t)g.len);
+        const int pi = g.plane == &out.q ? 0 : (g.plane == &out.s ? 1 : (g.plane == &out.h ? 2 : 3));
+        out.plane_bytes[pi] = R * nblk * (size_t)g.len;
+    }
+    std::vector<uint8_t> host;
     size_t row_base = 0;
     for (int i = 0; i < n; i++) {
-        const size_t r = (size_t)ws[i]->num_rows;
-        hq.resize(r * nblk * body);
-        hs.resize(r * nblk * 2);
+        const size_t r = (size_t)ws[i]->num_rows, nb = r * nblk;
         const uint8_t *src = (const uint8_t *)ws[i]->data;
+        for (const Seg &g : segs) {
+            host.resize(nb * (size_t)g.len);
 #pragma omp parallel for schedule(static)
-        for (long long k = 0; k < (long long)(r * nblk); k++) {
-            const uint8_t *b = src + (size_t)k * bsz;
-            std::memcpy(&hq[(size_t)k * body], b + boff, body);
-            hs[(size_t)k * 2] = b[doff];
-            hs[(size_t)k * 2 + 1] = b[doff + 1];
+            for (long long k = 0; k < (long long)nb; k++)
+                std::memcpy(&host[(size_t)k * g.len], src + (size_t)k * bsz + g.off, (size_t)g.len);
+            HIPCHK(ctx, hipMemcpy((uint8_t *)*g.plane + row_base * nblk * g.len, host.data(), host.size(),
+                                  hipMemcpyHostToDevice));
         }
-        HIPCHK(ctx, hipMemcpy((uint8_t *)out.q + row_base * nblk * body, hq.data(), hq.size(), hipMemcpyHostToDevice));
-        HIPCHK(ctx, hipMemcpy((uint8_t *)out.s + row_base * nblk * 2, hs.data(), hs.size(), hipMemcpyHostToDevice));
         row_base += r;
     }
     return 0;
@@ -449,43 +412,64 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws_in, int n, 
 
 // ---- launches ---------------------------------------------------------------
 
-static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
-                       const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
-                       float *out, unsigned long long *slot, const QkvEpi *qe = nullptr) {
-    if (pro == PRO_LOADQ && w.cols > 4 * 16 * kThreads)
-        return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
-    MvPlan p = mv_plan(w.format, w.rows, w.cols, false);
-    Q8inArgs a{w.desc(), pro, epi, x, nw, eps, q, s, sums, out, slot, QkvEpi{}};
-    if (epi == EPI_QKV) {
-        if (!qe) return fail(ctx, FL_E_INVALID, "EPI_QKV without its arguments");
-        if (w.rows != qe->nq + 2 * qe->nk || qe->nq % qe->hd || qe->nk % qe->hd)
-            return fail(ctx, FL_E_INVALID, "fused QKV rows %d do not match the heads", w.rows);
-        a.qkv = *qe;
-        p = mv_plan_even(p, w.format, w.rows, w.cols);
-    }
-    hipError_t e;
-    if (w.format == FL_Q8_0) e = launch_mv_q8in_q8_0(p, ctx->stream, a);
-    else if (w.format == FL_Q4K) e = launch_mv_q8in_q4k(p, ctx->stream, a);
-    else return fail(ctx, FL_E_UNSUPPORTED, "no Q8-input matvec for format %d", w.format);
+static MvsArgs mvs_args(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x, const float *nw,
+                        float eps, const int8_t *q, const float *s, const int *sums, float *out,
+                        unsigned long long *slot) {
+    MvsArgs a{};
+    a.W = w.desc();
+    a.pro = pro;
+    a.epi = epi;
+    a.x = x;
+    a.nw = nw;
+    a.eps = eps;
+    a.gq = q;
+    a.gs = s;
+    a.gsum = sums;
+    a.out = out;
+    a.slot = slot;
+    a.trace = ctx->bench_trace;
+    return a;
+}
+
+static int mvs_result(fl_ctx *ctx, hipError_t e, const MvsPlan &p) {
     if (e == hipErrorNotSupported)
-        return fail(ctx, FL_E_UNSUPPORTED, "no kernel for plan lpr=%d r=%d u=%d", p.lpr, p.r, p.u);
+        return fail(ctx, FL_E_UNSUPPORTED, "no matvec kernel for plan r=%d su=%d", p.r, p.su);
     HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
 
+// Q8-input matvec (Q8_0 / Q4_K weights): prologue pro, epilogue epi.
+static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
+                       const float *nw, float eps, const int8_t *q, const float *s, const int *sums,
+                       float *out, unsigned long long *slot, const QkvEpi *qe = nullptr) {
+    if (pro == PRO_LOADQ && w.cols > 4 * 16 * kMvsThreads)
+        return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
+    const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, false);
+    MvsArgs a = mvs_args(ctx, w, pro, epi, x, nw, eps, q, s, sums, out, slot);
+    if (epi == EPI_QKV) {
+        if (!qe) return fail(ctx, FL_E_INVALID, "EPI_QKV without its arguments");
+        if (w.rows != qe->nq + 2 * qe->nk || qe->nq % qe->hd || qe->nk % qe->hd)
+            return fail(ctx, FL_E_INVALID, "fused QKV rows %d do not match the heads", w.rows);
+        a.qkv = *qe;  // every plan has an even R
+    }
+    hipError_t e;
+    if (w.format == FL_Q8_0) e = launch_mvs_q8_0(false, p, ctx->stream, a);
+    else if (w.format == FL_Q4K) e = launch_mvs_q4k(p, ctx->stream, a);
+    else return fail(ctx, FL_E_UNSUPPORTED, "no Q8-input matvec for format %d", w.format);
+    return mvs_result(ctx, e, p);
+}
+
+// f32-input matvec (Q8_0 / Q6_K / f32 weights): pro 0 copies x, 1 = rmsnorm_into.
 static int launch_f32in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                         const float *nw, float eps, float *out, unsigned long long *slot) {
-    if (w.format != FL_Q8_0 && w.format != FL_Q6K && w.format != FL_F32)
-        return fail(ctx, FL_E_UNSUPPORTED, "no f32-input matvec for format %d", w.format);
-    const MvPlan p = mv_plan(w.format, w.rows, w.cols, true);
-    F32Args a{w.desc(), pro, epi, x, nw, eps, out, slot};
-    const hipError_t e = launch_mv_f32in(w.format, p, ctx->stream, a);
-    if (e == hipErrorNotSupported)
-        return fail(ctx, FL_E_UNSUPPORTED, "no kernel for plan lpr=%d r=%d u=%d", p.lpr, p.r, p.u);
-    HIPCHK(ctx, e);
-    HIPCHK(ctx, hipGetLastError());
-    return 0;
+    const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, true);
+    const MvsArgs a = mvs_args(ctx, w, pro, epi, x, nw, eps, nullptr, nullptr, nullptr, out, slot);
+    hipError_t e;
+    if (w.format == FL_Q8_0) e = launch_mvs_q8_0(true, p, ctx->stream, a);
+    else if (w.format == FL_Q6K || w.format == FL_F32) e = launch_mvs_f32(w.format, p, ctx->stream, a);
+    else return fail(ctx, FL_E_UNSUPPORTED, "no f32-input matvec for format %d", w.format);
+    return mvs_result(ctx, e, p);
 }
 
 static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *x, const float *nw,
@@ -493,17 +477,20 @@ static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *
                          float *hs, int *hsum, float *hout) {
     const int F = w.rows / 2;
     if (w.rows % 2 || F % 32) return fail(ctx, FL_E_INVALID, "gate_up rows %d must be 2*32k", w.rows);
-    GuArgs a{w.desc(), F, pro, x, nw, eps, q, s, sums, hq, hs, hsum, hout, ctx->bench_trace};
-    const GuPlan p = gu_plan(w.format, w.cols, F);
-    if (p.u == 0) return fail(ctx, FL_E_UNSUPPORTED, "gate_up input of %d columns is too wide", w.cols);
+    if (pro == PRO_LOADQ && w.cols > 4 * 16 * 4 * 64)
+        return fail(ctx, FL_E_UNSUPPORTED, "gate_up input of %d columns is too wide", w.cols);
+    MvsArgs a = mvs_args(ctx, w, pro, EPI_STORE, x, nw, eps, q, s, sums, nullptr, nullptr);
+    a.F = F;
+    a.hq = hq;
+    a.hs = hs;
+    a.hsum = hsum;
+    a.hout = hout;
+    const MvsPlan p = mvs_gu_plan(w.format, F, w.cols);
     hipError_t e;
-    if (w.format == FL_Q8_0) e = launch_gateup_q8_0(p, ctx->stream, a);
-    else if (w.format == FL_Q4K) e = launch_gateup_q4k(p, ctx->stream, a);
+    if (w.format == FL_Q8_0) e = launch_mvs_gu_q8_0(p, ctx->stream, a);
+    else if (w.format == FL_Q4K) e = launch_mvs_gu_q4k(p, ctx->stream, a);
     else return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel for format %d", w.format);
-    if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "no gate_up kernel lpr=%d u=%d", p.lpr, p.u);
-    HIPCHK(ctx, e);
-    HIPCHK(ctx, hipGetLastError());
-    return 0;
+    return mvs_result(ctx, e, p);
 }
 
 static int launch_attention(fl_ctx *ctx, int kv_format, int D, int G, AttnArgs &a) {
@@ -859,7 +846,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->hsum, F / 32 * 4);
     ALLOC(ctx, ctx->logits, (size_t)c.vocab_size * 4);
     ALLOC(ctx, ctx->bench_out, std::max({(size_t)c.vocab_size, H, qd + 2 * kvd, 2 * F}) * 4);
-    ALLOC(ctx, ctx->bench_trace, 64 * 8);
+    ALLOC(ctx, ctx->bench_trace, (64 + 2048) * 8);
     ALLOC(ctx, ctx->st, sizeof(DevState));
     ALLOC(ctx, ctx->tokens, S * 4);
     HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
@@ -1258,13 +1245,27 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         }
         if (rc) return rc;
     }
-    if (which == 2 && getenv("FLARE_MV_TRACE_PRINT")) {
-        long long tr[8] = {0};
+    if (which <= 4 && getenv("FLARE_MV_TRACE_PRINT")) {
+        // workgroup 0 phases, then the spread of workgroup start / end times
+        std::vector<long long> tr(64 + 2048, 0);
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
-        HIPCHK(ctx, hipMemcpy(tr, ctx->bench_trace, sizeof tr, hipMemcpyDeviceToHost));
-        fprintf(stderr, "gate_up trace (10ns ticks from start):");
+        HIPCHK(ctx, hipMemcpy(tr.data(), ctx->bench_trace, tr.size() * 8, hipMemcpyDeviceToHost));
+        fprintf(stderr, "mv trace which=%d (10ns ticks from wg0 start):", which);
         for (int i = 1; i < 6; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        long long s0 = 0, s1 = 0, e0 = 0, e1 = 0;
+        int n = 0;
+        for (int b = 0; b < 1024; b++) {
+            const long long st = tr[64 + 2 * b], en = tr[65 + 2 * b];
+            if (!st || !en || en < st) continue;
+            if (!n || st < s0) s0 = st;
+            if (!n || st > s1) s1 = st;
+            if (!n || en < e0) e0 = en;
+            if (!n || en > e1) e1 = en;
+            n++;
+        }
+        if (n) fprintf(stderr, " | %d wgs: starts %lld..%lld ends %lld..%lld", n, s0 - tr[0], s1 - tr[0], e0 - tr[0], e1 - tr[0]);
         fprintf(stderr, "\n");
+        HIPCHK(ctx, hipMemset(ctx->bench_trace, 0, tr.size() * 8));
     }
     if (which == 5 && getenv("FLARE_ATTN_TRACE_PRINT")) {
         long long tr[24] = {0};
@@ -1288,11 +1289,11 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
 const char *fl_bench_kernel_name(fl_ctx *ctx, int which) {
     if (!ctx || !ctx->have_weights) return "";
     switch (which) {
-    case 0: return "k_mv_q8in";
-    case 1: return "k_mv_q8in";
-    case 2: return "k_gateup";
-    case 3: return "k_mv_q8in";
-    case 4: return ctx->tied || ctx->output.format == FL_Q6K ? "k_mv_f32in" : "k_mv_q8in";
+    case 0: return "k_mvs";
+    case 1: return "k_mvs";
+    case 2: return "k_mvs_gu";
+    case 3: return "k_mvs";
+    case 4: return "k_mvs";
     case 5: return "k_attn";
     }
     return "";

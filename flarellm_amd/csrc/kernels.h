@@ -192,32 +192,60 @@ __device__ __forceinline__ void stage_q8(const float *x, const float *w, float e
             lsum[i] = gsum[i];
         }
     } else {
+        // one element per lane; the 32 lanes of a half-wave form one block
+        // (blockDim and n are multiples of 32), quantized by the lane quantizer
         const float inv = wg_inv_rms(x, n, eps, red);
-        for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-            float v[32];
-            const v4f_t *xs = (const v4f_t *)(x + b * 32), *ws = (const v4f_t *)(w + b * 32);
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v4f_t a = xs[j], c = ws[j];
-                if (PRO == PRO_NORMQ0) {
-                    v[4 * j + 0] = a.x * c.x * inv; v[4 * j + 1] = a.y * c.y * inv;
-                    v[4 * j + 2] = a.z * c.z * inv; v[4 * j + 3] = a.w * c.w * inv;
-                } else {
-                    v[4 * j + 0] = (a.x * inv) * c.x; v[4 * j + 1] = (a.y * inv) * c.y;
-                    v[4 * j + 2] = (a.z * inv) * c.z; v[4 * j + 3] = (a.w * inv) * c.w;
-                }
-            }
-            quant_block32(v, lq + b * 32, ls + b, lsum + b);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float v = (PRO == PRO_NORMQ0) ? x[i] * w[i] * inv : (x[i] * inv) * w[i];
+            quant_block32_lanes(v, lq + (i & ~31), ls + (i >> 5), lsum + (i >> 5));
         }
     }
     __syncthreads();
 }
 
+// A weight matrix on the device, in per-format planes (see mvs_kernels.h).
 struct WDesc {
-    const uint8_t *q;   // Q8_0: int8 quants; Q4_K: raw blocks; Q6_K: 208-B bodies; F32: floats
+    const uint8_t *q;   // Q8_0: int8 quants; Q4_K: qs nibbles; Q6_K: ql; F32: floats
     const uint16_t *s;  // Q8_0: f16 block scales; Q6_K: f16 super-block d
+    const uint8_t *h;   // Q4_K: 16-B headers (d, dmin, scales); Q6_K: qh
+    const uint8_t *h2;  // Q6_K: int8 sub-block scales
     int rows, cols;
 };
+
+// Element i of row `row` of a Q4_K / Q6_K weight (dequant_q4k_block /
+// dequant_q6k_block, flare-loader/src/quantize.rs:343-423).
+__device__ __forceinline__ float q4k_elem(const WDesc &W, int row, int i) {
+    const int nsb = W.cols >> 8, sb = i >> 8, e = i & 255, sblk = e >> 5, k = e & 31, ii = sblk & 3;
+    const size_t rs = (size_t)row * nsb + sb;
+    const uint8_t *hd = W.h + rs * 16;
+    const float d = h2f((uint16_t)(hd[0] | (hd[1] << 8))), dmin = h2f((uint16_t)(hd[2] | (hd[3] << 8)));
+    const uint8_t *s = hd + 4;
+    uint32_t sc, mn;
+    if (sblk < 4) {
+        sc = s[ii] & 63;
+        mn = s[ii + 4] & 63;
+    } else {
+        sc = (s[ii] >> 6) | ((s[ii + 8] & 0xF) << 2);
+        mn = (s[ii + 4] >> 6) | ((s[ii + 8] >> 4) << 2);
+    }
+    const uint8_t qb = W.q[rs * 128 + 32 * ii + k];
+    return d * (float)sc * (float)(sblk < 4 ? (qb & 0xF) : (qb >> 4)) - dmin * (float)mn;
+}
+__device__ __forceinline__ float q6k_elem(const WDesc &W, int row, int i) {
+    const int nsb = W.cols >> 8, sb = i >> 8, e = i & 255, hf = e >> 7, r = e & 127, grp = r >> 5, l = r & 31;
+    const size_t rs = (size_t)row * nsb + sb;
+    const uint8_t *ql = W.q + rs * 128 + 64 * hf, *qh = W.h + rs * 64 + 32 * hf;
+    const uint8_t la = ql[l], lb = ql[32 + l], hh = qh[l];
+    int q;
+    switch (grp) {
+    case 0: q = (int)((la & 0xF) | ((hh & 3) << 4)) - 32; break;
+    case 1: q = (int)((lb & 0xF) | (((hh >> 2) & 3) << 4)) - 32; break;
+    case 2: q = (int)((la >> 4) | (((hh >> 4) & 3) << 4)) - 32; break;
+    default: q = (int)((lb >> 4) | (((hh >> 6) & 3) << 4)) - 32; break;
+    }
+    const float sc = (float)(int8_t)W.h2[rs * 16 + hf * 8 + (l >> 4) + 2 * grp];
+    return h2f(W.s[rs]) * sc * (float)q;
+}
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 

@@ -1,0 +1,468 @@
+// Streaming quantized matvecs (gfx950).
+//
+// Every weight row is read as contiguous 16-byte pieces: lane l of a wave
+// loads bytes [16l, 16l+16) of a 1 KiB step of the row, so one load
+// instruction covers 1 KiB of one row.  Per-block integer dots that span two
+// lanes (a 32-value block = 2 pieces) are completed with a DPP lane-pair add,
+// which is exact, so every per-block term is formed from the same integers
+// as the reference.
+//
+// Weight planes on the device (uploaded once, see flare_hip.hip):
+//   Q8_0  q = int8 quants [rows][K]        s = f16 block scales [rows][K/32]
+//   Q4_K  q = qs nibbles [rows][nsb][128]  h = 16-B headers (d, dmin, scales[12]) [rows][nsb]
+//   Q6_K  q = ql [rows][nsb][128]          h = qh [rows][nsb][64]
+//         h2 = int8 scales [rows][nsb][16] s = f16 d [rows][nsb]
+//   F32   q = floats [rows][K]
+//
+// Kernels:
+//   k_mvs      one wave per row group of R rows; the persistent waves walk
+//              (row group, round of SU steps) units with the next unit's
+//              pieces in flight (ping-pong tiles).  Epilogues: store, residual
+//              add, fused QKV (RoPE + KV store), first-max argmax.
+//   k_mvs_gu   fused gate/up: a workgroup owns 32-hidden-unit blocks; SiLU*up
+//              and the Q8_0 quantization of the block are its epilogue.
+#pragma once
+
+#include "mv_kernels.h"
+
+namespace fl {
+
+// The four int8 of a word as exact floats: bias to unsigned (xor 0x80),
+// convert each byte in place (v_cvt_f32_ubyte0..3), subtract 128.
+__device__ __forceinline__ void i8x4_to_f32(int w, float *q) {
+    const uint32_t u = (uint32_t)w ^ 0x80808080u;
+    q[0] = (float)(u & 0xFFu) - 128.0f;
+    q[1] = (float)((u >> 8) & 0xFFu) - 128.0f;
+    q[2] = (float)((u >> 16) & 0xFFu) - 128.0f;
+    q[3] = (float)(u >> 24) - 128.0f;
+}
+
+#ifndef FLARE_NO_STAGE_BARRIER
+#define FLARE_STAGE_BARRIER() __builtin_amdgcn_sched_barrier(0)
+#else
+#define FLARE_STAGE_BARRIER() \
+    do {                      \
+    } while (0)
+#endif
+
+// lanes l and l^1 exchange a value (quad_perm [1,0,3,2])
+__device__ __forceinline__ int xpair(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+
+// bytes of one row in the streamed plane
+__host__ __device__ inline int mvs_span(int fmt, int K) {
+    return fmt == F_Q8_0 ? K : (fmt == F_F32 ? 4 * K : K / 2);
+}
+__host__ __device__ inline int mvs_steps(int fmt, int K) { return (mvs_span(fmt, K) + 1023) >> 10; }
+
+// ---------------------------------------------------------------------------
+// pieces: the 16 B (plus side data) of one lane for one (row, step)
+// ---------------------------------------------------------------------------
+template <int FMT>
+struct Pc;
+
+template <>
+struct Pc<F_Q8_0> {
+    v4i_t q;
+    uint32_t sc;
+    __device__ __forceinline__ void load(const WDesc &W, int row, int step, int lane) {
+        const int K = W.cols;
+        const int off = min(step * 1024 + 16 * lane, K - 16);
+        q = ld_stream(W.q + (size_t)row * K + off);
+        sc = W.s[(size_t)row * (K >> 5) + (off >> 5)];
+    }
+};
+
+template <>
+struct Pc<F_Q4K> {
+    v4i_t q, h;
+    __device__ __forceinline__ void load(const WDesc &W, int row, int step, int lane) {
+        const int nsb = W.cols >> 8, span = nsb * 128;
+        const int off = min(step * 1024 + 16 * lane, span - 16);
+        q = ld_stream(W.q + (size_t)row * span + off);
+        h = *(const v4i_t *)(W.h + ((size_t)row * nsb + (off >> 7)) * 16);  // 8 lanes share it
+    }
+};
+
+template <>
+struct Pc<F_Q6K> {
+    v4i_t ql, qh;
+    uint32_t sc;  // scale of the low-nibble weights | high-nibble weights << 8
+    uint32_t d;
+    __device__ __forceinline__ void load(const WDesc &W, int row, int step, int lane) {
+        const int nsb = W.cols >> 8, span = nsb * 128;
+        const int off = min(step * 1024 + 16 * lane, span - 16);
+        const int sb = off >> 7, o = off & 127, hf = o >> 6, q = (o >> 4) & 3;
+        const size_t rs = (size_t)row * nsb + sb;
+        ql = ld_stream(W.q + (size_t)row * span + off);
+        qh = *(const v4i_t *)(W.h + rs * 64 + hf * 32 + (q & 1) * 16);  // 2 lanes share it
+        const int si = hf * 8 + (q & 1) + 2 * (q >> 1);
+        const uint8_t *scp = W.h2 + rs * 16;
+        sc = (uint32_t)scp[si] | ((uint32_t)scp[si + 4] << 8);
+        d = W.s[rs];
+    }
+};
+
+template <>
+struct Pc<F_F32> {
+    v4f_t w;
+    __device__ __forceinline__ void load(const WDesc &W, int row, int step, int lane) {
+        const int K = W.cols;
+        const int off = min(step * 1024 + 16 * lane, 4 * K - 16);
+        w = ld_stream_f(W.q + (size_t)row * K * 4 + off);
+    }
+};
+
+// ---- Q8 input (int8 activations in LDS) -----------------------------------
+// matvec_q8_0_preq_into per-block term (model.rs:8082-8099):
+// (f16(w_scale) * x_scale) * (int dot as f32), counted once (even lane).
+__device__ __forceinline__ float pc_dot_q8(const Pc<F_Q8_0> &P, const WDesc &W, const int8_t *lq, const float *ls,
+                                           const int *, int step, int lane) {
+    const int K = W.cols, off0 = step * 1024 + 16 * lane;
+    const int off = min(off0, K - 16);
+    const v4i_t x = *(const v4i_t *)(lq + off);
+    int d = dot16(P.q, x, 0);
+    d += xpair(d);
+    const float t = (h2f((uint16_t)P.sc) * ls[off >> 5]) * (float)d;
+    return (off0 < K && !(lane & 1)) ? t : 0.0f;
+}
+
+// dot_q4k_q8_0_scalar per-sub-block term (model.rs:8969-9025):
+// s_x * (d*sc*dot - dmin*mn*sum(q_x)).  The 16 qs bytes of a lane hold half of
+// sub-block c (low nibbles) and half of sub-block c+4 (high nibbles); after
+// the pair add the even lane owns sub c, the odd lane sub c+4.
+__device__ __forceinline__ float pc_dot_q8(const Pc<F_Q4K> &P, const WDesc &W, const int8_t *lq, const float *ls,
+                                           const int *lsum, int step, int lane) {
+    const int span = (W.cols >> 8) * 128, off0 = step * 1024 + 16 * lane;
+    const int off = min(off0, span - 16);
+    const int sb = off >> 7, c = (off >> 5) & 3, half = (off >> 4) & 1;
+    const int blo = sb * 8 + c, bhi = blo + 4;
+    const v4i_t xl = *(const v4i_t *)(lq + blo * 32 + half * 16);
+    const v4i_t xh = *(const v4i_t *)(lq + bhi * 32 + half * 16);
+    const v4i_t lo = P.q & 0x0F0F0F0F, hi = (P.q >> 4) & 0x0F0F0F0F;
+    int dl = dot16(lo, xl, 0), dh = dot16(hi, xh, 0);
+    dl += xpair(dl);
+    dh += xpair(dh);
+    const uint32_t h0 = (uint32_t)P.h.x;
+    const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+    // unpack_q4k_scales (model.rs:8709-8719), flare packing
+    const uint32_t s_a = byte_of((uint32_t)P.h.y, c), s_b = byte_of((uint32_t)P.h.z, c),
+                   s_c = byte_of((uint32_t)P.h.w, c);
+    const bool own_hi = half;  // odd lane: sub-block c+4
+    const uint32_t sc = own_hi ? ((s_a >> 6) | ((s_c & 0xF) << 2)) : (s_a & 63);
+    const uint32_t mn = own_hi ? ((s_b >> 6) | ((s_c >> 4) << 2)) : (s_b & 63);
+    const int b = own_hi ? bhi : blo;
+    const int dot = own_hi ? dh : dl;
+    const float d_sc = d * (float)sc, dmin_mn = dmin * (float)mn;
+    const float t = ls[b] * (d_sc * (float)dot - dmin_mn * (float)lsum[b]);
+    return off0 < span ? t : 0.0f;
+}
+
+// ---- f32 input (activations in LDS as floats) ------------------------------
+// dequant (quantize.rs) then matvec_argmax_f32's f32 dot (model.rs:8668-8689)
+__device__ __forceinline__ float pc_dot_f32(const Pc<F_Q8_0> &P, const WDesc &W, const float *lx, int step,
+                                            int lane) {
+    const int K = W.cols, off0 = step * 1024 + 16 * lane;
+    const int off = min(off0, K - 16);
+    const float scale = h2f((uint16_t)P.sc);
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const v4f_t x = *(const v4f_t *)(lx + off + 4 * j);
+        float q[4];
+        i8x4_to_f32(P.q[j], q);
+#pragma unroll
+        for (int k = 0; k < 4; k++) a += (q[k] * scale) * x[k];
+    }
+    return off0 < K ? a : 0.0f;
+}
+
+// dequant_q6k_block (quantize.rs:343-384, llama.cpp layout): w = d*sc*q.
+// Lane bytes: ql[hf*64 + qq*16 + i]; qq<2 -> q1 (low) / q3 (high), qq>=2 ->
+// q2 / q4; the 2 qh bits sit at shift 2*(qq>>1) and +4.
+__device__ __forceinline__ float pc_dot_f32(const Pc<F_Q6K> &P, const WDesc &W, const float *lx, int step,
+                                            int lane) {
+    const int span = (W.cols >> 8) * 128, off0 = step * 1024 + 16 * lane;
+    const int off = min(off0, span - 16);
+    const int sb = off >> 7, o = off & 127, hf = o >> 6, qq = (o >> 4) & 3;
+    const int e_lo = sb * 256 + hf * 128 + (qq >> 1) * 32 + (qq & 1) * 16;
+    const int sh = 2 * (qq >> 1);
+    const float d = h2f((uint16_t)P.d);
+    const float ds_lo = d * (float)(int8_t)(P.sc & 0xFF), ds_hi = d * (float)(int8_t)(P.sc >> 8);
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const v4f_t xl = *(const v4f_t *)(lx + e_lo + 4 * j);
+        const v4f_t xh = *(const v4f_t *)(lx + e_lo + 64 + 4 * j);
+        // four 6-bit codes per word, assembled byte-wise: nibble | 2 qh bits << 4
+        const uint32_t lw = (uint32_t)P.ql[j], hw = (uint32_t)P.qh[j];
+        const uint32_t clo = (lw & 0x0F0F0F0Fu) | (((hw >> sh) & 0x03030303u) << 4);
+        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (sh + 4)) & 0x03030303u) << 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float q_lo = (float)((clo >> (8 * k)) & 0xFFu) - 32.0f;
+            const float q_hi = (float)((chi >> (8 * k)) & 0xFFu) - 32.0f;
+            a += (ds_lo * q_lo) * xl[k];
+            a += (ds_hi * q_hi) * xh[k];
+        }
+    }
+    return off0 < span ? a : 0.0f;
+}
+
+__device__ __forceinline__ float pc_dot_f32(const Pc<F_F32> &P, const WDesc &W, const float *lx, int step,
+                                            int lane) {
+    const int K = W.cols, off0 = step * 1024 + 16 * lane;
+    const int off = min(off0, 4 * K - 16);
+    const v4f_t x = *(const v4f_t *)(lx + (off >> 2));
+    const float a = P.w.x * x.x + P.w.y * x.y + P.w.z * x.z + P.w.w * x.w;
+    return off0 < 4 * K ? a : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// arguments
+// ---------------------------------------------------------------------------
+struct MvsArgs {
+    WDesc W;
+    int pro, epi;          // prologue (PRO_* for Q8 input; 0 copy / 1 rmsnorm for f32 input), epilogue
+    const float *x, *nw;   // prologue input and norm weight
+    float eps;
+    const int8_t *gq;      // PRO_LOADQ input
+    const float *gs;
+    const int *gsum;
+    float *out;
+    unsigned long long *slot;  // EPI_ARGMAX
+    QkvEpi qkv;                // EPI_QKV
+    // gate/up: F hidden units, Q8_0 output blocks, optional f32 copy
+    int F;
+    int8_t *hq;
+    float *hs;
+    int *hsum;
+    float *hout;
+    long long *trace;
+};
+
+__host__ __device__ inline size_t mvs_lds_bytes(bool f32in, int K) {
+    return f32in ? (size_t)K * 4 + 64 * 4 : (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64;
+}
+
+// prologue staging shared by both kernels: x (Q8 or f32) into LDS
+template <bool F32IN, int NT>
+struct Stage;
+template <int NT>
+struct Stage<false, NT> {
+    StageQ8<NT> s;
+    __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw, a.gq, a.gs, a.gsum); }
+    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
+        const int K = a.W.cols;
+        int8_t *lq = (int8_t *)smem;
+        float *ls = (float *)(smem + K);
+        int *lsum = (int *)(ls + (K >> 5));
+        float *red = (float *)(lsum + (K >> 5));
+        s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red);
+    }
+};
+template <int NT>
+struct Stage<true, NT> {
+    StageF32<NT> s;
+    __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw); }
+    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
+        const int K = a.W.cols;
+        float *lx = (float *)smem;
+        s.finish(a.pro, K, a.eps, a.x, a.nw, lx, lx + K);
+    }
+};
+
+template <int FMT, bool F32IN>
+__device__ __forceinline__ float pc_dot(const Pc<FMT> &P, const WDesc &W, const char *smem, int step, int lane) {
+    if constexpr (F32IN) {
+        return pc_dot_f32(P, W, (const float *)smem, step, lane);
+    } else {
+        const int K = W.cols;
+        const int8_t *lq = (const int8_t *)smem;
+        const float *ls = (const float *)(smem + K);
+        const int *lsum = (const int *)(ls + (K >> 5));
+        return pc_dot_q8(P, W, lq, ls, lsum, step, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_mvs: generic persistent streaming matvec
+// ---------------------------------------------------------------------------
+constexpr int kMvsThreads = 256;
+
+template <int FMT, bool F32IN, int R, int SU>
+__global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const WDesc &W = a.W;
+    const int K = W.cols;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int S = mvs_steps(FMT, K), NR = (S + SU - 1) / SU;
+    const int ngrp = (W.rows + R - 1) / R;
+    const int gw = blockIdx.x * (kMvsThreads / 64) + wave, tw = gridDim.x * (kMvsThreads / 64);
+    const int nunits = gw < ngrp ? ((ngrp - 1 - gw) / tw + 1) * NR : 0;
+
+    Pc<FMT> ta[R][SU], tb[R][SU];
+    auto load = [&](Pc<FMT>(&T)[R][SU], int u) {
+        const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = min(rg * R + r, W.rows - 1);
+#pragma unroll
+            for (int s = 0; s < SU; s++) T[r][s].load(W, row, min(rr * SU + s, S - 1), lane);
+        }
+    };
+    MV_TS(0);
+    MV_TSB(0);
+    Stage<F32IN, kMvsThreads> stg;
+    stg.issue(a);                  // 1. activation loads
+    FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
+    if (nunits > 0) load(ta, 0);   // 2. first weight pieces
+    const int qpos = a.epi == EPI_QKV ? *a.qkv.posp : 0;
+    MV_TS(1);
+    stg.finish(a, smem);           // 3. prologue arithmetic (ends with a barrier)
+    MV_TS(2);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    unsigned long long best = 0;
+    auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
+        const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int s = 0; s < SU; s++) {
+                acc[r] += pc_dot<FMT, F32IN>(T[r][s], W, smem, rr * SU + s, lane);
+                // one piece at a time: keeps the 16 activation floats of an
+                // f32 piece from being hoisted for the whole tile
+                if constexpr (F32IN) __builtin_amdgcn_sched_barrier(0);
+            }
+        if (u == 0) MV_TS(3);
+        if (rr == NR - 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+            const int row0 = rg * R;
+            if (a.epi == EPI_ARGMAX) {
+                best = umax64(best, rows_best<R>(acc, row0, W.rows));
+            } else if constexpr (R % 2 == 0) {
+                if (a.epi == EPI_QKV) store_qkv<R>(acc, row0, W.rows, lane, a.qkv, qpos, a.out);
+                else store_rows<R>(acc, row0, W.rows, lane, a.epi, a.out);
+            } else {
+                store_rows<R>(acc, row0, W.rows, lane, a.epi, a.out);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        }
+    };
+    // ping-pong: the next unit's pieces are in flight while this one is
+    // consumed (a wave with no next unit issues nothing)
+    for (int u = 0; u < nunits; u += 2) {
+        if (u + 1 < nunits) load(tb, u + 1);
+        consume(ta, u);
+        if (u + 1 >= nunits) break;
+        if (u + 2 < nunits) load(ta, u + 2);
+        consume(tb, u + 1);
+    }
+    MV_TS(4);
+    if (a.epi == EPI_ARGMAX) {
+        float *red = (float *)(smem + mvs_lds_bytes(F32IN, K) - 64 * 4 - (F32IN ? 0 : 64));
+        wg_argmax_commit(best, a.slot, (unsigned long long *)red);
+    }
+    MV_TSB(1);
+}
+
+// ---------------------------------------------------------------------------
+// k_mvs_gu: fused gate/up + SiLU + Q8_0 quantization of the hidden vector
+// (model.rs:2376-2416, silu_mul_into 9783-9796, quantize 2480-2522).
+// Rows [0, F) are w_gate, [F, 2F) w_up.  Workgroup b owns hidden blocks
+// b, b + grid, ...; wave w takes hidden units 32*blk + w*HU .. + HU, HU/2 at
+// a time (item = 2 gate rows + the 2 matching up rows).
+// ---------------------------------------------------------------------------
+template <int FMT, int SU, int NW>
+__global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int NT = NW * 64, HU = 32 / NW, IPB = HU / 2;  // items per wave per block
+    static_assert(HU % 2 == 0, "two hidden units per item");
+    constexpr int R = 4;
+    const WDesc &W = a.W;
+    const int K = W.cols, F = a.F;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int S = mvs_steps(FMT, K), NR = (S + SU - 1) / SU;
+    const int nblk = F / 32;
+    const int myblk = (int)blockIdx.x < nblk ? (nblk - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int upb = IPB * NR;  // units per block per wave
+    const int nunits = myblk * upb;
+    float *hb = (float *)(smem + mvs_lds_bytes(false, K));  // [32] SiLU*up of the current block
+
+    Pc<FMT> ta[R][SU], tb[R][SU];
+    auto rows_of = [&](int u, int &blk, int &item, int &rr) {
+        const int kb = u / upb, rem = u - kb * upb;
+        item = rem / NR;
+        rr = rem - item * NR;
+        blk = (int)blockIdx.x + kb * (int)gridDim.x;
+    };
+    auto load = [&](Pc<FMT>(&T)[R][SU], int u) {
+        int blk, item, rr;
+        rows_of(u, blk, item, rr);
+        const int f = blk * 32 + wave * HU + item * 2;
+        const int rws[R] = {f, f + 1, F + f, F + f + 1};
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int s = 0; s < SU; s++) T[r][s].load(W, rws[r], min(rr * SU + s, S - 1), lane);
+    };
+    MV_TS(0);
+    MV_TSB(0);
+    Stage<false, NT> stg;
+    stg.issue(a);
+    FLARE_STAGE_BARRIER();
+    if (nunits > 0) load(ta, 0);
+    MV_TS(1);
+    stg.finish(a, smem);
+    MV_TS(2);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
+        int blk, item, rr;
+        rows_of(u, blk, item, rr);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int s = 0; s < SU; s++) acc[r] += pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+        if (u == 0) MV_TS(3);
+        if (rr == NR - 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+            if (lane < 2) {
+                // silu_mul_into: g / (1 + exp(-g)) * u
+                const float g = lane ? acc[1] : acc[0], up = lane ? acc[3] : acc[2];
+                hb[wave * HU + item * 2 + lane] = (g / (1.0f + expf(-g))) * up;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = 0.0f;
+            if (item == IPB - 1) {
+                // block complete on every wave: quantize it
+                __syncthreads();
+                if (threadIdx.x < 32) {
+                    const float h = hb[threadIdx.x];
+                    if (a.hout) a.hout[blk * 32 + threadIdx.x] = h;
+                    quant_block32_lanes(h, a.hq + blk * 32, a.hs + blk, a.hsum + blk);
+                }
+                __syncthreads();  // hb reused by the next block
+                if (u == upb - 1) MV_TS(4);
+            }
+        }
+    };
+    for (int u = 0; u < nunits; u += 2) {
+        if (u + 1 < nunits) load(tb, u + 1);
+        consume(ta, u);
+        if (u + 1 >= nunits) break;
+        if (u + 2 < nunits) load(ta, u + 2);
+        consume(tb, u + 1);
+    }
+    MV_TS(5);
+    MV_TSB(1);
+}
+
+}  // namespace fl

@@ -1,0 +1,29 @@
+// Q4_K streaming matvec (Q8 input) and the Q4_K gate/up kernel.
+#include "launch.h"
+
+namespace fl {
+
+#define C(FMT, F32IN, RR, SS)                                                                         \
+    if (p.r == RR && p.su == SS) {                                                                    \
+        hipLaunchKernelGGL((k_mvs<FMT, F32IN, RR, SS>), dim3(p.grid), dim3(kMvsThreads), p.lds, st, a); \
+        return hipSuccess;                                                                            \
+    }
+
+hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
+    C(F_Q4K, false, 4, 1) C(F_Q4K, false, 2, 1) C(F_Q4K, false, 2, 2)
+    return hipErrorNotSupported;
+}
+#undef C
+
+hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
+#define G(SS, NW)                                                                               \
+    if (p.su == SS && p.r == NW) {                                                              \
+        hipLaunchKernelGGL((k_mvs_gu<F_Q4K, SS, NW>), dim3(p.grid), dim3(NW * 64), p.lds, st, a); \
+        return hipSuccess;                                                                      \
+    }
+    G(1, 8) G(1, 4)
+#undef G
+    return hipErrorNotSupported;
+}
+
+}  // namespace fl
