@@ -32,6 +32,10 @@ WORKLOADS = {
     "c3": dict(spec="Llama-3-8B", prompt=4096, kv="f16",
                desc="Llama-3-8B arch, Q4_K layers + Q6_K output/embedding, batch-1 greedy decode at "
                     "context 4096, fp16 KV cache"),
+    "c4": dict(spec="Llama-3-8B", prompt=0, kv="all",
+               desc="decode attention kernel alone at Llama-3-8B heads (32 q / 8 kv, head_dim 128), one query "
+                    "token, KV cache of 8k / 32k / 128k tokens in fp16, Q8 (per-32 fp16 scale) and KIVI 2-bit "
+                    "(group 32, fp16 residual window); q, K, V ~ N(0, 1)"),
     "c1": dict(spec="SmolLM2-135M", prompt=32, kv="f32",
                desc="SmolLM2-135M arch, Q8_0 tied, greedy decode after a 32-token prompt"),
 }
@@ -82,6 +86,82 @@ def cpu_baseline(model, spec, n_prompt: int, n_decode: int) -> dict:
                       f"model (f32 KV), C restatement of flare-core's x86 scalar path, {dt:.1f} s"}
 
 
+def bench_attention_c4(args) -> int:
+    """the decode attention kernel alone.  For each KV
+    form and context, the cache is filled with N(0,1) rows and enough layers
+    (>= 1 GB of K+V in total) that consecutive launches stream from HBM, not
+    the 256 MB MALL; HIP events on the context stream time `iters` launches."""
+    import numpy as np
+    import torch
+
+    from flarellm_amd import FL_KV_F16, FL_KV_KIVI2, FL_KV_Q8
+    from flarellm_amd import synth as S
+    from flarellm_amd.backend import HipBackend
+
+    base = S.CONFIGS["Llama-3-8B"]
+    nh, nkv, hd = base.heads, base.kv_heads, base.head_dim
+    kvd = nkv * hd
+    forms = {"f16": FL_KV_F16, "q8": FL_KV_Q8, "kivi2": FL_KV_KIVI2}
+    ctxs = [8192, 32768, 131072]
+    rng = np.random.default_rng(3)
+    rows_k = rng.standard_normal((max(ctxs), kvd), dtype=np.float32)
+    rows_v = rng.standard_normal((max(ctxs), kvd), dtype=np.float32)
+    q = rng.standard_normal(nh * hd, dtype=np.float32)
+    b = HipBackend(0)
+    stream = torch.cuda.ExternalStream(b.stream)
+    cases = {}
+    tot_bytes = tot_us = 0.0
+    for name, fmt in forms.items():
+        for T in ctxs:
+            # bytes of one launch decide the layer count (>= 1 GB rotated)
+            spec = S.replace(base, layers=1, max_seq=T)
+            b.init_gpu_kv_cache(spec, fmt)
+            nbytes = b.bench_attention(T, 0)
+            L = int(min(256, max(2, -(-1.0e9 // nbytes))))
+            spec = S.replace(base, layers=L, max_seq=T)
+            b.init_gpu_kv_cache(spec, fmt)
+            t0 = time.time()
+            for l in range(L):
+                b.gpu_kv_write_batch(l, 0, rows_k[:T], rows_v[:T])
+            out = b.grouped_query_attention_from_gpu_cache(q, 0, T)  # also stages q
+            assert np.isfinite(out).all()
+            b.bench_attention(T, 3)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            iters = args.kernel_iters
+            e0.record(stream)
+            nbytes = b.bench_attention(T, iters)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / iters
+            cases[f"{name}@{T // 1024}k"] = {"us": round(us, 2), "bytes": int(nbytes), "layers": L,
+                                            "GB_s": round(nbytes / us / 1e3, 1),
+                                            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            tot_bytes += nbytes
+            tot_us += us
+            log(f"[bench c4] {name:6s} T={T:6d} L={L:3d} fill {time.time() - t0:.1f}s  {us:9.2f} us  "
+                f"{nbytes / 1e6:8.2f} MB  {nbytes / us / 1e3:7.1f} GB/s")
+    b.close()
+    dom = max(cases, key=lambda k: cases[k]["us"])
+    d = cases[dom]
+    out = {
+        "metric": "decode attention HBM GB/s (one query token, Llama-3-8B heads, KV 8k/32k/128k in fp16/Q8/KIVI2)",
+        "value": round(tot_bytes / tot_us / 1e3, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.kernel_iters,
+        "warmup": 3, "ms_per_step": round(tot_us / len(cases) / 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (fp16 / int8 / 2-bit KV)",
+        "data": "synthetic (q, K, V ~ N(0,1))",
+        "config": {"workload": WORKLOADS["c4"]["desc"], "model": "Llama-3-8B heads", "global_batch": 1,
+                   "seq_len": max(ctxs), "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": d["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d["frac"], "traffic": None, "kernel": f"k_attn {dom}", "bytes_per_launch": d["bytes"],
+                     "avg_launch_us": d["us"]},
+        "cpu_baseline": None,
+        "cases": cases,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,6 +185,8 @@ def main() -> int:
     from flarellm_amd import synth as S
     from flarellm_amd.backend import HipBackend
 
+    if args.config == "c4":
+        return bench_attention_c4(args)
     wl = WORKLOADS[args.config]
     spec = S.CONFIGS[wl["spec"]]
     n_prompt = wl["prompt"]

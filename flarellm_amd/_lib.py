@@ -11,7 +11,7 @@ import os
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflare_hip.so")
 
 FL_F32, FL_Q8_0, FL_Q4K, FL_Q6K = 0, 1, 2, 3
-FL_KV_F32, FL_KV_F16 = 0, 1
+FL_KV_F32, FL_KV_F16, FL_KV_Q8, FL_KV_KIVI2 = 0, 1, 2, 3
 FORMAT_NAMES = {FL_F32: "F32", FL_Q8_0: "Q8_0", FL_Q4K: "Q4_K", FL_Q6K: "Q6_K"}
 
 
@@ -80,6 +80,9 @@ SIGNATURES = {
     "fl_has_kv_cache": (i32, [vp]),
     "fl_kv_write": (i32, [vp, i32, i32, vp, vp]),
     "fl_reset": (i32, [vp]),
+    "fl_kv_write_batch": (i32, [vp, i32, i32, i32, vp, vp]),
+    "fl_gqa_from_cache": (i32, [vp, i32, vp, i32, vp]),
+    "fl_bench_attention": (i32, [vp, i32, i32, C.POINTER(C.c_double)]),
     "fl_decode_step": (i32, [vp, C.c_uint32, i32, vp, C.POINTER(C.c_int32), C.POINTER(f32)]),
     "fl_generate": (i32, [vp, vp, i32, i32, vp]),
     "fl_decode_continue": (i32, [vp, i32]),

@@ -234,6 +234,28 @@ class HipBackend:
         value = np.ascontiguousarray(value, np.float32)
         check(self.lib.fl_kv_write(self.ctx, layer, position, key.ctypes.data, value.ctypes.data), self.ctx)
 
+    def gpu_kv_write_batch(self, layer: int, pos0: int, keys: np.ndarray, values: np.ndarray):
+        """gpu_kv_write (model.rs:287) for consecutive rows [n, nkv*hd] at pos0.."""
+        keys = np.ascontiguousarray(keys, np.float32)
+        values = np.ascontiguousarray(values, np.float32)
+        n = keys.shape[0]
+        check(self.lib.fl_kv_write_batch(self.ctx, layer, pos0, n, keys.ctypes.data, values.ctypes.data), self.ctx)
+
+    def grouped_query_attention_from_gpu_cache(self, q: np.ndarray, layer: int, seq_len: int) -> np.ndarray:
+        """grouped_query_attention_from_gpu_cache (model.rs:311): one query
+        token (RoPE applied) over slots 0..seq_len-1 of layer's cache."""
+        q = np.ascontiguousarray(q, np.float32)
+        out = np.empty(self.spec.heads * self.spec.head_dim, np.float32)
+        check(self.lib.fl_gqa_from_cache(self.ctx, layer, q.ctypes.data, seq_len, out.ctypes.data), self.ctx)
+        return out
+
+    def bench_attention(self, seq_len: int, iters: int) -> float:
+        """Enqueue iters attention launches over seq_len tokens (synchronises);
+        returns the algorithmic K+V bytes of one launch."""
+        b = C.c_double()
+        check(self.lib.fl_bench_attention(self.ctx, seq_len, iters, C.byref(b)), self.ctx)
+        return b.value
+
     def reset(self):
         check(self.lib.fl_reset(self.ctx), self.ctx)
 

@@ -1,4 +1,4 @@
-// Decode attention launchers.
+// Decode attention launchers and the Q8 / KIVI cache writers.
 #include "launch.h"
 
 namespace fl {
@@ -16,9 +16,118 @@ static hipError_t launch_attn_t(int D, int G, hipStream_t st, const AttnArgs &a)
     return hipErrorNotSupported;
 }
 
-hipError_t launch_attn(bool f16, int D, int G, hipStream_t st, const AttnArgs &a) {
+hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a) {
     if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit) return hipErrorInvalidValue;
-    return f16 ? launch_attn_t<__half>(D, G, st, a) : launch_attn_t<float>(D, G, st, a);
+    switch (kvfmt) {
+    case KV_F32: return launch_attn_t<float>(D, G, st, a);
+    case KV_F16: return launch_attn_t<__half>(D, G, st, a);
+    case KV_Q8: return launch_attn_t<KvQ8>(D, G, st, a);
+    case KV_KIVI: return launch_attn_t<KvKivi>(D, G, st, a);
+    }
+    return hipErrorNotSupported;
+}
+
+// ---------------------------------------------------------------------------
+// Cache writers for n new token rows (fl_kv_write / fl_kv_write_batch).
+// rows: f32 [n][nkv][D] staged on the device, token p0 + i in row i.
+// ---------------------------------------------------------------------------
+
+// Q8: one thread per (token, kv head, 32-block); quantize_input_q8_0_into
+// arithmetic with the scale stored as binary16.
+__global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *krows, const float *vrows, int p0,
+                                                     int n, int D) {
+    const int nb = D / 32;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)n * a.nkv * nb * 2;
+    if (i >= total) return;
+    const int isv = (int)(i & 1);
+    long long j = i >> 1;
+    const int b = (int)(j % nb);
+    j /= nb;
+    const int kvh = (int)(j % a.nkv);
+    const int r = (int)(j / a.nkv);
+    const float *x = (isv ? vrows : krows) + ((size_t)r * a.nkv + kvh) * D + 32 * b;
+    float amax = 0.0f;
+    for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(x[e]));
+    const float d = amax / 127.0f;
+    const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+    const int t = p0 + r;
+    int8_t *q = (int8_t *)(isv ? a.vc : a.kc) + (size_t)kvh * a.head_stride + (size_t)t * D + 32 * b;
+    for (int e = 0; e < 32; e++) q[e] = sat_i8(roundf(x[e] * id));
+    (isv ? a.vs : a.ks)[((size_t)kvh * a.S + t) * nb + b] = f2h(d);
+}
+
+// KIVI step 1: quantize the groups that leave the ring while rows
+// [p0, p0+n) are written (grid: groups x kv heads).  Values of staged rows are
+// rounded to binary16 first, as the ring would hold them.
+__global__ __launch_bounds__(256) void k_kv_kivi_groups(AttnArgs a, const float *krows, const float *vrows, int p0,
+                                                        int n, int D, int g0) {
+    const int gi = g0 + (int)blockIdx.x, kvh = (int)blockIdx.y;
+    auto src = [&](int t, int ch, bool is_v) -> float {
+        if (t >= p0) {
+            const float *r = is_v ? vrows : krows;
+            return __half2float(__float2half(r[((size_t)(t - p0) * a.nkv + kvh) * D + ch]));
+        }
+        const __half *r = is_v ? a.rv : a.rk;
+        return __half2float(r[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch]);
+    };
+    kivi_quantize_group(a, D, kvh, gi, src);
+}
+
+// KIVI step 2: the newest rows (at most kKiviRing) into the fp16 ring.
+__global__ __launch_bounds__(256) void k_kv_kivi_ring(AttnArgs a, const float *krows, const float *vrows, int p0,
+                                                      int n, int D, int first) {
+    const int r = first + (int)blockIdx.x, kvh = (int)blockIdx.y;
+    const int t = p0 + r;
+    for (int e = threadIdx.x; e < 2 * D; e += blockDim.x) {
+        const int isv = e >= D, ch = e % D;
+        const float v = (isv ? vrows : krows)[((size_t)r * a.nkv + kvh) * D + ch];
+        (isv ? a.rv : a.rk)[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch] = __float2half(v);
+    }
+}
+
+// F32 / F16: plain copy (binary16 RNE for F16, as half::f16::from_f32).
+__global__ __launch_bounds__(256) void k_kv_plain_write(AttnArgs a, const float *krows, const float *vrows, int p0,
+                                                        int n, int D, int f16) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long per = (long long)a.nkv * D;
+    if (i >= (long long)n * per * 2) return;
+    const int isv = (int)(i / ((long long)n * per));
+    const long long j = i % ((long long)n * per);
+    const int r = (int)(j / per), kvh = (int)((j % per) / D), ch = (int)(j % D);
+    const float v = (isv ? vrows : krows)[j];
+    const size_t o = (size_t)kvh * a.head_stride + (size_t)(p0 + r) * D + ch;
+    void *dst = isv ? (void *)a.vc : (void *)a.kc;
+    if (f16) ((__half *)dst)[o] = __float2half(v);
+    else ((float *)dst)[o] = v;
+}
+
+hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
+                           int p0, int n, int D) {
+    if (n <= 0) return hipSuccess;
+    if (kvfmt == KV_F32 || kvfmt == KV_F16) {
+        const long long total = (long long)n * a.nkv * D * 2;
+        hipLaunchKernelGGL(k_kv_plain_write, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, krows,
+                           vrows, p0, n, D, kvfmt == KV_F16 ? 1 : 0);
+        return hipGetLastError();
+    }
+    if (kvfmt == KV_Q8) {
+        const long long total = (long long)n * a.nkv * (D / 32) * 2;
+        hipLaunchKernelGGL(k_kv_q8_write, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, krows, vrows,
+                           p0, n, D);
+        return hipGetLastError();
+    }
+    if (kvfmt != KV_KIVI) return hipErrorNotSupported;
+    // groups [0, kivi_qlen(T + 1)) are quantized once T tokens are written
+    const int g0 = kivi_qlen(p0 + 1) / kKiviGroup, g1 = kivi_qlen(p0 + n + 1) / kKiviGroup;
+    if (g1 > g0) {
+        hipLaunchKernelGGL(k_kv_kivi_groups, dim3(g1 - g0, a.nkv), dim3(256), 0, st, a, krows, vrows, p0, n, D, g0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const int first = n > kKiviRing ? n - kKiviRing : 0;
+    hipLaunchKernelGGL(k_kv_kivi_ring, dim3(n - first, a.nkv), dim3(256), 0, st, a, krows, vrows, p0, n, D, first);
+    return hipGetLastError();
 }
 
 }  // namespace fl

@@ -1,6 +1,8 @@
 // Split-K GQA decode attention kernel (gfx950 wave64).
 #pragma once
 
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace fl {
@@ -16,8 +18,8 @@ namespace fl {
 // ---------------------------------------------------------------------------
 struct AttnArgs {
     const float *q;      // [nh*D], RoPE already applied
-    const void *kc, *vc; // this layer's cache
-    long long tok_stride, head_stride;  // elements between slots / kv heads
+    const void *kc, *vc; // this layer's cache (F32/F16 values, Q8 int8 codes, KIVI 2-bit codes)
+    long long tok_stride, head_stride;  // elements between slots / kv heads (F32/F16/Q8)
     const int *posp;     // attends slots 0..*posp
     int nkv, nsplit;     // grid = (nsplit, nkv)
     int chmin;           // minimum tokens per split (a multiple of attn_tpp(D))
@@ -28,7 +30,32 @@ struct AttnArgs {
     float *os;
     int *osum;
     long long *trace;    // FLARE_ATTN_TRACE builds: per-phase timestamps of workgroup (0,0)
+    // Q8 / KIVI caches (head-major, max_seq slots per kv head)
+    int S;               // slots per kv head (a multiple of 32)
+    uint16_t *ks, *vs;   // Q8: f16 scale per 32 values [kvh][S][D/32]
+    uint32_t *kp, *vp;   // KIVI: (scale, min) f16 pairs; K [kvh][S/32][D], V [kvh][S][D/32]
+    __half *rk, *rv;     // KIVI: fp16 residual ring [kvh][kKiviRing][D]
+    // new token (Q8 / KIVI decode step): K / V rows [nkv*D] as f32 from the
+    // QKV epilogue; quantized (Q8) or rounded (KIVI ring) and stored into the
+    // cache slot *posp by the workgroup whose chunk holds it.  nullptr when
+    // the cache was written beforehand (fl_kv_write).
+    const float *knew, *vnew;
 };
+
+// KIVI 2-bit cache constants: groups of 32 (K per channel over 32 tokens, V
+// per token over 32 channels); the newest tokens stay in an fp16 ring.
+constexpr int kKiviGroup = 32;
+constexpr int kKiviResidual = 128;  // at least this many newest tokens are fp16
+constexpr int kKiviRing = kKiviResidual + kKiviGroup;  // ring slots per kv head
+// Tokens [0, kivi_qlen(T)) of a T-token cache are read from the 2-bit groups,
+// [kivi_qlen(T), T) from the ring (between 129 and 160 tokens once T > 128).
+__host__ __device__ inline int kivi_qlen(int T) {
+    return T - 1 - kKiviResidual > 0 ? kKiviGroup * ((T - 1 - kKiviResidual) / kKiviGroup) : 0;
+}
+
+// KV storage tags for the attention kernel
+struct KvQ8 {};
+struct KvKivi {};
 
 
 
@@ -53,23 +80,6 @@ struct AttnArgs {
     } while (0)
 #endif
 
-template <typename KT>
-__device__ __forceinline__ void load8(const KT *p, float *v);
-template <>
-__device__ __forceinline__ void load8<__half>(const __half *p, float *v) {
-    const v4i_t t = *(const v4i_t *)p;
-    const uint32_t w[4] = {(uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[2 * i] = h2f((uint16_t)(w[i] & 0xFFFF));
-        v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
-    }
-}
-template <>
-__device__ __forceinline__ void load8<float>(const float *p, float *v) {
-    const v4f_t a = ((const v4f_t *)p)[0], b = ((const v4f_t *)p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
 // Agent-scope relaxed atomic float store / load (cross-XCD visible without
 // a cache write-back fence).
 __device__ __forceinline__ void st_agent(float *p, float v) {
@@ -79,33 +89,265 @@ __device__ __forceinline__ float ld_agent(const float *p) {
     return __uint_as_float(__hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// K/V rows kept raw in registers (8 elements) and converted at use.
-template <typename KT>
-struct KVRaw;
-template <>
-struct KVRaw<__half> {
-    v4i_t v;
-    __device__ __forceinline__ void load(const __half *p) { v = *(const v4i_t *)p; }
-    __device__ __forceinline__ void get(float *o) const {
-        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+__device__ __forceinline__ void h8_to_f32(const v4i_t &v, float *o) {
+    const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            o[2 * i] = h2f((uint16_t)(w[i] & 0xFFFF));
-            o[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+    for (int i = 0; i < 4; i++) {
+        o[2 * i] = h2f((uint16_t)(w[i] & 0xFFFF));
+        o[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+    }
+}
+__device__ __forceinline__ v4i_t f32_to_h8(const float *x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = (uint32_t)f2h(x[2 * i]) | ((uint32_t)f2h(x[2 * i + 1]) << 16);
+    return v4i_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// KIVI 2-bit group quantizer (quantize_to_packed arithmetic,
+// flare-core/src/kv_cache.rs:336-371): min / max of the group, scale =
+// (max - min) / 3 (0 for a range below f32::EPSILON), code =
+// clamp(round((v - min) * 3 / range), 0, 3).  The (scale, min) pair is kept
+// as two binary16 values; dequantization is code * scale + min.
+struct KiviQ {
+    float mn, inv, scale;
+    __device__ __forceinline__ void init(float lo, float hi) {
+        const float range = hi - lo;
+        scale = fabsf(range) < 1.1920929e-7f ? 0.0f : range / 3.0f;
+        inv = fabsf(scale) < 1.1920929e-7f ? 0.0f : 3.0f / range;
+        mn = lo;
+    }
+    __device__ __forceinline__ uint32_t code(float v) const {
+        if (scale == 0.0f) return 0u;
+        return (uint32_t)fminf(fmaxf(roundf((v - mn) * inv), 0.0f), 3.0f);
+    }
+    __device__ __forceinline__ uint32_t packed() const { return (uint32_t)f2h(scale) | ((uint32_t)f2h(mn) << 16); }
+};
+__device__ __forceinline__ float kivi_deq(uint32_t code, uint32_t sm) {
+    return (float)code * h2f((uint16_t)(sm & 0xFFFF)) + h2f((uint16_t)(sm >> 16));
+}
+
+// One token's K and V elements [8c, 8c+8) for kv head kvh, kept raw in
+// registers and decoded at use.
+template <typename KT>
+struct KVRow;
+template <>
+struct KVRow<float> {
+    v4f_t k0, k1, v0, v1;
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
+        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
+        const v4f_t *kp = (const v4f_t *)((const float *)a.kc + o), *vp = (const v4f_t *)((const float *)a.vc + o);
+        k0 = kp[0]; k1 = kp[1]; v0 = vp[0]; v1 = vp[1];
+    }
+    __device__ __forceinline__ void getk(float *o) const {
+        o[0] = k0.x; o[1] = k0.y; o[2] = k0.z; o[3] = k0.w; o[4] = k1.x; o[5] = k1.y; o[6] = k1.z; o[7] = k1.w;
+    }
+    __device__ __forceinline__ void getv(float *o) const {
+        o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w; o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
+    }
+};
+template <>
+struct KVRow<__half> {
+    v4i_t k, v;
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
+        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
+        k = *(const v4i_t *)((const __half *)a.kc + o);
+        v = *(const v4i_t *)((const __half *)a.vc + o);
+    }
+    __device__ __forceinline__ void getk(float *o) const { h8_to_f32(k, o); }
+    __device__ __forceinline__ void getv(float *o) const { h8_to_f32(v, o); }
+};
+// Q8: int8 codes [kvh][S][D] with one f16 scale per 32 values.
+template <>
+struct KVRow<KvQ8> {
+    v2i_t k, v;
+    uint32_t sc;  // K scale | V scale << 16
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
+        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
+        k = *(const v2i_t *)((const int8_t *)a.kc + o);
+        v = *(const v2i_t *)((const int8_t *)a.vc + o);
+        const size_t so = ((size_t)kvh * a.S + t) * (a.tok_stride >> 5) + (c >> 2);
+        sc = (uint32_t)a.ks[so] | ((uint32_t)a.vs[so] << 16);
+    }
+    __device__ __forceinline__ static void dec(const v2i_t &q, uint16_t s, float *o) {
+        const float d = h2f(s);
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = (float)(int8_t)(((uint32_t)(i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFF) * d;
+    }
+    __device__ __forceinline__ void getk(float *o) const { dec(k, (uint16_t)(sc & 0xFFFF), o); }
+    __device__ __forceinline__ void getv(float *o) const { dec(v, (uint16_t)(sc >> 16), o); }
+};
+// KIVI: tokens below qlen from the 2-bit groups, the rest from the fp16 ring.
+// Quantized token: x.x = K codes | V codes << 16 (8 channels x 2 bits each),
+// x.y = V (scale, min) of the channel group; y / z = K (scale, min) of the 8
+// channels.  Ring token: x = K halves, y = V halves.
+template <>
+struct KVRow<KvKivi> {
+    v4i_t x, y, z;
+    bool ring;
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int qlen) {
+        const int D = (int)a.tok_stride;
+        ring = t >= qlen;
+        if (ring) {
+            const size_t o = ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + 8 * c;
+            x = *(const v4i_t *)(a.rk + o);
+            y = *(const v4i_t *)(a.rv + o);
+        } else {
+            const size_t ro = ((size_t)kvh * a.S + t) * (D >> 2) + 2 * c;
+            const uint32_t kc = *(const uint16_t *)((const uint8_t *)a.kc + ro);
+            const uint32_t vc = *(const uint16_t *)((const uint8_t *)a.vc + ro);
+            x.x = (int)(kc | (vc << 16));
+            x.y = (int)a.vp[((size_t)kvh * a.S + t) * (D >> 5) + (c >> 2)];
+            const v4i_t *kp = (const v4i_t *)(a.kp + ((size_t)kvh * (a.S >> 5) + (t >> 5)) * D + 8 * c);
+            y = kp[0];
+            z = kp[1];
+        }
+    }
+    __device__ __forceinline__ void getk(float *o) const {
+        if (ring) {
+            h8_to_f32(x, o);
+        } else {
+            const uint32_t codes = (uint32_t)x.x;
+            const uint32_t sm[8] = {(uint32_t)y.x, (uint32_t)y.y, (uint32_t)y.z, (uint32_t)y.w,
+                                    (uint32_t)z.x, (uint32_t)z.y, (uint32_t)z.z, (uint32_t)z.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = kivi_deq((codes >> (2 * i)) & 3u, sm[i]);
+        }
+    }
+    __device__ __forceinline__ void getv(float *o) const {
+        if (ring) {
+            h8_to_f32(y, o);
+        } else {
+            const uint32_t codes = (uint32_t)x.x >> 16, sm = (uint32_t)x.y;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = kivi_deq((codes >> (2 * i)) & 3u, sm);
+        }
+    }
+};
+
+// The new token's row for the Q8 / KIVI decode step: every thread builds the
+// stored form of elements [8c, 8c+8) from the f32 QKV output (Q8: the four
+// lanes of a 32-block agree on its scale through DPP; KIVI: binary16), so the
+// thread that meets slot pos uses exactly what it stores.
+template <typename KT>
+struct NewRow {
+    __device__ __forceinline__ void build(const AttnArgs &, int, int) {}
+    __device__ __forceinline__ void apply(KVRow<KT> &) const {}
+    __device__ __forceinline__ void store(const AttnArgs &, int, int, int) const {}
+};
+__device__ __forceinline__ void q8_block8(const float *x, v2i_t &q, uint16_t &s) {
+    // quantize_input_q8_0_into arithmetic (model.rs:5557-5570) over a 32-block
+    // spread across 4 adjacent lanes (8 values each); scale stored as binary16
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(x[i]));
+    amax = row_max<4>(amax);
+    const float d = amax / 127.0f;
+    const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)sat_i8(roundf(x[i] * id)) << (8 * (i & 3));
+    q = v2i_t{(int)w[0], (int)w[1]};
+    s = f2h(d);
+}
+template <>
+struct NewRow<KvQ8> {
+    KVRow<KvQ8> r;
+    __device__ __forceinline__ void build(const AttnArgs &a, int kvh, int c) {
+        const int D = (int)a.tok_stride;
+        float kx[8], vx[8];
+        const v4f_t *kp = (const v4f_t *)(a.knew + kvh * D + 8 * c), *vp = (const v4f_t *)(a.vnew + kvh * D + 8 * c);
+        const v4f_t k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+        kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w; kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
+        vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w; vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+        uint16_t sk, sv;
+        q8_block8(kx, r.k, sk);
+        q8_block8(vx, r.v, sv);
+        r.sc = (uint32_t)sk | ((uint32_t)sv << 16);
+    }
+    __device__ __forceinline__ void apply(KVRow<KvQ8> &row) const { row = r; }
+    __device__ __forceinline__ void store(const AttnArgs &a, int kvh, int t, int c) const {
+        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
+        *(v2i_t *)((int8_t *)a.kc + o) = r.k;
+        *(v2i_t *)((int8_t *)a.vc + o) = r.v;
+        if ((c & 3) == 0) {
+            const size_t so = ((size_t)kvh * a.S + t) * (a.tok_stride >> 5) + (c >> 2);
+            a.ks[so] = (uint16_t)(r.sc & 0xFFFF);
+            a.vs[so] = (uint16_t)(r.sc >> 16);
         }
     }
 };
 template <>
-struct KVRaw<float> {
-    v4f_t a, b;
-    __device__ __forceinline__ void load(const float *p) {
-        a = ((const v4f_t *)p)[0];
-        b = ((const v4f_t *)p)[1];
+struct NewRow<KvKivi> {
+    v4i_t k, v;
+    __device__ __forceinline__ void build(const AttnArgs &a, int kvh, int c) {
+        const int D = (int)a.tok_stride;
+        float kx[8], vx[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            kx[i] = a.knew[kvh * D + 8 * c + i];
+            vx[i] = a.vnew[kvh * D + 8 * c + i];
+        }
+        k = f32_to_h8(kx);
+        v = f32_to_h8(vx);
     }
-    __device__ __forceinline__ void get(float *o) const {
-        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    __device__ __forceinline__ void apply(KVRow<KvKivi> &row) const {
+        row.ring = true;
+        row.x = k;
+        row.y = v;
+    }
+    __device__ __forceinline__ void store(const AttnArgs &a, int kvh, int t, int c) const {
+        const int D = (int)a.tok_stride;
+        const size_t o = ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + 8 * c;
+        *(v4i_t *)(a.rk + o) = k;
+        *(v4i_t *)(a.rv + o) = v;
     }
 };
+
+// Quantize KIVI group gi of kv head kvh (tokens [32gi, 32gi+32)) into the
+// 2-bit store.  src(t, ch) returns the fp16-rounded value of token t, channel
+// ch (is_v selects V).  Uses threads [0, D/4) for K (4 channels each, per
+// channel over the 32 tokens) and [128, 128 + D) for V (one token x one
+// 32-channel group each).  No barrier inside: the caller's threads run it once.
+template <typename Src>
+__device__ __forceinline__ void kivi_quantize_group(const AttnArgs &a, int D, int kvh, int gi, Src src) {
+    const int tid = threadIdx.x;
+    const int t0 = gi * kKiviGroup;
+    if (tid < D / 4) {
+        KiviQ qz[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float lo = INFINITY, hi = -INFINITY;
+            for (int t = 0; t < kKiviGroup; t++) {
+                const float v = src(t0 + t, 4 * tid + i, false);
+                lo = v < lo ? v : lo;
+                hi = v > hi ? v : hi;
+            }
+            qz[i].init(lo, hi);
+            a.kp[((size_t)kvh * (a.S >> 5) + gi) * D + 4 * tid + i] = qz[i].packed();
+        }
+        for (int t = 0; t < kKiviGroup; t++) {
+            uint32_t b = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) b |= qz[i].code(src(t0 + t, 4 * tid + i, false)) << (2 * i);
+            ((uint8_t *)a.kc)[((size_t)kvh * a.S + t0 + t) * (D >> 2) + tid] = (uint8_t)b;
+        }
+    } else if (tid >= 128 && tid < 128 + D) {
+        const int t = t0 + ((tid - 128) % kKiviGroup), cg = (tid - 128) / kKiviGroup;
+        float lo = INFINITY, hi = -INFINITY;
+        for (int i = 0; i < kKiviGroup; i++) {
+            const float v = src(t, 32 * cg + i, true);
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+        }
+        KiviQ qz;
+        qz.init(lo, hi);
+        a.vp[((size_t)kvh * a.S + t) * (D >> 5) + cg] = qz.packed();
+        uint32_t w[2] = {0u, 0u};
+        for (int i = 0; i < kKiviGroup; i++) w[i >> 4] |= qz.code(src(t, 32 * cg + i, true)) << (2 * (i & 15));
+        *(v2i_t *)((uint8_t *)a.vc + ((size_t)kvh * a.S + t) * (D >> 2) + 8 * cg) = v2i_t{(int)w[0], (int)w[1]};
+    }
+}
 
 constexpr int kAttnThreads = 256;  // 4 waves per workgroup
 constexpr int kAttnMaxSplit = 256; // splits per kv head
@@ -148,23 +390,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         qr[g][0] = q0.x; qr[g][1] = q0.y; qr[g][2] = q0.z; qr[g][3] = q0.w;
         qr[g][4] = q1.x; qr[g][5] = q1.y; qr[g][6] = q1.z; qr[g][7] = q1.w;
     }
-    const int T = *a.posp + 1;
+    const int pos = *a.posp, T = pos + 1;
     int CH = max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
     CH = (CH + TPP - 1) / TPP * TPP;
     const int t0 = s * CH;
     if (t0 >= T) return;
     const int t1 = min(T, t0 + CH);
     const int nact = (T + CH - 1) / CH;
-    const KT *kc = (const KT *)a.kc + (size_t)kvh * a.head_stride + c * 8;
-    const KT *vc = (const KT *)a.vc + (size_t)kvh * a.head_stride + c * 8;
+    const int qlen = kivi_qlen(T);
 
-    KVRaw<KT> kb[NP], vb[NP];
+    // the new token (Q8 / KIVI decode step) in its stored form
+    NewRow<KT> nrow;
+    const bool has_new = a.knew != nullptr;
+    if (has_new) nrow.build(a, kvh, c);
+
+    KVRow<KT> rows[NP];
     auto fetch = [&](int tb) {
 #pragma unroll
         for (int p = 0; p < NP; p++) {
-            const int t = min(tb + tk + p * TPP, t1 - 1);
-            kb[p].load(kc + (size_t)t * a.tok_stride);
-            vb[p].load(vc + (size_t)t * a.tok_stride);
+            const int tu = tb + tk + p * TPP;
+            const int t = min(tu, t1 - 1);
+            rows[p].load(a, kvh, t, c, qlen);
+            if (has_new && tu == pos) {
+                nrow.apply(rows[p]);
+                nrow.store(a, kvh, pos, c);
+            }
         }
     };
     fetch(t0);
@@ -186,7 +436,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int p = 0; p < NP; p++) {
             float kk[8];
-            kb[p].get(kk);
+            rows[p].getk(kk);
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 float d = 0.0f;
@@ -230,7 +480,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int p = 0; p < NP; p++) {
             float vv[8];
-            vb[p].get(vv);
+            rows[p].getv(vv);
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 const float pr = sc[g][tk + p * TPP];
@@ -244,6 +494,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         }
     }
     ATTN_TS(4);
+    if constexpr (std::is_same<KT, KvKivi>::value) {
+        // decode step T: the group that leaves the ring before step T+1 is
+        // quantized now (by split 0 of each kv head; no workgroup of this
+        // launch reads the 2-bit store of that group)
+        const int qn = kivi_qlen(T + 1);
+        if (has_new && s == 0 && qn > qlen) {
+            auto src = [&](int t, int ch, bool is_v) -> float {
+                const __half *r = is_v ? a.rv : a.rk;
+                return __half2float(r[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch]);
+            };
+            kivi_quantize_group(a, D, kvh, qn / kKiviGroup - 1, src);
+        }
+    }
     // reduce o over the WPT token rows of the wave, then over the waves
 #pragma unroll
     for (int g = 0; g < G; g++)

@@ -238,8 +238,14 @@ struct fl_ctx {
     fl_weight embed, output;
     bool tied = true;
     float *out_norm = nullptr;
-    void *kcache = nullptr, *vcache = nullptr;
-    size_t kv_layer_elems = 0;
+    void *kcache = nullptr, *vcache = nullptr;  // values (F32/F16) or codes (Q8/KIVI)
+    size_t kv_layer_elems = 0;                  // elements (F32/F16) or code bytes (Q8/KIVI) per layer
+    int kv_slots = 0;                           // slots per kv head (max_seq; a multiple of 32 for Q8/KIVI)
+    uint16_t *kscale = nullptr, *vscale = nullptr;  // Q8 scales [L][nkv][S][D/32]
+    uint32_t *kparam = nullptr, *vparam = nullptr;  // KIVI (scale, min): K [L][nkv][S/32][D], V [L][nkv][S][D/32]
+    __half *kring = nullptr, *vring = nullptr;      // KIVI fp16 ring [L][nkv][kKiviRing][D]
+    float *kvstage = nullptr;                       // host rows staged for fl_kv_write(_batch): 2 x cap x nkv*D
+    size_t kvstage_rows = 0;
     float *rope = nullptr;
     int nsplit = 1, chmin = 1;
     // activations
@@ -494,12 +500,29 @@ static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *
 }
 
 static int launch_attention(fl_ctx *ctx, int kv_format, int D, int G, AttnArgs &a) {
-    const hipError_t e = launch_attn(kv_format == FL_KV_F16, D, G, ctx->stream, a);
+    const hipError_t e = launch_attn(kv_format, D, G, ctx->stream, a);
     if (e == hipErrorNotSupported)
         return fail(ctx, FL_E_UNSUPPORTED, "attention: head_dim %d / group %d not supported", D, G);
     HIPCHK(ctx, e);
     HIPCHK(ctx, hipGetLastError());
     return 0;
+}
+
+// Algorithmic K+V bytes one decode attention launch reads over T tokens.
+static double attn_bytes(const fl_ctx *ctx, int T) {
+    const fl_model_config &c = ctx->cfg;
+    const double kvd = (double)c.num_kv_heads * c.head_dim;
+    switch (ctx->kv_format) {
+    case FL_KV_F32: return 2.0 * T * kvd * 4;
+    case FL_KV_F16: return 2.0 * T * kvd * 2;
+    case FL_KV_Q8: return 2.0 * T * (kvd + kvd / 32 * 2);
+    default: {
+        const int Q = kivi_qlen(T);
+        // codes (2 bits) + K (scale, min) per 32 tokens x channel + V (scale, min) per token x 32 channels
+        const double quant = 2.0 * Q * kvd / 4 + (Q / 32) * kvd * 4 + Q * (kvd / 32) * 4;
+        return quant + 2.0 * (T - Q) * kvd * 2;
+    }
+    }
 }
 
 static int ensure_part(fl_ctx *ctx, size_t floats) {
@@ -564,6 +587,11 @@ static void model_release(fl_ctx *c) {
     c->layers.clear();
     weight_release(c->embed);
     weight_release(c->output);
+    void *kvp[] = {c->kscale, c->vscale, c->kparam, c->vparam, c->kring, c->vring, c->kvstage};
+    for (void *p : kvp)
+        if (p) (void)hipFree(p);
+    c->kscale = c->vscale = nullptr; c->kparam = c->vparam = nullptr; c->kring = c->vring = nullptr;
+    c->kvstage = nullptr; c->kvstage_rows = 0;
     void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits, c->bench_out,
                     c->bench_trace,
                     c->aq, c->hq, c->as, c->hs, c->asum, c->hsum, c->st, c->tokens};
@@ -804,20 +832,44 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         c.intermediate_dim % 32 || c.vocab_size <= 0 || c.max_seq_len <= 0)
         return fail(ctx, FL_E_INVALID,
                     "unsupported config (hidden %% 32, head_dim 64/128, inter %% 32 required)");
-    if (kv_format != FL_KV_F16 && kv_format != FL_KV_F32) return fail(ctx, FL_E_UNSUPPORTED, "kv format %d", kv_format);
+    if (kv_format < FL_KV_F32 || kv_format > FL_KV_KIVI2) return fail(ctx, FL_E_UNSUPPORTED, "kv format %d", kv_format);
     if (!attn_supported(c.head_dim, c.num_heads / c.num_kv_heads))
         return fail(ctx, FL_E_UNSUPPORTED, "heads per kv group %d", c.num_heads / c.num_kv_heads);
     model_release(ctx);
     ctx->cfg = c;
     ctx->kv_format = kv_format;
     const size_t H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
-    const size_t F = c.intermediate_dim, S = c.max_seq_len, L = c.num_layers;
-    const size_t esz = kv_format == FL_KV_F16 ? 2 : 4;
-    ctx->kv_layer_elems = S * kvd;
-    ALLOC(ctx, ctx->kcache, L * S * kvd * esz);
-    ALLOC(ctx, ctx->vcache, L * S * kvd * esz);
-    HIPCHK(ctx, hipMemset(ctx->kcache, 0, L * S * kvd * esz));
-    HIPCHK(ctx, hipMemset(ctx->vcache, 0, L * S * kvd * esz));
+    const size_t F = c.intermediate_dim, L = c.num_layers, S = c.max_seq_len;
+    {
+        const bool quant = kv_format == FL_KV_Q8 || kv_format == FL_KV_KIVI2;
+        const size_t Sa = quant ? (S + 31) / 32 * 32 : S;
+        ctx->kv_slots = (int)Sa;
+        const size_t code_bytes = kv_format == FL_KV_F32 ? 4 * kvd : kv_format == FL_KV_F16 ? 2 * kvd
+                                : kv_format == FL_KV_Q8 ? kvd : kvd / 4;  // per token
+        ctx->kv_layer_elems = kv_format <= FL_KV_F16 ? Sa * kvd : Sa * code_bytes;
+        ALLOC(ctx, ctx->kcache, L * Sa * code_bytes);
+        ALLOC(ctx, ctx->vcache, L * Sa * code_bytes);
+        HIPCHK(ctx, hipMemset(ctx->kcache, 0, L * Sa * code_bytes));
+        HIPCHK(ctx, hipMemset(ctx->vcache, 0, L * Sa * code_bytes));
+        if (kv_format == FL_KV_Q8) {
+            const size_t n = L * Sa * (kvd / 32) * 2;
+            ALLOC(ctx, ctx->kscale, n);
+            ALLOC(ctx, ctx->vscale, n);
+            HIPCHK(ctx, hipMemset(ctx->kscale, 0, n));
+            HIPCHK(ctx, hipMemset(ctx->vscale, 0, n));
+        }
+        if (kv_format == FL_KV_KIVI2) {
+            const size_t nk = L * (Sa / 32) * kvd * 4, nv = L * Sa * (kvd / 32) * 4, nr = L * kKiviRing * kvd * 2;
+            ALLOC(ctx, ctx->kparam, nk);
+            ALLOC(ctx, ctx->vparam, nv);
+            ALLOC(ctx, ctx->kring, nr);
+            ALLOC(ctx, ctx->vring, nr);
+            HIPCHK(ctx, hipMemset(ctx->kparam, 0, nk));
+            HIPCHK(ctx, hipMemset(ctx->vparam, 0, nv));
+            HIPCHK(ctx, hipMemset(ctx->kring, 0, nr));
+            HIPCHK(ctx, hipMemset(ctx->vring, 0, nr));
+        }
+    }
     // RoPE table for every position (RopeTable::new formula, host libm)
     const int half = c.head_dim / 2;
     std::vector<float> tab(2 * S * half);
@@ -931,16 +983,20 @@ int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *con
     return 0;
 }
 
+static void kv_layer_args(fl_ctx *ctx, int l, AttnArgs &a);
+
 int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const float *value) {
     if (!ctx || !key || !value) return fail(ctx, FL_E_INVALID, "null argument");
     if (!ctx->have_cfg) return fail(ctx, FL_E_STATE, "no kv cache");
     const fl_model_config &c = ctx->cfg;
     if (layer < 0 || layer >= c.num_layers) return fail(ctx, FL_E_INVALID, "layer %d", layer);
+    if (ctx->kv_format == FL_KV_Q8 || ctx->kv_format == FL_KV_KIVI2)
+        return fl_kv_write_batch(ctx, layer, position, 1, key, value);
     const int slot = position % c.max_seq_len;  // ring write (GpuKvCache::write)
     const size_t hd = (size_t)c.head_dim;
     // device layout is head-major: [layer][kv_head][slot][head_dim]
     for (int h = 0; h < c.num_kv_heads; h++) {
-        const size_t off = (size_t)layer * ctx->kv_layer_elems + ((size_t)h * c.max_seq_len + slot) * hd;
+        const size_t off = (size_t)layer * ctx->kv_layer_elems + ((size_t)h * ctx->kv_slots + slot) * hd;
         if (ctx->kv_format == FL_KV_F32) {
             HIPCHK(ctx, hipMemcpy((float *)ctx->kcache + off, key + h * hd, hd * 4, hipMemcpyHostToDevice));
             HIPCHK(ctx, hipMemcpy((float *)ctx->vcache + off, value + h * hd, hd * 4, hipMemcpyHostToDevice));
@@ -957,17 +1013,85 @@ int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const fl
     return 0;
 }
 
+int fl_kv_write_batch(fl_ctx *ctx, int layer, int pos0, int n, const float *keys, const float *values) {
+    if (!ctx || !keys || !values) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_cfg) return fail(ctx, FL_E_STATE, "no kv cache");
+    const fl_model_config &c = ctx->cfg;
+    if (layer < 0 || layer >= c.num_layers) return fail(ctx, FL_E_INVALID, "layer %d", layer);
+    if (n <= 0 || pos0 < 0 || pos0 + n > c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "rows [%d, %d) outside the cache (max_seq_len %d)", pos0, pos0 + n,
+                    c.max_seq_len);
+    const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
+    // stage the rows (at most 4096 per launch pair), then quantize on the device
+    const int chunk = 4096;
+    const size_t cap = (size_t)std::min(n, chunk);
+    if (ctx->kvstage_rows < cap) {
+        if (ctx->kvstage) (void)hipFree(ctx->kvstage);
+        ctx->kvstage = nullptr;
+        ctx->kvstage_rows = 0;
+        ALLOC(ctx, ctx->kvstage, 2 * cap * kvd * 4);
+        ctx->kvstage_rows = cap;
+    }
+    AttnArgs a{};
+    kv_layer_args(ctx, layer, a);
+    for (int r0 = 0; r0 < n; r0 += chunk) {
+        const int m = std::min(chunk, n - r0);
+        float *kd = ctx->kvstage, *vd = ctx->kvstage + ctx->kvstage_rows * kvd;
+        HIPCHK(ctx, hipMemcpyAsync(kd, keys + (size_t)r0 * kvd, (size_t)m * kvd * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIPCHK(ctx, hipMemcpyAsync(vd, values + (size_t)r0 * kvd, (size_t)m * kvd * 4, hipMemcpyHostToDevice,
+                                   ctx->stream));
+        HIPCHK(ctx, launch_kv_write(ctx->kv_format, ctx->stream, a, kd, vd, pos0 + r0, m, c.head_dim));
+        HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // the staging buffer is reused
+    }
+    return 0;
+}
+
 int fl_reset(fl_ctx *ctx) {
     if (!ctx || !ctx->have_cfg) return fail(ctx, FL_E_STATE, "no model");
     const fl_model_config &c = ctx->cfg;
-    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
-    const size_t bytes = (size_t)c.num_layers * ctx->kv_layer_elems * esz;
+    const size_t L = c.num_layers, Sa = ctx->kv_slots, kvd = (size_t)c.num_kv_heads * c.head_dim;
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : ctx->kv_format == FL_KV_F32 ? 4 : 1;
+    const size_t bytes = L * ctx->kv_layer_elems * esz;
     HIPCHK(ctx, hipMemsetAsync(ctx->kcache, 0, bytes, ctx->stream));
     HIPCHK(ctx, hipMemsetAsync(ctx->vcache, 0, bytes, ctx->stream));
+    if (ctx->kscale) {
+        HIPCHK(ctx, hipMemsetAsync(ctx->kscale, 0, L * Sa * (kvd / 32) * 2, ctx->stream));
+        HIPCHK(ctx, hipMemsetAsync(ctx->vscale, 0, L * Sa * (kvd / 32) * 2, ctx->stream));
+    }
+    if (ctx->kparam) {
+        HIPCHK(ctx, hipMemsetAsync(ctx->kparam, 0, L * (Sa / 32) * kvd * 4, ctx->stream));
+        HIPCHK(ctx, hipMemsetAsync(ctx->vparam, 0, L * Sa * (kvd / 32) * 4, ctx->stream));
+        HIPCHK(ctx, hipMemsetAsync(ctx->kring, 0, L * kKiviRing * kvd * 2, ctx->stream));
+        HIPCHK(ctx, hipMemsetAsync(ctx->vring, 0, L * kKiviRing * kvd * 2, ctx->stream));
+    }
     HIPCHK(ctx, hipMemsetAsync(ctx->st, 0, sizeof(DevState), ctx->stream));
     HIPCHK(ctx, hipMemsetAsync(ctx->d_counters, 0, 1024 * 4, ctx->stream));
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
     return 0;
+}
+
+// Cache planes of layer l (every KV format), head-major with kv_slots slots
+// per kv head.
+static void kv_layer_args(fl_ctx *ctx, int l, AttnArgs &a) {
+    const fl_model_config &c = ctx->cfg;
+    const size_t D = c.head_dim, kvd = (size_t)c.num_kv_heads * D, Sa = ctx->kv_slots;
+    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : ctx->kv_format == FL_KV_F32 ? 4 : 1;
+    a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
+    a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
+    a.tok_stride = (long long)D;
+    a.head_stride = (long long)(Sa * D);
+    a.nkv = c.num_kv_heads;
+    a.S = (int)Sa;
+    if (ctx->kscale) {
+        a.ks = ctx->kscale + (size_t)l * Sa * (kvd / 32);
+        a.vs = ctx->vscale + (size_t)l * Sa * (kvd / 32);
+    }
+    if (ctx->kparam) {
+        a.kp = ctx->kparam + (size_t)l * (Sa / 32) * kvd;
+        a.vp = ctx->vparam + (size_t)l * Sa * (kvd / 32);
+        a.rk = ctx->kring + (size_t)l * kKiviRing * kvd;
+        a.rv = ctx->vring + (size_t)l * kKiviRing * kvd;
+    }
 }
 
 // Enqueue one decode step (kernels only; no host synchronisation).
@@ -975,15 +1099,10 @@ int fl_reset(fl_ctx *ctx) {
 // (q from the fused QKV output, RoPE already applied by its epilogue).
 static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
     const fl_model_config &c = ctx->cfg;
-    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
     AttnArgs a{};
+    kv_layer_args(ctx, l, a);
     a.q = ctx->qkv;
-    a.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
-    a.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
-    a.tok_stride = c.head_dim;
-    a.head_stride = (long long)c.max_seq_len * c.head_dim;
     a.posp = &ctx->st->pos;
-    a.nkv = c.num_kv_heads;
     a.nsplit = ctx->nsplit;
     a.chmin = ctx->chmin;
     a.part = ctx->d_part;
@@ -992,6 +1111,12 @@ static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
     a.oq = ctx->aq;
     a.os = ctx->as;
     a.osum = ctx->asum;
+    if (ctx->kv_format == FL_KV_Q8 || ctx->kv_format == FL_KV_KIVI2) {
+        // the QKV epilogue leaves the new K / V rows (f32) after q
+        const size_t qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
+        a.knew = ctx->qkv + qd;
+        a.vnew = ctx->qkv + qd + kvd;
+    }
     return a;
 }
 
@@ -999,18 +1124,22 @@ static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
 // this layer's cache slot.
 static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
     const fl_model_config &c = ctx->cfg;
-    const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
+    AttnArgs a{};
+    kv_layer_args(ctx, l, a);
     QkvEpi e{};
     e.rope = ctx->rope;
     e.sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
     e.posp = &ctx->st->pos;
-    e.kc = (uint8_t *)ctx->kcache + (size_t)l * ctx->kv_layer_elems * esz;
-    e.vc = (uint8_t *)ctx->vcache + (size_t)l * ctx->kv_layer_elems * esz;
-    e.head_stride = (long long)c.max_seq_len * c.head_dim;
+    e.kc = (void *)a.kc;
+    e.vc = (void *)a.vc;
+    e.head_stride = a.head_stride;
     e.nq = c.num_heads * c.head_dim;
     e.nk = c.num_kv_heads * c.head_dim;
     e.hd = c.head_dim;
     e.kv_f16 = ctx->kv_format == FL_KV_F16;
+    // Q8 / KIVI: K (after RoPE) and V stay f32 in the output after q; the
+    // attention kernel quantizes and stores them
+    e.kv_stage = ctx->kv_format == FL_KV_Q8 || ctx->kv_format == FL_KV_KIVI2;
     return e;
 }
 
@@ -1201,6 +1330,56 @@ int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out) {
     return 0;
 }
 
+int fl_gqa_from_cache(fl_ctx *ctx, int layer, const float *q, int seq_len, float *out) {
+    if (!ctx || !q || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_cfg) return fail(ctx, FL_E_STATE, "no kv cache");
+    const fl_model_config &c = ctx->cfg;
+    if (layer < 0 || layer >= c.num_layers) return fail(ctx, FL_E_INVALID, "layer %d", layer);
+    if (seq_len <= 0 || seq_len > c.max_seq_len) return fail(ctx, FL_E_INVALID, "seq_len %d", seq_len);
+    const size_t qd = (size_t)c.num_heads * c.head_dim;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->qkv, q, qd * 4, hipMemcpyHostToDevice, ctx->stream));
+    const int pos = seq_len - 1;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->d_pos, &pos, 4, hipMemcpyHostToDevice, ctx->stream));
+    AttnArgs a{};
+    kv_layer_args(ctx, layer, a);
+    a.q = ctx->qkv;
+    a.posp = ctx->d_pos;
+    a.nsplit = ctx->nsplit;
+    a.chmin = ctx->chmin;
+    a.part = ctx->d_part;
+    a.counters = ctx->d_counters;
+    a.out = ctx->attn;
+    int rc = launch_attention(ctx, ctx->kv_format, c.head_dim, c.num_heads / c.num_kv_heads, a);
+    if (rc) return rc;
+    HIPCHK(ctx, hipMemcpyAsync(out, ctx->attn, qd * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_launch) {
+    if (!ctx || !ctx->have_cfg) return fail(ctx, FL_E_STATE, "no kv cache");
+    const fl_model_config &c = ctx->cfg;
+    if (seq_len <= 0 || seq_len > c.max_seq_len) return fail(ctx, FL_E_INVALID, "seq_len %d", seq_len);
+    const int pos = seq_len - 1;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->d_pos, &pos, 4, hipMemcpyHostToDevice, ctx->stream));
+    for (int i = 0; i < iters; i++) {
+        AttnArgs a{};
+        kv_layer_args(ctx, i % c.num_layers, a);
+        a.q = ctx->qkv;
+        a.posp = ctx->d_pos;
+        a.nsplit = ctx->nsplit;
+        a.chmin = ctx->chmin;
+        a.part = ctx->d_part;
+        a.counters = ctx->d_counters;
+        a.out = ctx->attn;
+        const int rc = launch_attention(ctx, ctx->kv_format, c.head_dim, c.num_heads / c.num_kv_heads, a);
+        if (rc) return rc;
+    }
+    if (bytes_per_launch) *bytes_per_launch = attn_bytes(ctx, seq_len);
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // pos staged from the host stack
+    return 0;
+}
+
 // Launch `iters` copies of one layer kernel on the context stream, cycling
 // through the layers.
 int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, double *bytes_per_launch) {
@@ -1278,8 +1457,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
     if (bytes_per_launch && which == 5) {
         DevState st{};
         HIPCHK(ctx, hipMemcpy(&st, ctx->st, sizeof st, hipMemcpyDeviceToHost));
-        const size_t esz = ctx->kv_format == FL_KV_F16 ? 2 : 4;
-        *bytes_per_launch = 2.0 * (st.pos + 1) * c.num_kv_heads * c.head_dim * esz;
+        *bytes_per_launch = attn_bytes(ctx, st.pos + 1);
     } else if (bytes_per_launch && w) {
         *bytes_per_launch = (double)w->gguf_bytes;
     }

@@ -79,6 +79,11 @@ hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 hipError_t launch_mvs_f32(int fmt, const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 hipError_t launch_mvs_gu_q8_0(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
-hipError_t launch_attn(bool f16, int D, int G, hipStream_t st, const AttnArgs &a);
+enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2, KV_KIVI = 3 };  // == FL_KV_*
+hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a);
+// Write n token rows (device f32 [n][nkv][D]) at positions p0.. into a Q8 or
+// KIVI cache (quantizing the KIVI groups that leave the ring).
+hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
+                           int p0, int n, int D);
 
 }  // namespace fl

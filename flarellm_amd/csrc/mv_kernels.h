@@ -23,6 +23,7 @@ struct QkvEpi {
     int nq, nk;         // q rows (Nq*D) and k rows (Nkv*D); v rows follow
     int hd;             // head_dim
     int kv_f16;         // cache element: 1 = binary16 (RNE), 0 = f32
+    int kv_stage;       // 1: K (after RoPE) and V go to the output after q, as f32
 };
 
 #ifdef FLARE_MV_TRACE
@@ -284,6 +285,10 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
             const int h = n / D;
             q[h * D + i] = y0;
             q[h * D + i + half] = y1;
+        } else if (e.kv_stage) {
+            const int k0 = (n - e.nq) - j;  // start of this kv head's row
+            q[e.nq + k0 + i] = y0;
+            q[e.nq + k0 + i + half] = y1;
         } else {
             const int kvh = (n - e.nq) / D;
             const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D;
@@ -298,6 +303,11 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
     } else {
         // v rows keep their original order
         const int vi = n - e.nq - e.nk, kvh = vi / D, d = vi % D;
+        if (e.kv_stage) {
+            q[e.nq + e.nk + vi] = x0;
+            q[e.nq + e.nk + vi + 1] = x1;
+            return;
+        }
         const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D + d;
         if (e.kv_f16) {
             ((uint16_t *)e.vc)[off] = f2h(x0);

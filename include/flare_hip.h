@@ -56,6 +56,21 @@ extern "C" {
  * F16 = flare-gpu GpuKvCache f16 (flare-gpu/src/kv_cache.rs:51-66). */
 #define FL_KV_F32 0
 #define FL_KV_F16 1
+/* Q8: int8 + binary16 scale per 32 values of a (token, kv head) row, the
+ * quantize_input_q8_0_into arithmetic (model.rs:5557-5570).  The reference
+ * README lists a Q8 KV cache (README.md:70) with no implementation; this is the
+ * long-context benchmark's form. */
+#define FL_KV_Q8 2
+/* KIVI 2-bit in the long-context benchmark's form: K quantized per channel over groups
+ * of 32 tokens, V per token over groups of 32 channels, with the
+ * quantize_to_packed arithmetic of flare-core/src/kv_cache.rs:336-371
+ * ((max-min)/3, round, clamp 0..3, 4 codes per byte LSB first) and
+ * (scale, min) kept as binary16.  The newest tokens stay binary16 in a
+ * 160-slot ring: tokens [0, Q) come from the 2-bit groups and [Q, T) from the
+ * ring, Q = 32*floor((T-129)/32) for T > 128 (else 0).  The reference's own
+ * QuantizedKvCache (kv_cache.rs:35-323: 32-token f32 window, per-token K codes
+ * read with running per-channel stats) is not reproduced. */
+#define FL_KV_KIVI2 3
 
 typedef struct fl_ctx fl_ctx;
 typedef struct fl_weight fl_weight;
@@ -160,6 +175,17 @@ int fl_has_kv_cache(const fl_ctx *ctx);
 /* gpu_kv_write (model.rs:287): store one token's K and V (host floats,
  * num_kv_heads*head_dim each) at ring slot `position` of `layer`. */
 int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const float *value);
+/* Write n consecutive token rows (host floats, [n][num_kv_heads*head_dim]
+ * each for K and V) at positions pos0..pos0+n-1 of `layer`: gpu_kv_write
+ * (model.rs:287) for n rows at once.  Q8 rows are quantized on the device;
+ * KIVI rows enter the ring and the groups that leave it are quantized. */
+int fl_kv_write_batch(fl_ctx *ctx, int layer, int pos0, int n, const float *keys, const float *values);
+/* grouped_query_attention_from_gpu_cache (model.rs:311): decode attention of
+ * one query token (host floats, num_heads*head_dim, RoPE applied) over slots
+ * 0..seq_len-1 of `layer`'s cache; writes num_heads*head_dim host floats.
+ * seq_len must be the number of tokens written (the KIVI ring holds only the
+ * newest ones). */
+int fl_gqa_from_cache(fl_ctx *ctx, int layer, const float *q, int seq_len, float *out);
 /* Model::reset / KvCache::clear (model.rs:1591, kv_cache.rs:534-545). */
 int fl_reset(fl_ctx *ctx);
 /* forward_greedy (model.rs:1872-1942) when out_logits == NULL, else
@@ -190,6 +216,11 @@ int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out);
  * bytes of one launch (GGUF weight bytes; K+V bytes for attention) to
  * *bytes_per_launch.  No counterpart in the reference: measurement only. */
 int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, double *bytes_per_launch);
+/* Enqueue `iters` decode attention launches over slots 0..seq_len-1 (layer
+ * i % num_layers, the query left by the last fl_gqa_from_cache / decode step)
+ * and synchronise; writes the algorithmic K+V bytes of one launch.  Needs no
+ * weights.  Measurement only. */
+int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_launch);
 /* Name of the device kernel fl_bench_layer_kernel launches for `which`. */
 const char *fl_bench_kernel_name(fl_ctx *ctx, int which);
 

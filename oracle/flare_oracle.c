@@ -444,6 +444,70 @@ void or_kivi_quantize_to_packed(const float *v, size_t n, uint8_t *packed, float
     *min_out = mn;
 }
 
+/* ---- KV forms of the long-context attention benchmark ------------------- */
+/* No reference implementation exists (README.md:70 lists a Q8 KV cache; the
+ * KIVI variant of the benchmark differs from QuantizedKvCache): the
+ * arithmetic follows quantize_input_q8_0_into (model.rs:5557-5570, via
+ * or_quantize_input_q8_0) and quantize_to_packed (kv_cache.rs:332-371, via
+ * or_kivi_quantize_to_packed); stored scales are binary16 (RNE). */
+#define KIVI_GROUP 32
+#define KIVI_RESIDUAL 128
+
+size_t or_kivi32_qlen(size_t T) {
+    if (T <= KIVI_RESIDUAL + 1) return 0;
+    return KIVI_GROUP * ((T - 1 - KIVI_RESIDUAL) / KIVI_GROUP);
+}
+
+static float h16(float x) { return or_f16_to_f32(or_f32_to_f16_rne(x)); }
+
+/* quantize n values (gathered with stride) and write back their binary16-
+ * scale dequantization code * scale + min (kv_cache.rs:384-392 order) */
+static void kivi_group_roundtrip(float *v, size_t n, size_t stride) {
+    float buf[KIVI_GROUP];
+    uint8_t packed[KIVI_GROUP / 4];
+    float scale, mn;
+    for (size_t i = 0; i < n; i++) buf[i] = v[i * stride];
+    or_kivi_quantize_to_packed(buf, n, packed, &scale, &mn);
+    float sh = h16(scale), mh = h16(mn);
+    for (size_t i = 0; i < n; i++) {
+        float code = (float)((packed[i / 4] >> ((i % 4) * 2)) & 3);
+        v[i * stride] = code * sh + mh;
+    }
+}
+
+void or_kv_view(int kv_mode, const float *K, const float *V, size_t T, size_t nkv, size_t D,
+                float *Kout, float *Vout) {
+    size_t kvd = nkv * D, n = T * kvd;
+    if (kv_mode == OR_KV_Q8) {
+        float sc[1];
+        int8_t q[32];
+        for (size_t b = 0; b < n / 32; b++) {
+            for (int w = 0; w < 2; w++) {
+                const float *src = (w ? V : K) + 32 * b;
+                float *dst = (w ? Vout : Kout) + 32 * b;
+                or_quantize_input_q8_0(src, 32, sc, q);
+                float d = h16(sc[0]);
+                for (int i = 0; i < 32; i++) dst[i] = (float)q[i] * d;
+            }
+        }
+        return;
+    }
+    for (size_t i = 0; i < n; i++) {
+        Kout[i] = kv_mode == OR_KV_F32 ? K[i] : h16(K[i]);
+        Vout[i] = kv_mode == OR_KV_F32 ? V[i] : h16(V[i]);
+    }
+    if (kv_mode != OR_KV_KIVI32) return;
+    size_t Q = or_kivi32_qlen(T);
+    for (size_t g = 0; g < Q / KIVI_GROUP; g++) {
+        size_t t0 = g * KIVI_GROUP;
+        for (size_t ch = 0; ch < kvd; ch++) /* K: per channel over the 32 tokens */
+            kivi_group_roundtrip(Kout + t0 * kvd + ch, KIVI_GROUP, kvd);
+        for (size_t t = t0; t < t0 + KIVI_GROUP; t++) /* V: per token over 32 channels */
+            for (size_t cg = 0; cg < kvd / KIVI_GROUP; cg++)
+                kivi_group_roundtrip(Vout + t * kvd + cg * KIVI_GROUP, KIVI_GROUP, 1);
+    }
+}
+
 /* ======================================================================= */
 /* Whole-model greedy decode: flare-core/src/model.rs:1872-1942            */
 /* (forward_greedy) and 1955-2561 (forward_layers), x86 flags:             */
@@ -528,6 +592,8 @@ or_model *or_model_create(const or_config *cfg, const or_layer *layers,
             k->rk[l] = (float *)calloc(k->res_len * kvd, sizeof(float));
             k->rv[l] = (float *)calloc(k->res_len * kvd, sizeof(float));
         }
+    }
+    if (cfg->kv_mode == OR_KV_KIVI2 || cfg->kv_mode == OR_KV_Q8 || cfg->kv_mode == OR_KV_KIVI32) {
         m->kdq = (float *)calloc(S * kvd, sizeof(float));
         m->vdq = (float *)calloc(S * kvd, sizeof(float));
     }
@@ -563,8 +629,8 @@ void or_model_destroy(or_model *m) {
         }
         free(k->kp); free(k->vp); free(k->ks); free(k->kmin);
         free(k->vs); free(k->vmin); free(k->rk); free(k->rv);
-        free(m->kdq); free(m->vdq);
     }
+    free(m->kdq); free(m->vdq);
     if (m->out_f32 && m->out_f32 != m->embed_f32) free(m->out_f32);
     free(m->embed_f32);
     free(m->layers);
@@ -700,6 +766,10 @@ static void forward_layers(or_model *m, uint32_t token, size_t pos) {
         size_t seq_len = m->length + 1; /* model.rs:2209 */
         if (c->kv_mode == OR_KV_KIVI2) {
             kivi_dequant(m, l, m->kdq, m->vdq);
+            or_gqa_attention(m->q, m->kdq, m->vdq, nh, nkv, hd, seq_len, m->attn);
+        } else if (c->kv_mode == OR_KV_Q8 || c->kv_mode == OR_KV_KIVI32) {
+            /* rows 0..seq_len-1 as written (no ring wrap: seq_len <= max_seq) */
+            or_kv_view(c->kv_mode, m->kc[l], m->vc[l], seq_len, nkv, hd, m->kdq, m->vdq);
             or_gqa_attention(m->q, m->kdq, m->vdq, nh, nkv, hd, seq_len, m->attn);
         } else {
             or_gqa_attention(m->q, m->kc[l], m->vc[l], nh, nkv, hd, seq_len, m->attn);

@@ -27,7 +27,7 @@ extern "C" {
 /* WeightFormat subset on the hot path (flare-core/src/model.rs WeightFormat). */
 enum { OR_F32 = 0, OR_Q8_0 = 1, OR_Q4K = 2, OR_Q6K = 3 };
 /* KV cache storage modes (see or_model_create). */
-enum { OR_KV_F32 = 0, OR_KV_F16 = 1, OR_KV_KIVI2 = 2 };
+enum { OR_KV_F32 = 0, OR_KV_F16 = 1, OR_KV_KIVI2 = 2, OR_KV_Q8 = 3, OR_KV_KIVI32 = 4 };
 
 /* ---- scalar codecs ---------------------------------------------------- */
 float or_f16_to_f32(uint16_t bits);
@@ -76,6 +76,19 @@ void or_gqa_attention(const float *q, const float *k_cache, const float *v_cache
 /* ---- KIVI 2-bit cache helpers (reference semantics) -------------------- */
 void or_kivi_quantize_to_packed(const float *v, size_t n, uint8_t *packed, float *scale,
                                 float *minv);
+
+/* ---- KV forms of the long-context attention benchmark ------------------
+ * OR_KV_Q8: every (token, kv head) row quantized per 32 values with the
+ * quantize_input_q8_0_into arithmetic and the scale rounded to binary16.
+ * OR_KV_KIVI32: rows rounded to binary16; tokens below
+ * or_kivi32_qlen(T) replaced by their 2-bit group dequantization (K per
+ * channel over 32 tokens, V per token over 32 channels, quantize_to_packed
+ * arithmetic, (scale, min) rounded to binary16). */
+size_t or_kivi32_qlen(size_t T);
+/* Rows K, V: token-major [T][nkv][D] f32 as written.  Writes the values a
+ * decode attention over T tokens reads, same layout. */
+void or_kv_view(int kv_mode, const float *K, const float *V, size_t T, size_t nkv, size_t D,
+                float *Kout, float *Vout);
 
 /* ---- whole-model greedy decode ----------------------------------------- */
 typedef struct {

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 OR_F32, OR_Q8_0, OR_Q4K, OR_Q6K = 0, 1, 2, 3
-OR_KV_F32, OR_KV_F16, OR_KV_KIVI2 = 0, 1, 2
+OR_KV_F32, OR_KV_F16, OR_KV_KIVI2, OR_KV_Q8, OR_KV_KIVI32 = 0, 1, 2, 3, 4
 
 
 def build() -> str:
@@ -64,6 +64,8 @@ def lib() -> C.CDLL:
             "or_silu_mul": (None, [vp, vp, sz, vp]),
             "or_gqa_attention": (None, [vp, vp, vp, sz, sz, sz, sz, vp]),
             "or_kivi_quantize_to_packed": (None, [vp, sz, vp, C.POINTER(f32), C.POINTER(f32)]),
+            "or_kivi32_qlen": (sz, [sz]),
+            "or_kv_view": (None, [C.c_int, vp, vp, sz, sz, sz, vp, vp]),
             "or_model_create": (vp, [C.POINTER(Config), C.POINTER(Layer), vp, vp, vp]),
             "or_model_destroy": (None, [vp]),
             "or_model_reset": (None, [vp]),
@@ -109,6 +111,22 @@ def unpack_q4k_scales(raw12: bytes):
     buf = (C.c_uint8 * 12)(*raw12)
     lib().or_unpack_q4k_scales(buf, sc, mn)
     return list(sc), list(mn)
+
+
+def kivi32_qlen(T: int) -> int:
+    return int(lib().or_kivi32_qlen(T))
+
+
+def kv_view(kv_mode: int, K: np.ndarray, V: np.ndarray):
+    """The K/V values a decode attention over all T rows of K, V ([T, nkv, D])
+    reads in cache form kv_mode (OR_KV_F32 / F16 / Q8 / KIVI32)."""
+    K = np.ascontiguousarray(K, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    T, nkv, D = K.shape
+    Ko = np.empty_like(K)
+    Vo = np.empty_like(V)
+    lib().or_kv_view(kv_mode, _p(K), _p(V), T, nkv, D, _p(Ko), _p(Vo))
+    return Ko, Vo
 
 
 def quantize_q8(x: np.ndarray):

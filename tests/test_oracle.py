@@ -535,3 +535,131 @@ def test_q6k_layout_probes(oracle):
         half, k = divmod(sidx, 8)
         start = half * 128 + (k // 2) * 32 + (k % 2) * 16
         assert list(changed) == list(range(start, start + 16)), sidx
+
+
+# ---- KV forms of the long-context attention benchmark (Q8, KIVI 2-bit) ------
+# No reference implementation exists for these forms; they are pinned by
+# closed forms, the quantize_to_packed known answers of kv_cache.rs's own
+# tests (exact codes 0..3, constant input -> no NaN) and error bounds.
+
+def test_kivi32_qlen_closed_form(oracle):
+    assert [oracle.kivi32_qlen(T) for T in (1, 128, 129, 130, 160, 161, 192, 193)] == [0, 0, 0, 0, 0, 32, 32, 64]
+    for T in range(1, 2000):
+        Q = oracle.kivi32_qlen(T)
+        assert Q % 32 == 0 and Q <= T
+        if T > 128:
+            assert 129 <= T - Q <= 160  # the fp16 window always holds the newest 128 tokens (+ <= 32)
+
+
+def _kv_rows(seed, T, nkv, D, std=1.0):
+    from flarellm_amd import synth as S
+
+    K = S.normal(seed, 0, T * nkv * D, 0.0, std).reshape(T, nkv, D)
+    V = S.normal(seed, 1 << 40, T * nkv * D, 0.0, std).reshape(T, nkv, D)
+    return K, V
+
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def test_kv_view_identity_forms(oracle):
+    K, V = _kv_rows(3, 40, 2, 64)
+    Ko, Vo = oracle.kv_view(oracle.OR_KV_F32, K, V)
+    assert np.array_equal(Ko, K) and np.array_equal(Vo, V)
+    Ko, Vo = oracle.kv_view(oracle.OR_KV_F16, K, V)
+    assert np.array_equal(Ko, _f16(K)) and np.array_equal(Vo, _f16(V))
+
+
+def test_kv_view_q8_closed_forms(oracle):
+    T, nkv, D = 9, 2, 64
+    K, V = _kv_rows(4, T, nkv, D)
+    K[0, 0, :32] = 0.0                    # zero block -> zeros (d = 0, id = 0)
+    K[1, 0, :32] = 0.75                   # constant block -> 127 * f16(0.75/127)
+    K[2, 1, 32:] = np.linspace(-1, 1, 32)  # amax element -> +-127 codes
+    Ko, Vo = oracle.kv_view(oracle.OR_KV_Q8, K, V)
+    assert np.all(Ko[0, 0, :32] == 0.0)
+    assert np.all(Ko[1, 0, :32] == np.float32(127.0) * _f16(np.float32(0.75) / np.float32(127.0)))
+    d = _f16(np.float32(1.0) / np.float32(127.0))
+    assert Ko[2, 1, 32] == -127 * d and Ko[2, 1, 63] == 127 * d
+    # every value within half a step (+ the binary16 rounding of the step)
+    for X, Xo in ((K, Ko), (V, Vo)):
+        blk = X.reshape(-1, 32)
+        amax = np.abs(blk).max(axis=1, keepdims=True)
+        step = _f16(amax / 127.0)
+        err = np.abs(Xo.reshape(-1, 32) - blk)
+        assert np.all(err <= step / 2 + 127 * np.abs(step - amax / 127.0) + 1e-7)
+        # the values are integer multiples of the stored step
+        k = Xo.reshape(-1, 32) / np.where(step == 0, 1, step)
+        assert np.allclose(k, np.round(k), atol=1e-4) and np.abs(np.round(k)).max() <= 127
+
+
+def test_kv_view_kivi_window_and_groups(oracle):
+    for T in (100, 160, 161, 200, 300):
+        K, V = _kv_rows(5, T, 2, 64)
+        Ko, Vo = oracle.kv_view(oracle.OR_KV_KIVI32, K, V)
+        Q = oracle.kivi32_qlen(T)
+        # the fp16 window is exact binary16
+        assert np.array_equal(Ko[Q:], _f16(K[Q:])) and np.array_equal(Vo[Q:], _f16(V[Q:]))
+        for g in range(Q // 32):
+            kg = _f16(K[32 * g:32 * g + 32])       # [32 tokens, nkv, D]
+            ko = Ko[32 * g:32 * g + 32]
+            # K per channel: 4 levels spanning [min, max] of the channel's 32 values
+            for h in range(2):
+                for ch in range(0, 64, 7):
+                    col, out = kg[:, h, ch], ko[:, h, ch]
+                    assert len(np.unique(out)) <= 4
+                    step = (col.max() - col.min()) / 3
+                    assert np.abs(out - col).max() <= step / 2 + 2e-3 * (np.abs(col).max() + step)
+                    assert abs(out.min() - col.min()) <= 1e-3 * max(1.0, abs(col.min()))
+            # V per token over 32-channel groups
+            vg = _f16(V[32 * g:32 * g + 32]).reshape(32, -1, 32)
+            vo = Vo[32 * g:32 * g + 32].reshape(32, -1, 32)
+            for t in range(0, 32, 5):
+                for cg in range(vg.shape[1]):
+                    row, out = vg[t, cg], vo[t, cg]
+                    assert len(np.unique(out)) <= 4
+                    step = (row.max() - row.min()) / 3
+                    assert np.abs(out - row).max() <= step / 2 + 2e-3 * (np.abs(row).max() + step)
+
+
+def test_kv_view_kivi_exact_levels_and_constant(oracle):
+    # kv_cache.rs test_quantized_value_per_token_dequant_accuracy: values
+    # 0,1,2,3 map to codes 0..3 exactly; test_quantized_constant_values_no_nan:
+    # a constant group (range 0, scale 0) dequantizes to the constant.
+    T, nkv, D = 200, 1, 64
+    K = np.zeros((T, nkv, D), np.float32)
+    V = np.zeros((T, nkv, D), np.float32)
+    levels = np.array([0.0, 1.0, 2.0, 3.0], np.float32)
+    K[:32, 0, :] = levels[np.arange(32) % 4][:, None]       # per channel over tokens: 0,1,2,3,...
+    V[:32, 0, :] = levels[np.arange(64) % 4][None, :]       # per token over channels
+    K[32:64] = 42.0
+    V[32:64] = 42.0
+    Ko, Vo = oracle.kv_view(oracle.OR_KV_KIVI32, K, V)
+    assert oracle.kivi32_qlen(T) == 64
+    assert np.array_equal(Ko[:64], K[:64]) and np.array_equal(Vo[:64], V[:64])
+    assert not np.isnan(Ko).any() and not np.isnan(Vo).any()
+
+
+def test_model_kv_quantized_modes_close_to_f32(oracle):
+    """Whole-model oracle in Q8 / KIVI32 modes past the first quantized KIVI
+    group: the logits stay finite and near the F32-cache logits (the KV
+    quantization error is bounded; a dropped or misplaced term would not be)."""
+    from flarellm_amd import FL_Q8_0
+    from flarellm_amd import synth as S
+
+    spec = S.tiny_spec(FL_Q8_0, max_seq=256)
+    model = S.make_model(spec, seed=9)
+    prompt = S.random_tokens(19, 170, spec.vocab)
+
+    def last_logits(mode):
+        om = oracle.OracleModel(model, mode)
+        for pos, t in enumerate(prompt[:-1]):
+            om.forward_greedy(int(t), pos)
+        return om.forward_logits(int(prompt[-1]), len(prompt) - 1)
+
+    b = last_logits(oracle.OR_KV_F32)
+    for mode, tol in ((oracle.OR_KV_Q8, 0.05), (oracle.OR_KV_KIVI32, 0.5)):
+        a = last_logits(mode)
+        rel = np.linalg.norm(a - b) / np.linalg.norm(b)
+        assert np.isfinite(a).all() and 0 < rel < tol, (mode, rel)
