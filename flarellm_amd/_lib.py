@@ -65,6 +65,7 @@ SIGNATURES = {
     "fl_op_rmsnorm": (i32, [vp, vp, vp, i32, f32, vp]),
     "fl_op_matvec_q8in": (i32, [vp, vp, vp, vp, vp, vp]),
     "fl_op_matvec_f32in": (i32, [vp, vp, vp, vp]),
+    "fl_op_batched_matvec_q8in": (i32, [vp, vp, i32, vp, vp, vp, vp]),
     "fl_op_block_dots": (i32, [vp, vp, vp, vp]),
     "fl_op_dequant": (i32, [vp, vp, vp]),
     "fl_op_matvec_argmax": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
@@ -86,6 +87,7 @@ SIGNATURES = {
     "fl_decode_step": (i32, [vp, C.c_uint32, i32, vp, C.POINTER(C.c_int32), C.POINTER(f32)]),
     "fl_generate": (i32, [vp, vp, i32, i32, vp]),
     "fl_decode_continue": (i32, [vp, i32]),
+    "fl_verify": (i32, [vp, vp, i32, i32, vp, vp]),
     "fl_read_tokens": (i32, [vp, i32, i32, vp]),
     "fl_bench_layer_kernel": (i32, [vp, i32, i32, i32, C.POINTER(C.c_double)]),
     "fl_bench_kernel_name": (C.c_char_p, [vp, i32]),

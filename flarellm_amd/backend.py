@@ -132,6 +132,18 @@ class HipBackend:
         self.sync()
         return out
 
+    def batched_matvec_q8in(self, w: Weight, q, s, su):
+        """batched_dequant_matmul (model.rs:740) over n pre-quantized rows:
+        q [n, cols] int8, s / su [n, cols/32] -> [n, rows] f32."""
+        import torch
+
+        n = q.shape[0]
+        out = torch.empty((n, w.rows), dtype=torch.float32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_batched_matvec_q8in(self.ctx, w.handle, n, _ptr(q), _ptr(s), _ptr(su), _ptr(out)),
+              self.ctx)
+        return out
+
     def matvec_f32in(self, w: Weight, x):
         import torch
 
@@ -280,6 +292,16 @@ class HipBackend:
         out = np.empty(n_gen, np.uint32)
         check(self.lib.fl_generate(self.ctx, prompt.ctypes.data, prompt.size, n_gen, out.ctypes.data), self.ctx)
         return out
+
+    def verify(self, tokens, pos0: int):
+        """Speculative verify of draft tokens at pos0.. in one pass: the greedy
+        token after each draft (and its logit)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(tokens.size, np.int32)
+        vals = np.empty(tokens.size, np.float32)
+        check(self.lib.fl_verify(self.ctx, tokens.ctypes.data, tokens.size, pos0, out.ctypes.data,
+                                 vals.ctypes.data), self.ctx)
+        return out, vals
 
     def decode_continue(self, n_steps: int):
         """Enqueue n_steps more device-resident greedy steps (asynchronous)."""

@@ -4,10 +4,10 @@
 namespace fl {
 
 template <typename KT>
-static hipError_t launch_attn_t(int D, int G, hipStream_t st, const AttnArgs &a) {
+static hipError_t launch_attn_t(int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
 #define C(DD, GG)                                                                                  \
     if (D == DD && G == GG) {                                                                      \
-        hipLaunchKernelGGL((k_attn<KT, DD, GG>), dim3(a.nsplit, a.nkv), dim3(kAttnThreads), 0, st, a); \
+        hipLaunchKernelGGL((k_attn<KT, DD, GG>), dim3(a.nsplit, a.nkv, nq), dim3(kAttnThreads), 0, st, a); \
         return hipSuccess;                                                                         \
     }
     C(64, 1) C(64, 2) C(64, 3) C(64, 4) C(64, 8)
@@ -16,13 +16,14 @@ static hipError_t launch_attn_t(int D, int G, hipStream_t st, const AttnArgs &a)
     return hipErrorNotSupported;
 }
 
-hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a) {
-    if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit) return hipErrorInvalidValue;
+hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
+    if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit || nq < 1) return hipErrorInvalidValue;
+    if (nq > 1 && a.knew) return hipErrorInvalidValue;  // new-token stores are single-query
     switch (kvfmt) {
-    case KV_F32: return launch_attn_t<float>(D, G, st, a);
-    case KV_F16: return launch_attn_t<__half>(D, G, st, a);
-    case KV_Q8: return launch_attn_t<KvQ8>(D, G, st, a);
-    case KV_KIVI: return launch_attn_t<KvKivi>(D, G, st, a);
+    case KV_F32: return launch_attn_t<float>(D, G, st, a, nq);
+    case KV_F16: return launch_attn_t<__half>(D, G, st, a, nq);
+    case KV_Q8: return launch_attn_t<KvQ8>(D, G, st, a, nq);
+    case KV_KIVI: return launch_attn_t<KvKivi>(D, G, st, a, nq);
     }
     return hipErrorNotSupported;
 }

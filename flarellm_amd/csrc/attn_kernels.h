@@ -40,13 +40,20 @@ struct AttnArgs {
     // cache slot *posp by the workgroup whose chunk holds it.  nullptr when
     // the cache was written beforehand (fl_kv_write).
     const float *knew, *vnew;
+    // several query tokens (speculative verify): grid z = query index; query
+    // z sits at position *posp + z and attends slots 0..*posp+z (causal).
+    // q / out / oq advance by qstride / ostride floats per query; split
+    // partials and counters have one set per query.
+    int qstride, ostride;
 };
 
 // KIVI 2-bit cache constants: groups of 32 (K per channel over 32 tokens, V
 // per token over 32 channels); the newest tokens stay in an fp16 ring.
 constexpr int kKiviGroup = 32;
 constexpr int kKiviResidual = 128;  // at least this many newest tokens are fp16
-constexpr int kKiviRing = kKiviResidual + kKiviGroup;  // ring slots per kv head
+// ring slots per kv head: the window plus two groups, so a verify batch of up
+// to 32 tokens still finds every query's window tokens in the ring
+constexpr int kKiviRing = kKiviResidual + 2 * kKiviGroup;
 // Tokens [0, kivi_qlen(T)) of a T-token cache are read from the 2-bit groups,
 // [kivi_qlen(T), T) from the ring (between 129 and 160 tokens once T > 128).
 __host__ __device__ inline int kivi_qlen(int T) {
@@ -369,7 +376,20 @@ __host__ __device__ constexpr int attn_round(int D) { return attn_tpp(D) * attn_
 // nsplit > 1: (m, l, o) partials are published with agent-scope stores and
 // the last workgroup of the kv head merges them (flash-decode rescale).
 template <typename KT, int D, int G>
-__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a0) {
+    AttnArgs a = a0;
+    const int zq = (int)blockIdx.z;
+    if (zq) {
+        a.q += (size_t)zq * a.qstride;
+        if (a.out) a.out += (size_t)zq * a.ostride;
+        if (a.oq) {
+            a.oq += (size_t)zq * a.ostride;
+            a.os += (size_t)zq * (a.ostride / 32);
+            a.osum += (size_t)zq * (a.ostride / 32);
+        }
+        a.part += (size_t)zq * a.nkv * a.nsplit * G * (D + 2);
+        a.counters += (size_t)zq * a.nkv;
+    }
     constexpr int LPT = attn_lpt(D), TPP = attn_tpp(D), NP = attn_np(D), CR = TPP * NP;
     constexpr int NW = kAttnThreads / 64, WPT = 64 / LPT;  // token rows per wave per pass
     __shared__ float sc[G][CR];
@@ -390,7 +410,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         qr[g][0] = q0.x; qr[g][1] = q0.y; qr[g][2] = q0.z; qr[g][3] = q0.w;
         qr[g][4] = q1.x; qr[g][5] = q1.y; qr[g][6] = q1.z; qr[g][7] = q1.w;
     }
-    const int pos = *a.posp, T = pos + 1;
+    const int pos = *a.posp + zq, T = pos + 1;
     int CH = max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
     CH = (CH + TPP - 1) / TPP * TPP;
     const int t0 = s * CH;

@@ -260,6 +260,15 @@ struct fl_ctx {
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     bool graph_ready = false;
+    // speculative verify buffers (allocated on first fl_verify)
+    bool have_verify = false;
+    float *vx = nullptr, *vq = nullptr, *vk = nullptr, *vv = nullptr, *vpart = nullptr;
+    int8_t *vxq = nullptr, *vaq = nullptr;
+    float *vxs = nullptr, *vas = nullptr;
+    int *vxsum = nullptr, *vasum = nullptr;
+    int *vtok = nullptr, *vpos = nullptr;
+    unsigned long long *vslots = nullptr;
+    size_t vpart_floats = 0;
 };
 
 static std::string g_err;
@@ -600,6 +609,13 @@ static void model_release(fl_ctx *c) {
     c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
     c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
+    void *vp[] = {c->vx, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
+                  c->vtok, c->vpos, c->vslots};
+    for (void *p : vp)
+        if (p) (void)hipFree(p);
+    c->vx = c->vq = c->vk = c->vv = c->vpart = nullptr; c->vxq = c->vaq = nullptr; c->vxs = c->vas = nullptr;
+    c->vxsum = c->vasum = nullptr; c->vtok = c->vpos = nullptr; c->vslots = nullptr; c->vpart_floats = 0;
+    c->have_verify = false;
     c->have_cfg = c->have_weights = false;
 }
 
@@ -1377,6 +1393,189 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
     }
     if (bytes_per_launch) *bytes_per_launch = attn_bytes(ctx, seq_len);
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));  // pos staged from the host stack
+    return 0;
+}
+
+// ---- speculative verify -------------------------------------------------------
+
+constexpr int kVerifyMaxKsplit = 16;
+
+static int verify_alloc(fl_ctx *ctx) {
+    if (ctx->have_verify) return 0;
+    const fl_model_config &c = ctx->cfg;
+    const size_t M = kVerifyMaxTokens, H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim;
+    const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, F = c.intermediate_dim;
+    const size_t kmax = std::max({H, qd, F});
+    const size_t rmax = std::max({qd + 2 * kvd, 2 * F, H});
+    ALLOC(ctx, ctx->vx, M * H * 4);
+    ALLOC(ctx, ctx->vq, M * qd * 4);
+    ALLOC(ctx, ctx->vk, M * kvd * 4);
+    ALLOC(ctx, ctx->vv, M * kvd * 4);
+    ctx->vpart_floats = (size_t)kVerifyMaxKsplit * M * rmax;
+    ALLOC(ctx, ctx->vpart, ctx->vpart_floats * 4);
+    ALLOC(ctx, ctx->vxq, M * kmax);
+    ALLOC(ctx, ctx->vxs, M * (kmax / 32) * 4);
+    ALLOC(ctx, ctx->vxsum, M * (kmax / 32) * 4);
+    ALLOC(ctx, ctx->vaq, M * qd);
+    ALLOC(ctx, ctx->vas, M * (qd / 32) * 4);
+    ALLOC(ctx, ctx->vasum, M * (qd / 32) * 4);
+    ALLOC(ctx, ctx->vtok, M * 4);
+    ALLOC(ctx, ctx->vpos, 4);
+    ALLOC(ctx, ctx->vslots, M * 8);
+    ctx->have_verify = true;
+    return 0;
+}
+
+// K chunks of a verify GEMM: about 2048 waves (one 16-row tile x one chunk
+// each), at most kVerifyMaxKsplit.
+static int verify_ksplit(const fl_weight &w) {
+    const int tiles = (w.rows + 15) / 16;
+    const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
+    const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (2048 + tiles - 1) / tiles}));
+    // every chunk non-empty: the reducers sum all ksplit partial sets
+    const int chunk = (units + want - 1) / want;
+    return (units + chunk - 1) / chunk;
+}
+
+static int verify_gemm(fl_ctx *ctx, const fl_weight &w, int M, const int8_t *xq, const float *xs, const int *xsum,
+                       int &ksplit) {
+    VgArgs a{};
+    a.W = w.desc();
+    a.xq = xq;
+    a.xs = xs;
+    a.xsum = xsum;
+    a.M = M;
+    a.ksplit = ksplit = verify_ksplit(w);
+    a.part = ctx->vpart;
+    if ((size_t)ksplit * M * w.rows > ctx->vpart_floats) return fail(ctx, FL_E_INVALID, "verify partials too small");
+    const hipError_t e = launch_vgemm(w.format, ctx->stream, a);
+    if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "no verify GEMM for format %d", w.format);
+    HIPCHK(ctx, e);
+    return 0;
+}
+
+int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q, const float *scales,
+                               const int32_t *sums, float *out) {
+    if (!ctx || !w || !q || !scales || !sums || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n_tokens < 1 || n_tokens > kVerifyMaxTokens)
+        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kVerifyMaxTokens);
+    if (w->format != FL_Q8_0 && w->format != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
+    // partials of this op live in their own buffer (sized for this weight)
+    const int ks = verify_ksplit(*w);
+    const size_t need = (size_t)ks * n_tokens * w->rows;
+    float *part = nullptr;
+    ALLOC(ctx, part, need * 4);
+    VgArgs a{};
+    a.W = w->desc();
+    a.xq = q;
+    a.xs = scales;
+    a.xsum = sums;
+    a.M = n_tokens;
+    a.ksplit = ks;
+    a.part = part;
+    hipError_t e = launch_vgemm(w->format, ctx->stream, a);
+    if (e == hipSuccess) e = launch_v_store(ctx->stream, part, ks, n_tokens, w->rows, out);
+    const hipError_t e2 = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(part);
+    HIPCHK(ctx, e);
+    HIPCHK(ctx, e2);
+    return 0;
+}
+
+int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
+    if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    const int M = n_tokens;
+    if (M < 1 || M > kVerifyMaxTokens) return fail(ctx, FL_E_INVALID, "verify batch of %d tokens (1..%d)", M, kVerifyMaxTokens);
+    if (pos0 < 0 || pos0 + M > c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "positions [%d, %d) outside the KV cache (max_seq_len %d)", pos0, pos0 + M,
+                    c.max_seq_len);
+    if (M * c.num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
+    for (int i = 0; i < M; i++)
+        if ((int)tokens[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", tokens[i]);
+    int rc = verify_alloc(ctx);
+    if (rc) return rc;
+    const int H = c.hidden_dim, D = c.head_dim, G = c.num_heads / c.num_kv_heads;
+    const int qd = c.num_heads * D, kvd = c.num_kv_heads * D, F = c.intermediate_dim;
+    const float eps = c.rms_norm_eps;
+    const int pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
+    hipStream_t st = ctx->stream;
+    std::vector<int> tk(tokens, tokens + M);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data(), (size_t)M * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, &pos0, 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
+    rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (D + 2));
+    if (rc) return rc;
+    HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, ctx->vx));
+    for (int l = 0; l < c.num_layers; l++) {
+        Layer &L = ctx->layers[l];
+        int ks;
+        // attention block (model.rs:2016-2311), M tokens at positions pos0..pos0+M-1
+        HIPCHK(ctx, launch_v_normquant(pro, st, ctx->vx, L.attn_norm, eps, H, M, ctx->vxq, ctx->vxs, ctx->vxsum));
+        rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+        if (rc) return rc;
+        HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, qd, kvd, D, ctx->rope,
+                                      (long long)c.max_seq_len * (D / 2), ctx->vpos, ctx->vq, ctx->vk, ctx->vv));
+        AttnArgs a{};
+        kv_layer_args(ctx, l, a);
+        HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D));
+        a.q = ctx->vq;
+        a.posp = ctx->vpos;
+        a.nsplit = ctx->nsplit;
+        a.chmin = ctx->chmin;
+        a.part = ctx->d_part;
+        a.counters = ctx->d_counters;
+        a.out = nullptr;
+        a.oq = ctx->vaq;
+        a.os = ctx->vas;
+        a.osum = ctx->vasum;
+        a.qstride = qd;
+        a.ostride = qd;
+        {
+            const hipError_t e = launch_attn(ctx->kv_format, D, G, st, a, M);
+            if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "attention shape");
+            HIPCHK(ctx, e);
+        }
+        rc = verify_gemm(ctx, L.wo, M, ctx->vaq, ctx->vas, ctx->vasum, ks);
+        if (rc) return rc;
+        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, ctx->vx));
+        // FFN block (model.rs:2376-2543)
+        HIPCHK(ctx, launch_v_normquant(pro, st, ctx->vx, L.ffn_norm, eps, H, M, ctx->vxq, ctx->vxs, ctx->vxsum));
+        rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+        if (rc) return rc;
+        HIPCHK(ctx, launch_v_silu_quant(st, ctx->vpart, ks, M, F, ctx->vxq, ctx->vxs, ctx->vxsum));
+        rc = verify_gemm(ctx, L.down, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+        if (rc) return rc;
+        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, ctx->vx));
+    }
+    // output projection + fused argmax per token (forward_greedy, model.rs:1898-1932)
+    const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
+    const bool q8out = !ctx->tied && ((O.format == FL_Q8_0 && ctx->layer_fmt == FL_Q8_0) ||
+                                      (O.format == FL_Q4K && ctx->layer_fmt == FL_Q4K));
+    for (int t = 0; t < M; t++) {
+        const float *xt = ctx->vx + (size_t)t * H;
+        if (q8out) {
+            rc = launch_q8in(ctx, O, PRO_NORMQ1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, nullptr, nullptr,
+                             nullptr, ctx->vslots + t);
+        } else {
+            if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
+            rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, ctx->vslots + t);
+        }
+        if (rc) return rc;
+    }
+    std::vector<unsigned long long> keys(M);
+    HIPCHK(ctx, hipMemcpyAsync(keys.data(), ctx->vslots, (size_t)M * 8, hipMemcpyDeviceToHost, st));
+    HIPCHK(ctx, hipStreamSynchronize(st));
+    for (int t = 0; t < M; t++) {
+        const unsigned long long k = keys[t];
+        out_tokens[t] = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+        if (out_vals) {
+            uint32_t u = (uint32_t)(k >> 32);
+            u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+            std::memcpy(&out_vals[t], &u, 4);
+        }
+    }
     return 0;
 }
 

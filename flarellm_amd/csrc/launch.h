@@ -8,6 +8,7 @@
 
 #include "attn_kernels.h"
 #include "mvs_kernels.h"
+#include "verify_args.h"
 
 namespace fl {
 
@@ -80,10 +81,23 @@ hipError_t launch_mvs_f32(int fmt, const MvsPlan &p, hipStream_t st, const MvsAr
 hipError_t launch_mvs_gu_q8_0(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2, KV_KIVI = 3 };  // == FL_KV_*
-hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a);
+hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq = 1);
 // Write n token rows (device f32 [n][nkv][D]) at positions p0.. into a Q8 or
 // KIVI cache (quantizing the KIVI groups that leave the ring).
 hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
                            int p0, int n, int D);
+
+// speculative verify (verify.hip)
+hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a);
+hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *tokens, int M, float *x);
+hipError_t launch_v_normquant(int pro, hipStream_t st, const float *x, const float *w, float eps, int n, int M,
+                              int8_t *q, float *s, int *sum);
+hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
+                             const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
+                             float *Vst);
+hipError_t launch_v_store(hipStream_t st, const float *part, int ksplit, int M, int rows, float *out);
+hipError_t launch_v_residual(hipStream_t st, const float *part, int ksplit, int M, int H, float *x);
+hipError_t launch_v_silu_quant(hipStream_t st, const float *part, int ksplit, int M, int F, int8_t *q, float *s,
+                               int *sum);
 
 }  // namespace fl

@@ -1,0 +1,74 @@
+// Speculative-verify launchers (kernels in verify_kernels.h).
+#include "launch.h"
+#include "verify_kernels.h"
+
+namespace fl {
+
+hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
+    const int tiles = (a.W.rows + 15) / 16;
+    const dim3 grid((tiles + 3) / 4, a.ksplit);
+    if (a.M < 1 || a.M > kVerifyMaxTokens || a.ksplit < 1) return hipErrorInvalidValue;
+    if (a.W.cols % 32) return hipErrorInvalidValue;
+    size_t kn;
+    if (fmt == F_Q4K) {
+        if (a.W.cols % 256) return hipErrorInvalidValue;
+        const int nsb = a.W.cols >> 8;
+        kn = (size_t)((nsb + a.ksplit - 1) / a.ksplit) * 256;
+        const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+        hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);
+    } else {
+        if (fmt != F_Q8_0) return hipErrorNotSupported;
+        const int nb = a.W.cols >> 5;
+        kn = (size_t)((nb + a.ksplit - 1) / a.ksplit) * 32;
+        const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+        hipLaunchKernelGGL(k_vgemm_q8_0, grid, dim3(256), lds, st, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *tokens, int M, float *x) {
+    switch (fmt) {
+    case F_Q8_0: hipLaunchKernelGGL(k_v_embed<F_Q8_0>, dim3(M), dim3(256), 0, st, E, tokens, x); break;
+    case F_Q6K: hipLaunchKernelGGL(k_v_embed<F_Q6K>, dim3(M), dim3(256), 0, st, E, tokens, x); break;
+    case F_Q4K: hipLaunchKernelGGL(k_v_embed<F_Q4K>, dim3(M), dim3(256), 0, st, E, tokens, x); break;
+    default: hipLaunchKernelGGL(k_v_embed<F_F32>, dim3(M), dim3(256), 0, st, E, tokens, x); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_v_normquant(int pro, hipStream_t st, const float *x, const float *w, float eps, int n, int M,
+                              int8_t *q, float *s, int *sum) {
+    if (pro == PRO_NORMQ0)
+        hipLaunchKernelGGL(k_v_normquant<PRO_NORMQ0>, dim3(M), dim3(256), 0, st, x, w, eps, n, q, s, sum);
+    else
+        hipLaunchKernelGGL(k_v_normquant<PRO_NORMQ1>, dim3(M), dim3(256), 0, st, x, w, eps, n, q, s, sum);
+    return hipGetLastError();
+}
+
+hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
+                             const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
+                             float *Vst) {
+    const dim3 grid((rows / 2 + 255) / 256, M);
+    hipLaunchKernelGGL(k_v_qkv_post, grid, dim3(256), 0, st, part, ksplit, M, rows, nq, nk, D, rope, sin_off, pos0p, Q,
+                       Kst, Vst);
+    return hipGetLastError();
+}
+
+hipError_t launch_v_store(hipStream_t st, const float *part, int ksplit, int M, int rows, float *out) {
+    hipLaunchKernelGGL(k_v_store, dim3((rows + 255) / 256, M), dim3(256), 0, st, part, ksplit, M, rows, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_v_residual(hipStream_t st, const float *part, int ksplit, int M, int H, float *x) {
+    hipLaunchKernelGGL(k_v_residual, dim3((H + 255) / 256, M), dim3(256), 0, st, part, ksplit, M, H, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_v_silu_quant(hipStream_t st, const float *part, int ksplit, int M, int F, int8_t *q, float *s,
+                               int *sum) {
+    if (F % 32) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_v_silu_quant, dim3((F + 255) / 256, M), dim3(256), 0, st, part, ksplit, M, F, q, s, sum);
+    return hipGetLastError();
+}
+
+}  // namespace fl

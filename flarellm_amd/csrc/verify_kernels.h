@@ -1,0 +1,258 @@
+// Speculative-verify batch (M <= 16 draft tokens through the model in one
+// pass): quantized GEMMs on int8 MFMA plus the per-token glue kernels.
+//
+// The reference verifies drafts one forward pass at a time
+// (Generator::speculative_step, flare-core/src/generate.rs:244-312) and runs
+// batched projections as one quantized matvec per token
+// (CpuBackend::batched_dequant_matmul, flare-core/src/model.rs:740-1036: each
+// row quantized by quantize_input_q8_0_into, then the single-token
+// per-block integer dots).  Here the M tokens share each weight read: one
+// v_mfma_i32_16x16x32_i8 forms the exact 32-value block dot of 16 weight rows
+// with all M tokens at once, and the fp32 block terms follow the reference's
+// per-block formulas.
+#pragma once
+
+#include "verify_args.h"
+
+namespace fl {
+
+// LDS staging of one K chunk: int8 activations of the M tokens, then
+// (scale, block sum as float) pairs.
+template <int FMT>
+__device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t *lx, float2 *lsc) {
+    const int K = a.W.cols, nb = kn >> 5, b0 = k0 >> 5;
+    for (int i = threadIdx.x; i < a.M * (kn >> 3); i += blockDim.x) {
+        const int t = i / (kn >> 3), o = (i % (kn >> 3)) * 8;
+        *(i64x1_t *)(lx + t * kn + o) = *(const i64x1_t *)(a.xq + (size_t)t * K + k0 + o);
+    }
+    for (int i = threadIdx.x; i < a.M * nb; i += blockDim.x) {
+        const int t = i / nb, b = i % nb;
+        lsc[t * nb + b] = make_float2(a.xs[(size_t)t * (K >> 5) + b0 + b], (float)a.xsum[(size_t)t * (K >> 5) + b0 + b]);
+    }
+    __syncthreads();
+}
+
+// D[token][row] = sum_k X[token][k] * W[row][k] for one 32-value block.
+// Lane l: A = X[t = l%16][8*(l/16) .. +8], B = W[row = l%16][8*(l/16) .. +8],
+// D[i] = token 4*(l/16)+i, row l%16.
+__device__ __forceinline__ v4i32_t vg_mfma(i64x1_t a, i64x1_t b) {
+    const v4i32_t z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+// Q8_0 weights: unit = one 32-block.  Block term of matvec_q8_0_preq_into
+// (model.rs:8082-8099): (f16(w_scale) * x_scale) * (int dot as f32).
+__global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const WDesc &W = a.W;
+    const int K = W.cols, nbk = K >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = (nbk + a.ksplit - 1) / a.ksplit;
+    const int b0 = blockIdx.y * chunk, b1 = min(nbk, b0 + chunk);
+    if (b0 >= b1) return;
+    const int kn = (b1 - b0) * 32;
+    int8_t *lx = (int8_t *)smem;
+    float2 *lsc = (float2 *)(smem + ((kVerifyMaxTokens * kn + 15) & ~15));
+    vg_stage<F_Q8_0>(a, b0 * 32, kn, lx, lsc);
+    const int tile = blockIdx.x * 4 + wave;
+    if (tile * 16 >= W.rows) return;
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int row = min(n, W.rows - 1);
+    const int nbc = b1 - b0;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const int8_t *wq = (const int8_t *)W.q + (size_t)row * K + 8 * kg;
+    const uint16_t *ws = W.s + (size_t)row * nbk;
+    i64x1_t wn = *(const i64x1_t *)(wq + 32 * b0);
+    uint16_t sn = ws[b0];
+    for (int b = b0; b < b1; b++) {
+        const i64x1_t wcur = wn;
+        const uint16_t scur = sn;
+        if (b + 1 < b1) {
+            wn = *(const i64x1_t *)(wq + 32 * (b + 1));
+            sn = ws[b + 1];
+        }
+        const int bl = b - b0;
+        const i64x1_t x = tA < a.M ? *(const i64x1_t *)(lx + tA * kn + 32 * bl + 8 * kg) : 0;
+        const v4i32_t d = vg_mfma(x, wcur);
+        const float wsc = h2f(scur);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * kg + i;
+            if (t < a.M) acc[i] += (wsc * lsc[t * nbc + bl].x) * (float)d[i];
+        }
+    }
+    if (n < W.rows) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * kg + i;
+            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[i];
+        }
+    }
+}
+
+// Q4_K weights (flarellm layout): unit = one 256-value super-block, 8 MFMAs
+// (sub-block j: low nibbles of qs[32j..32j+32) for j < 4, high nibbles of
+// qs[32(j-4)..] for j >= 4).  Block term of dot_q4k_q8_0_scalar
+// (model.rs:8969-9025): s_x * (d*sc*dot - dmin*mn*sum(q_x)).
+__global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const WDesc &W = a.W;
+    const int K = W.cols, nsb = K >> 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = (nsb + a.ksplit - 1) / a.ksplit;
+    const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
+    if (s0 >= s1) return;
+    const int kn = (s1 - s0) * 256, nbc = kn >> 5;
+    int8_t *lx = (int8_t *)smem;
+    float2 *lsc = (float2 *)(smem + ((kVerifyMaxTokens * kn + 15) & ~15));
+    vg_stage<F_Q4K>(a, s0 * 256, kn, lx, lsc);
+    const int tile = blockIdx.x * 4 + wave;
+    if (tile * 16 >= W.rows) return;
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int row = min(n, W.rows - 1);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t *qs = W.q + (size_t)row * nsb * 128 + 8 * kg;
+    const uint8_t *hd = W.h + (size_t)row * nsb * 16;
+    auto load = [&](int sb, i64x1_t *w, v4i_t &h) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) w[jj] = *(const i64x1_t *)(qs + (size_t)sb * 128 + 32 * jj);
+        h = *(const v4i_t *)(hd + (size_t)sb * 16);
+    };
+    i64x1_t wn[4];
+    v4i_t hn;
+    load(s0, wn, hn);
+    for (int sb = s0; sb < s1; sb++) {
+        i64x1_t w[4];
+        const v4i_t h = hn;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) w[jj] = wn[jj];
+        if (sb + 1 < s1) load(sb + 1, wn, hn);
+        const uint32_t h0 = (uint32_t)h.x;
+        const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+        const int sl = sb - s0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int jj = j & 3;
+            const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
+            const i64x1_t wb = j < 4 ? (w[jj] & m4) : ((w[jj] >> 4) & m4);
+            const i64x1_t x = tA < a.M ? *(const i64x1_t *)(lx + tA * kn + sl * 256 + 32 * j + 8 * kg) : 0;
+            const v4i32_t dd = vg_mfma(x, wb);
+            // unpack_q4k_scales (model.rs:8709-8719), flare packing
+            const uint32_t sa = byte_of((uint32_t)h.y, jj), sbb = byte_of((uint32_t)h.z, jj),
+                           scc = byte_of((uint32_t)h.w, jj);
+            const uint32_t sc = j < 4 ? (sa & 63) : ((sa >> 6) | ((scc & 0xF) << 2));
+            const uint32_t mn = j < 4 ? (sbb & 63) : ((sbb >> 6) | ((scc >> 4) << 2));
+            const float dsc = d * (float)sc, dmn = dmin * (float)mn;
+            const int bl = sl * 8 + j;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 4 * kg + i;
+                if (t < a.M) {
+                    const float2 xs = lsc[t * nbc + bl];
+                    acc[i] += xs.x * (dsc * (float)dd[i] - dmn * xs.y);
+                }
+            }
+        }
+    }
+    if (n < W.rows) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * kg + i;
+            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[i];
+        }
+    }
+}
+
+// ---- per-token glue ------------------------------------------------------
+
+__device__ __forceinline__ float vsum_part(const float *part, int ksplit, int M, int rows, int t, int n) {
+    float v = 0.0f;
+    for (int k = 0; k < ksplit; k++) v += part[((size_t)k * M + t) * rows + n];
+    return v;
+}
+
+// Embedding rows of the M tokens (token_embedding lookup, model.rs:1964).
+template <int FMT>
+__global__ __launch_bounds__(256) void k_v_embed(WDesc E, const int *tokens, float *x) {
+    const int t = blockIdx.x, H = E.cols;
+    const int row = min(max(tokens[t], 0), E.rows - 1);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v;
+        if (FMT == F_Q8_0) v = (float)((const int8_t *)E.q)[(size_t)row * H + i] * h2f(E.s[(size_t)row * (H >> 5) + (i >> 5)]);
+        else if (FMT == F_Q6K) v = q6k_elem(E, row, i);
+        else if (FMT == F_Q4K) v = q4k_elem(E, row, i);
+        else v = ((const float *)E.q)[(size_t)row * H + i];
+        x[(size_t)t * H + i] = v;
+    }
+}
+
+// Per token: RMSNorm + Q8_0 quantization (the decode prologue's arithmetic,
+// stage_q8; PRO_NORMQ0 / PRO_NORMQ1).
+template <int PRO>
+__global__ __launch_bounds__(256) void k_v_normquant(const float *x, const float *w, float eps, int n, int8_t *q,
+                                                     float *s, int *sum) {
+    __shared__ float red[8];
+    const int t = blockIdx.x;
+    stage_q8<PRO>(x + (size_t)t * n, w, eps, n, nullptr, nullptr, nullptr, q + (size_t)t * n, s + (size_t)t * (n >> 5),
+                  sum + (size_t)t * (n >> 5), red);
+}
+
+// QKV partials -> per token: RoPE (apply_rope_with_table, model.rs:7283-7296)
+// on the pair-interleaved q / k rows at position pos0 + t; q to Q[t], K / V
+// rows (f32) to the staging rows written into the cache afterwards.
+__global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int ksplit, int M, int rows, int nq, int nk,
+                                                    int D, const float *rope, long long sin_off, const int *pos0p,
+                                                    float *Q, float *Kst, float *Vst) {
+    const int t = blockIdx.y;
+    const int pair = blockIdx.x * blockDim.x + threadIdx.x;  // rows 2*pair, 2*pair+1
+    if (2 * pair >= rows) return;
+    const int n = 2 * pair, half = D >> 1, pos = *pos0p + t;
+    const float x0 = vsum_part(part, ksplit, M, rows, t, n), x1 = vsum_part(part, ksplit, M, rows, t, n + 1);
+    if (n < nq + nk) {
+        const int j = n % D, i = j >> 1;
+        const float c = rope[(size_t)pos * half + i], sn = rope[sin_off + (size_t)pos * half + i];
+        const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+        if (n < nq) {
+            const int h = n / D;
+            Q[(size_t)t * nq + h * D + i] = y0;
+            Q[(size_t)t * nq + h * D + i + half] = y1;
+        } else {
+            const int k0 = (n - nq) - j;
+            Kst[(size_t)t * nk + k0 + i] = y0;
+            Kst[(size_t)t * nk + k0 + i + half] = y1;
+        }
+    } else {
+        const int vi = n - nq - nk;
+        Vst[(size_t)t * nk + vi] = x0;
+        Vst[(size_t)t * nk + vi + 1] = x1;
+    }
+}
+
+// out[t] = partials (plain store, fl_op_batched_matvec_q8in)
+__global__ __launch_bounds__(256) void k_v_store(const float *part, int ksplit, int M, int rows, float *out) {
+    const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < rows) out[(size_t)t * rows + i] = vsum_part(part, ksplit, M, rows, t, i);
+}
+
+// x[t] += partials (residual add, model.rs:2305-2311 / 2537-2543)
+__global__ __launch_bounds__(256) void k_v_residual(const float *part, int ksplit, int M, int H, float *x) {
+    const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < H) x[(size_t)t * H + i] += vsum_part(part, ksplit, M, H, t, i);
+}
+
+// gate/up partials -> SiLU(g) * u (silu_mul_into, model.rs:9783-9796) ->
+// Q8_0 quantization per 32-block (the down projection's input).
+__global__ __launch_bounds__(256) void k_v_silu_quant(const float *part, int ksplit, int M, int F, int8_t *q, float *s,
+                                                      int *sum) {
+    const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;  // F % 256 == 0 not required:
+    const int rows = 2 * F;
+    const int ic = min(i, F - 1);
+    const float g = vsum_part(part, ksplit, M, rows, t, ic), u = vsum_part(part, ksplit, M, rows, t, F + ic);
+    const float h = (g / (1.0f + expf(-g))) * u;
+    // 32 lanes per block (F % 32 == 0, so a block never straddles the end)
+    if (i - (threadIdx.x & 31) < F)
+        quant_block32_lanes(h, q + (size_t)t * F + (i & ~31), s + (size_t)t * (F >> 5) + (i >> 5),
+                            sum + (size_t)t * (F >> 5) + (i >> 5));
+}
+
+}  // namespace fl

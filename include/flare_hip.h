@@ -66,7 +66,7 @@ extern "C" {
  * quantize_to_packed arithmetic of flare-core/src/kv_cache.rs:336-371
  * ((max-min)/3, round, clamp 0..3, 4 codes per byte LSB first) and
  * (scale, min) kept as binary16.  The newest tokens stay binary16 in a
- * 160-slot ring: tokens [0, Q) come from the 2-bit groups and [Q, T) from the
+ * 192-slot ring: tokens [0, Q) come from the 2-bit groups and [Q, T) from the
  * ring, Q = 32*floor((T-129)/32) for T > 128 (else 0).  The reference's own
  * QuantizedKvCache (kv_cache.rs:35-323: 32-token f32 window, per-token K codes
  * read with running per-channel stats) is not reproduced. */
@@ -127,6 +127,13 @@ int fl_op_rmsnorm(fl_ctx *ctx, const float *x, const float *w, int n, float eps,
  * (model.rs:9672-9779) over a Q8_0-quantized input. */
 int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
                       const int32_t *sums, float *out);
+/* CpuBackend::batched_dequant_matmul (model.rs:740-1036) over n_tokens
+ * (1..16) Q8_0-quantized input rows: q [n][cols] int8, scales / sums
+ * [n][cols/32]; out [n][rows] f32.  Every row of out is the single-token
+ * matvec_q8_0_preq_into / matvec_q4k_q8_into of that input row (the same
+ * per-block integer dots, formed on int8 MFMA).  Synchronises. */
+int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
+                              const float *scales, const int32_t *sums, float *out);
 /* Dequantized-weight x f32-input matvec (the f32 logits path,
  * matvec_into model.rs:7549 on dequantize_tensor output, gguf.rs:717). */
 int fl_op_matvec_f32in(fl_ctx *ctx, const fl_weight *w, const float *x, float *out);
@@ -200,6 +207,19 @@ int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int3
  * per token, one host synchronisation at the end. */
 int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen,
                 uint32_t *out_tokens);
+
+/* Speculative verify: n_tokens (1..16) draft tokens at positions
+ * pos0..pos0+n_tokens-1 through the model in one pass: every projection as
+ * batched_dequant_matmul (model.rs:740-1036, int8 MFMA), causal attention
+ * (the default prefill_attention_gpu, model.rs:336-368: token i attends
+ * 0..pos0+i), their K/V written to the cache, then the fused argmax per token
+ * (forward_greedy, model.rs:1872-1942).  out_tokens[i] (and out_vals[i] if
+ * not NULL) is the greedy token after draft i -- what n_tokens sequential
+ * fl_decode_step calls return; Generator::speculative_step
+ * (generate.rs:244-312) accepts drafts while they match.  Cache slots beyond
+ * the accepted prefix are simply rewritten by later steps. */
+int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens,
+              float *out_vals);
 
 /* Enqueue n_steps more device-resident greedy steps after fl_generate (no
  * host synchronisation; tokens land in the device token buffer). */

@@ -1,0 +1,117 @@
+"""Speculative verify (BASELINE config 5's pass) on the GPU.
+
+* fl_op_batched_matvec_q8in: every token row of the int8-MFMA GEMM equals the
+  oracle's single-token quantized matvec within 1e-3 relative (the per-block
+  integer dots are exact; only the fp32 order of the block terms differs).
+* fl_verify: the greedy token after each of M drafts equals what sequential
+  decode gives -- the GPU's own fl_decode_step loop and the oracle -- wherever
+  the oracle's top-2 logit gap is not a near-tie.
+"""
+import numpy as np
+import pytest
+
+from flarellm_amd import FL_KV_F16, FL_KV_F32, FL_KV_KIVI2, FL_KV_Q8, FL_Q4K, FL_Q6K, FL_Q8_0
+from flarellm_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-3
+
+
+def _t(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _close(got, want, rel=REL):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    err = np.abs(got - want)
+    bound = rel * np.maximum(np.abs(want), 1e-3 * scale) + 1e-6 * scale
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} / {bad.size} outside tol; max err {err.max():.3e}, scale {scale:.3e}"
+
+
+GEMM_SHAPES = [(FL_Q8_0, 96, 256, 1), (FL_Q8_0, 1001, 2048, 8), (FL_Q8_0, 64, 576, 3), (FL_Q8_0, 200, 8192, 16),
+               (FL_Q4K, 96, 256, 8), (FL_Q4K, 130, 4096, 5), (FL_Q4K, 64, 14336, 8), (FL_Q4K, 6144, 4096, 8),
+               (FL_Q4K, 1536, 4096, 16)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols,M", GEMM_SHAPES)
+def test_batched_matvec_q8in(backend, oracle, fmt, rows, cols, M):
+    print(f"[batched] fmt={fmt} {rows}x{cols} M={M}", flush=True)
+    w = S.quantize(S.normal(rows + 3, 0, rows * cols, 0, 0.02).reshape(rows, cols), fmt)
+    W = backend.upload(S.QWeight(w, fmt, rows, cols))
+    qs, ss, sums = [], [], []
+    for m in range(M):
+        q, s = oracle.quantize_q8(S.normal(50 + m, 0, cols, 0.0, 1.0))
+        qs.append(q)
+        ss.append(s)
+        sums.append(q.reshape(-1, 32).astype(np.int32).sum(1, dtype=np.int32))
+    got = backend.batched_matvec_q8in(W, _t(np.stack(qs)), _t(np.stack(ss)), _t(np.stack(sums))).cpu().numpy()
+    for m in range(M):
+        _close(got[m], oracle.matvec(w, fmt, rows, cols, qs[m], ss[m]))
+
+
+MODELS = {
+    "q8_tied": S.tiny_spec(FL_Q8_0, max_seq=128),
+    "q4k_q6k_out": S.tiny_spec(FL_Q4K, embed_fmt=FL_Q6K, output_fmt=FL_Q6K, max_seq=128),
+    "q8_hd128": S.tiny_spec(FL_Q8_0, heads=8, kv_heads=2, head_dim=128, hidden=512, inter=768, max_seq=128),
+}
+KV = {"f32": FL_KV_F32, "f16": FL_KV_F16, "q8": FL_KV_Q8, "kivi": FL_KV_KIVI2}
+MARGIN = 2e-2  # top-2 gap (relative) below which a position counts as a near-tie
+
+
+def _omode(oracle, kv):
+    return {FL_KV_F32: oracle.OR_KV_F32, FL_KV_F16: oracle.OR_KV_F16, FL_KV_Q8: oracle.OR_KV_Q8,
+            FL_KV_KIVI2: oracle.OR_KV_KIVI32}[kv]
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+@pytest.mark.parametrize("kv", list(KV))
+def test_verify_matches_sequential_decode(backend, oracle, name, kv):
+    spec = MODELS[name]
+    M, n_prompt = 8, 40
+    print(f"[verify] {name} kv={kv}", flush=True)
+    model = S.make_model(spec, seed=6)
+    prompt = S.random_tokens(106, n_prompt, spec.vocab)
+    drafts = S.random_tokens(206, M, spec.vocab)
+    backend.init_gpu_kv_cache(spec, KV[kv])
+    backend.upload_weights_to_gpu(model)
+    for pos, t in enumerate(prompt):
+        backend.forward_greedy(int(t), pos)
+    got, vals = backend.verify(drafts, n_prompt)
+    # the GPU's own sequential decode over the same drafts
+    seq = [backend.forward_greedy(int(t), n_prompt + i) for i, t in enumerate(drafts)]
+    # oracle logits for the near-tie margin
+    om = oracle.OracleModel(model, _omode(oracle, KV[kv]))
+    for pos, t in enumerate(prompt):
+        om.forward_greedy(int(t), pos)
+    checked = 0
+    for i, t in enumerate(drafts):
+        logits = om.forward_logits(int(t), n_prompt + i)
+        top2 = np.sort(logits)[-2:]
+        assert abs(vals[i] - seq[i][1]) <= 1e-2 * abs(seq[i][1]) + 1e-6, (i, vals[i], seq[i])
+        if top2[1] - top2[0] > MARGIN * abs(top2[1]):
+            assert got[i] == seq[i][0] == int(np.argmax(logits)), (i, got[i], seq[i], int(np.argmax(logits)))
+            checked += 1
+    assert checked >= M // 2
+
+
+def test_verify_accepts_sequential_greedy_stream(backend, oracle):
+    """Drafts taken from the model's own greedy stream are all accepted:
+    verify returns the stream shifted by one."""
+    spec = MODELS["q8_tied"]
+    model = S.make_model(spec, seed=8)
+    prompt = S.random_tokens(108, 20, spec.vocab)
+    backend.init_gpu_kv_cache(spec, FL_KV_F16)
+    backend.upload_weights_to_gpu(model)
+    stream = backend.generate(prompt, 17)  # greedy tokens after the prompt
+    backend.reset()
+    for pos, t in enumerate(prompt):
+        backend.forward_greedy(int(t), pos)
+    drafts = stream[:8].astype(np.uint32)
+    got, _ = backend.verify(drafts, len(prompt))
+    assert got.tolist() == stream[1:9].tolist()
