@@ -37,6 +37,8 @@ HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "a
 
 
 def build(verbose: bool = True) -> str:
+    # FLARE_BUILD_DEFS: extra -D flags for diagnostic builds (e.g. -DFLARE_ATTN_TRACE)
+    extra = os.environ.get("FLARE_BUILD_DEFS", "").split()
     from concurrent.futures import ThreadPoolExecutor
 
     os.makedirs(BUILD, exist_ok=True)
@@ -44,7 +46,7 @@ def build(verbose: bool = True) -> str:
     objs = []
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     syn_obj = os.path.join(BUILD, "synth.o")
     jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "synth.cpp"), "-o", syn_obj])

@@ -1,4 +1,5 @@
 // Decode attention launchers and the Q8 / KIVI cache writers.
+#include "attm_kernels.h"
 #include "launch.h"
 
 namespace fl {
@@ -16,13 +17,31 @@ static hipError_t launch_attn_t(int D, int G, hipStream_t st, const AttnArgs &a,
     return hipErrorNotSupported;
 }
 
+template <typename KT>
+static hipError_t launch_attm_t(int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
+#define C(DD, GG)                                                                                  \
+    if (D == DD && G == GG) {                                                                      \
+        hipLaunchKernelGGL((k_attm<KT, DD, GG>), dim3(a.nsplit, a.nkv, nq), dim3(kAttmThreads), 0, st, a); \
+        return hipSuccess;                                                                         \
+    }
+    C(64, 1) C(64, 2) C(64, 3) C(64, 4) C(64, 8)
+    C(128, 1) C(128, 2) C(128, 3) C(128, 4) C(128, 8)
+#undef C
+    return hipErrorNotSupported;
+}
+
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
-    if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit || nq < 1) return hipErrorInvalidValue;
+    if (nq < 1) return hipErrorInvalidValue;
     if (nq > 1 && a.knew) return hipErrorInvalidValue;  // new-token stores are single-query
+    // model caches in fp16 / Q8 (V in transposed blocks): the MFMA kernel
+    if ((kvfmt == KV_F16 && a.v_tblk) || kvfmt == KV_Q8) {
+        if (!a.v_tblk || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32) return hipErrorInvalidValue;
+        return kvfmt == KV_F16 ? launch_attm_t<__half>(D, G, st, a, nq) : launch_attm_t<KvQ8>(D, G, st, a, nq);
+    }
+    if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit) return hipErrorInvalidValue;
     switch (kvfmt) {
     case KV_F32: return launch_attn_t<float>(D, G, st, a, nq);
     case KV_F16: return launch_attn_t<__half>(D, G, st, a, nq);
-    case KV_Q8: return launch_attn_t<KvQ8>(D, G, st, a, nq);
     case KV_KIVI: return launch_attn_t<KvKivi>(D, G, st, a, nq);
     }
     return hipErrorNotSupported;
@@ -53,8 +72,13 @@ __global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *kr
     const float d = amax / 127.0f;
     const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
     const int t = p0 + r;
-    int8_t *q = (int8_t *)(isv ? a.vc : a.kc) + (size_t)kvh * a.head_stride + (size_t)t * D + 32 * b;
-    for (int e = 0; e < 32; e++) q[e] = sat_i8(roundf(x[e] * id));
+    if (isv) {  // V codes into the 32-slot transposed blocks
+        int8_t *q = (int8_t *)a.vc + (size_t)kvh * a.head_stride;
+        for (int e = 0; e < 32; e++) q[vt_off(t, 32 * b + e, D)] = sat_i8(roundf(x[e] * id));
+    } else {
+        int8_t *q = (int8_t *)a.kc + (size_t)kvh * a.head_stride + (size_t)t * D + 32 * b;
+        for (int e = 0; e < 32; e++) q[e] = sat_i8(roundf(x[e] * id));
+    }
     (isv ? a.vs : a.ks)[((size_t)kvh * a.S + t) * nb + b] = f2h(d);
 }
 
@@ -97,7 +121,8 @@ __global__ __launch_bounds__(256) void k_kv_plain_write(AttnArgs a, const float 
     const long long j = i % ((long long)n * per);
     const int r = (int)(j / per), kvh = (int)((j % per) / D), ch = (int)(j % D);
     const float v = (isv ? vrows : krows)[j];
-    const size_t o = (size_t)kvh * a.head_stride + (size_t)(p0 + r) * D + ch;
+    const size_t o = (size_t)kvh * a.head_stride +
+                     ((isv && a.v_tblk) ? vt_off(p0 + r, ch, D) : (size_t)(p0 + r) * D + ch);
     void *dst = isv ? (void *)a.vc : (void *)a.kc;
     if (f16) ((__half *)dst)[o] = __float2half(v);
     else ((float *)dst)[o] = v;

@@ -45,6 +45,7 @@ struct AttnArgs {
     // q / out / oq advance by qstride / ostride floats per query; split
     // partials and counters have one set per query.
     int qstride, ostride;
+    int v_tblk;  // F16 / Q8 model caches: V stored in 32-slot transposed blocks [slot/32][D][32]
 };
 
 // KIVI 2-bit cache constants: groups of 32 (K per channel over 32 tokens, V
@@ -164,26 +165,6 @@ struct KVRow<__half> {
     __device__ __forceinline__ void getk(float *o) const { h8_to_f32(k, o); }
     __device__ __forceinline__ void getv(float *o) const { h8_to_f32(v, o); }
 };
-// Q8: int8 codes [kvh][S][D] with one f16 scale per 32 values.
-template <>
-struct KVRow<KvQ8> {
-    v2i_t k, v;
-    uint32_t sc;  // K scale | V scale << 16
-    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
-        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
-        k = *(const v2i_t *)((const int8_t *)a.kc + o);
-        v = *(const v2i_t *)((const int8_t *)a.vc + o);
-        const size_t so = ((size_t)kvh * a.S + t) * (a.tok_stride >> 5) + (c >> 2);
-        sc = (uint32_t)a.ks[so] | ((uint32_t)a.vs[so] << 16);
-    }
-    __device__ __forceinline__ static void dec(const v2i_t &q, uint16_t s, float *o) {
-        const float d = h2f(s);
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = (float)(int8_t)(((uint32_t)(i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFF) * d;
-    }
-    __device__ __forceinline__ void getk(float *o) const { dec(k, (uint16_t)(sc & 0xFFFF), o); }
-    __device__ __forceinline__ void getv(float *o) const { dec(v, (uint16_t)(sc >> 16), o); }
-};
 // KIVI: tokens below qlen from the 2-bit groups, the rest from the fp16 ring.
 // Quantized token: x.x = K codes | V codes << 16 (8 channels x 2 bits each),
 // x.y = V (scale, min) of the channel group; y / z = K (scale, min) of the 8
@@ -259,7 +240,8 @@ __device__ __forceinline__ void q8_block8(const float *x, v2i_t &q, uint16_t &s)
 }
 template <>
 struct NewRow<KvQ8> {
-    KVRow<KvQ8> r;
+    v2i_t k, v;
+    uint32_t sc;  // K scale | V scale << 16 (binary16) of this lane's 32-block
     __device__ __forceinline__ void build(const AttnArgs &a, int kvh, int c) {
         const int D = (int)a.tok_stride;
         float kx[8], vx[8];
@@ -268,19 +250,24 @@ struct NewRow<KvQ8> {
         kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w; kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
         vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w; vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
         uint16_t sk, sv;
-        q8_block8(kx, r.k, sk);
-        q8_block8(vx, r.v, sv);
-        r.sc = (uint32_t)sk | ((uint32_t)sv << 16);
+        q8_block8(kx, k, sk);
+        q8_block8(vx, v, sv);
+        sc = (uint32_t)sk | ((uint32_t)sv << 16);
     }
-    __device__ __forceinline__ void apply(KVRow<KvQ8> &row) const { row = r; }
+    // K row-major, V into the 32-slot transposed blocks
     __device__ __forceinline__ void store(const AttnArgs &a, int kvh, int t, int c) const {
-        const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
-        *(v2i_t *)((int8_t *)a.kc + o) = r.k;
-        *(v2i_t *)((int8_t *)a.vc + o) = r.v;
+        const int D = (int)a.tok_stride;
+        int8_t *kc = (int8_t *)a.kc + (size_t)kvh * a.head_stride;
+        int8_t *vc = (int8_t *)a.vc + (size_t)kvh * a.head_stride;
+        *(v2i_t *)(kc + (size_t)t * D + 8 * c) = k;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            vc[((size_t)(t >> 5) * D + 8 * c + i) * 32 + (t & 31)] =
+                (int8_t)(((uint32_t)(i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF);
         if ((c & 3) == 0) {
-            const size_t so = ((size_t)kvh * a.S + t) * (a.tok_stride >> 5) + (c >> 2);
-            a.ks[so] = (uint16_t)(r.sc & 0xFFFF);
-            a.vs[so] = (uint16_t)(r.sc >> 16);
+            const size_t so = ((size_t)kvh * a.S + t) * (D >> 5) + (c >> 2);
+            a.ks[so] = (uint16_t)(sc & 0xFFFF);
+            a.vs[so] = (uint16_t)(sc >> 16);
         }
     }
 };

@@ -25,6 +25,7 @@
 
 #include "../../include/flare_hip.h"
 #include "kernels.h"
+#include "attm_kernels.h"
 #include "launch.h"
 
 using namespace fl;
@@ -857,8 +858,9 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     const size_t H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
     const size_t F = c.intermediate_dim, L = c.num_layers, S = c.max_seq_len;
     {
-        const bool quant = kv_format == FL_KV_Q8 || kv_format == FL_KV_KIVI2;
-        const size_t Sa = quant ? (S + 31) / 32 * 32 : S;
+        // Q8 / KIVI groups and the fp16 / Q8 transposed V blocks span 32 slots
+        const bool blk32 = kv_format != FL_KV_F32;
+        const size_t Sa = blk32 ? (S + 31) / 32 * 32 : S;
         ctx->kv_slots = (int)Sa;
         const size_t code_bytes = kv_format == FL_KV_F32 ? 4 * kvd : kv_format == FL_KV_F16 ? 2 * kvd
                                 : kv_format == FL_KV_Q8 ? kvd : kvd / 4;  // per token
@@ -894,11 +896,19 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         rope_row_host(c.head_dim, (int)p, c.rope_theta, &tab[p * half], &tab[S * half + p * half]);
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
-    choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
+    if (kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) {
+        // MFMA kernel: chunks of whole rounds (one 32-slot block per wave),
+        // at most kAttmMaxSplit per kv head
+        ctx->chmin = kAttmBlock * (kAttmThreads / 64);
+        ctx->nsplit = std::max(1, std::min(kAttmMaxSplit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin));
+    } else {
+        choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
+    }
     if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
     if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
         const int ns = atoi(ev);
-        if (ns > 0 && ns <= kAttnMaxSplit) ctx->nsplit = ns;
+        if (ns > 0 && ns <= ((kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) ? kAttmMaxSplit : kAttnMaxSplit))
+            ctx->nsplit = ns;
     }
     const int G = c.num_heads / c.num_kv_heads;
     int rc = ensure_part(ctx, (size_t)c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
@@ -1023,7 +1033,11 @@ int fl_kv_write(fl_ctx *ctx, int layer, int position, const float *key, const fl
                 hv[i] = __float2half(value[h * hd + i]);
             }
             HIPCHK(ctx, hipMemcpy((__half *)ctx->kcache + off, hk.data(), hd * 2, hipMemcpyHostToDevice));
-            HIPCHK(ctx, hipMemcpy((__half *)ctx->vcache + off, hv.data(), hd * 2, hipMemcpyHostToDevice));
+            // V: channel d of the slot sits in the 32-slot transposed block
+            const size_t vbase = (size_t)layer * ctx->kv_layer_elems + (size_t)h * ctx->kv_slots * hd;
+            for (size_t d = 0; d < hd; d++)
+                HIPCHK(ctx, hipMemcpy((__half *)ctx->vcache + vbase + vt_off(slot, (int)d, (int)hd), &hv[d], 2,
+                                      hipMemcpyHostToDevice));
         }
     }
     return 0;
@@ -1098,6 +1112,7 @@ static void kv_layer_args(fl_ctx *ctx, int l, AttnArgs &a) {
     a.head_stride = (long long)(Sa * D);
     a.nkv = c.num_kv_heads;
     a.S = (int)Sa;
+    a.v_tblk = ctx->kv_format == FL_KV_F16 || ctx->kv_format == FL_KV_Q8;
     if (ctx->kscale) {
         a.ks = ctx->kscale + (size_t)l * Sa * (kvd / 32);
         a.vs = ctx->vscale + (size_t)l * Sa * (kvd / 32);
@@ -1153,6 +1168,7 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
     e.nk = c.num_kv_heads * c.head_dim;
     e.hd = c.head_dim;
     e.kv_f16 = ctx->kv_format == FL_KV_F16;
+    e.v_tblk = ctx->kv_format == FL_KV_F16;
     // Q8 / KIVI: K (after RoPE) and V stay f32 in the output after q; the
     // attention kernel quantizes and stores them
     e.kv_stage = ctx->kv_format == FL_KV_Q8 || ctx->kv_format == FL_KV_KIVI2;

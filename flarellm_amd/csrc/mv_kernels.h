@@ -24,6 +24,7 @@ struct QkvEpi {
     int hd;             // head_dim
     int kv_f16;         // cache element: 1 = binary16 (RNE), 0 = f32
     int kv_stage;       // 1: K (after RoPE) and V go to the output after q, as f32
+    int v_tblk;         // 1: V stored in 32-slot transposed blocks [slot/32][D][32]
 };
 
 #ifdef FLARE_MV_TRACE
@@ -306,6 +307,12 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
         if (e.kv_stage) {
             q[e.nq + e.nk + vi] = x0;
             q[e.nq + e.nk + vi + 1] = x1;
+            return;
+        }
+        if (e.v_tblk) {  // channels d, d+1 of slot pos: 32 elements apart
+            const size_t o = (size_t)kvh * e.head_stride + ((size_t)(pos >> 5) * D + d) * 32 + (pos & 31);
+            ((uint16_t *)e.vc)[o] = f2h(x0);
+            ((uint16_t *)e.vc)[o + 32] = f2h(x1);
             return;
         }
         const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D + d;
