@@ -27,6 +27,7 @@ typedef float v4f32_t __attribute__((ext_vector_type(4)));
 constexpr int kAttmThreads = 512;  // 8 waves, each walking 32-token blocks
 constexpr int kAttmBlock = 32;
 constexpr int kAttmMaxSplit = 64;
+constexpr int kAttmSingle = 1024;  // contexts up to this many tokens run as one split
 
 // Offset of (slot t, channel d) in one kv head's transposed V store.
 __host__ __device__ inline size_t vt_off(int t, int d, int D) {
@@ -145,7 +146,9 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
     ATTN_TS(0);
     const int pos = *a.posp + zq, T = pos + 1;
-    int CH = max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
+    // up to kAttmSingle tokens: one split (no cross-workgroup merge);
+    // beyond: chunks of at least chmin slots over the nsplit workgroups
+    int CH = T <= kAttmSingle ? T : max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
     CH = (CH + kAttmBlock * NW - 1) / (kAttmBlock * NW) * (kAttmBlock * NW);
     const int t0 = s * CH;
     if (t0 >= T) return;
@@ -188,9 +191,9 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int bi = wave; bi < nblk; bi += NW) {
+    // one 32-slot block (slots tb .. tb+31) with its tile in registers
+    auto process = [&](AttmTile<KT, D> &tile, int bi) {
         const int tb = t0 + bi * kAttmBlock;
-        if (bi != wave) tile.load(a, kvh, tb, t1 - 1, lane);
         if constexpr (std::is_same<KT, KvQ8>::value) {
             // Q8 decode step: the block holding slot pos quantizes the new
             // token, stores it, and patches its K row / V column in registers
@@ -335,6 +338,23 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
             }
         }
         __builtin_amdgcn_wave_barrier();
+    };
+    if constexpr (std::is_same<KT, __half>::value) {
+        // ping-pong: the wave's next block is in flight while this one computes
+        AttmTile<KT, D> tile2;
+        for (int bi = wave; bi < nblk; bi += 2 * NW) {
+            if (bi + NW < nblk) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
+            process(tile, bi);
+            if (bi + NW >= nblk) break;
+            if (bi + 2 * NW < nblk) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
+            process(tile2, bi + NW);
+        }
+    } else {
+        // Q8 (more registers per block): one tile, loaded at the top
+        for (int bi = wave; bi < nblk; bi += NW) {
+            if (bi != wave) tile.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
+            process(tile, bi);
+        }
     }
 
     ATTN_TS(3);

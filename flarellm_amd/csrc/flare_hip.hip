@@ -897,14 +897,17 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
     if (kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) {
-        // MFMA kernel: chunks of whole rounds (one 32-slot block per wave),
-        // at most kAttmMaxSplit per kv head
-        ctx->chmin = kAttmBlock * (kAttmThreads / 64);
+        // MFMA kernel: chunks of at least 512 slots (two 32-slot blocks per
+        // wave, the second in flight while the first computes), at most
+        // kAttmMaxSplit splits per kv head; up to kAttmSingle tokens the
+        // kernel runs one split
+        ctx->chmin = 2 * kAttmBlock * (kAttmThreads / 64);
+        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(256, atoi(ev) / 256 * 256);
         ctx->nsplit = std::max(1, std::min(kAttmMaxSplit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin));
     } else {
         choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
+        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
     }
-    if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
     if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
         const int ns = atoi(ev);
         if (ns > 0 && ns <= ((kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) ? kAttmMaxSplit : kAttnMaxSplit))
