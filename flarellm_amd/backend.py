@@ -144,6 +144,17 @@ class HipBackend:
               self.ctx)
         return out
 
+    def batched_matvec_f32in(self, w: Weight, x):
+        """f32-input matvec for n rows x [n, cols] (Q6_K / Q8_0) -> [n, rows]."""
+        import torch
+
+        n = x.shape[0]
+        out = torch.empty((n, w.rows), dtype=torch.float32, device=x.device)
+        self._torch_sync()
+        check(self.lib.fl_op_batched_matvec_f32in(self.ctx, w.handle, n, _ptr(x), _ptr(out)), self.ctx)
+        self.sync()
+        return out
+
     def matvec_f32in(self, w: Weight, x):
         import torch
 

@@ -27,6 +27,7 @@
 #include "kernels.h"
 #include "attm_kernels.h"
 #include "launch.h"
+#include "mvo_kernels.h"
 
 using namespace fl;
 
@@ -263,7 +264,7 @@ struct fl_ctx {
     bool graph_ready = false;
     // speculative verify buffers (allocated on first fl_verify)
     bool have_verify = false;
-    float *vx = nullptr, *vq = nullptr, *vk = nullptr, *vv = nullptr, *vpart = nullptr;
+    float *vx = nullptr, *vx2 = nullptr, *vq = nullptr, *vk = nullptr, *vv = nullptr, *vpart = nullptr;
     int8_t *vxq = nullptr, *vaq = nullptr;
     float *vxs = nullptr, *vas = nullptr;
     int *vxsum = nullptr, *vasum = nullptr;
@@ -477,8 +478,28 @@ static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const 
 }
 
 // f32-input matvec (Q8_0 / Q6_K / f32 weights): pro 0 copies x, 1 = rmsnorm_into.
+// Several tokens (speculative verify) over Q6_K / Q8_0 weights: the MFMA
+// kernel (rows of M tokens at x, x + cols, ..., argmax keys at slot[0..M)),
+// which dequantizes each weight once for all M tokens.  One token: the
+// streaming kernel (per-block scale work dominates either way, and the
+// streaming kernel keeps more bytes in flight per wave).
 static int launch_f32in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
-                        const float *nw, float eps, float *out, unsigned long long *slot) {
+                        const float *nw, float eps, float *out, unsigned long long *slot, int M = 1) {
+    if ((w.format == FL_Q6K || w.format == FL_Q8_0) && (M > 1 || getenv("FLARE_MVO_SINGLE"))) {
+        MvoArgs a{};
+        a.W = w.desc();
+        a.x = x;
+        a.nw = pro == 1 ? nw : nullptr;
+        a.eps = eps;
+        a.M = M;
+        a.epi = epi;
+        a.out = out;
+        a.slots = slot;
+        const hipError_t e = launch_mvo(w.format, ctx->stream, a);
+        HIPCHK(ctx, e);
+        return 0;
+    }
+    if (M != 1) return fail(ctx, FL_E_UNSUPPORTED, "multi-token f32-input matvec for format %d", w.format);
     const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, true);
     const MvsArgs a = mvs_args(ctx, w, pro, epi, x, nw, eps, nullptr, nullptr, nullptr, out, slot);
     hipError_t e;
@@ -610,11 +631,11 @@ static void model_release(fl_ctx *c) {
     c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
     c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
-    void *vp[] = {c->vx, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
+    void *vp[] = {c->vx, c->vx2, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
                   c->vtok, c->vpos, c->vslots};
     for (void *p : vp)
         if (p) (void)hipFree(p);
-    c->vx = c->vq = c->vk = c->vv = c->vpart = nullptr; c->vxq = c->vaq = nullptr; c->vxs = c->vas = nullptr;
+    c->vx = c->vx2 = c->vq = c->vk = c->vv = c->vpart = nullptr; c->vxq = c->vaq = nullptr; c->vxs = c->vas = nullptr;
     c->vxsum = c->vasum = nullptr; c->vtok = c->vpos = nullptr; c->vslots = nullptr; c->vpart_floats = 0;
     c->have_verify = false;
     c->have_cfg = c->have_weights = false;
@@ -1427,6 +1448,7 @@ static int verify_alloc(fl_ctx *ctx) {
     const size_t kmax = std::max({H, qd, F});
     const size_t rmax = std::max({qd + 2 * kvd, 2 * F, H});
     ALLOC(ctx, ctx->vx, M * H * 4);
+    ALLOC(ctx, ctx->vx2, M * H * 4);
     ALLOC(ctx, ctx->vq, M * qd * 4);
     ALLOC(ctx, ctx->vk, M * kvd * 4);
     ALLOC(ctx, ctx->vv, M * kvd * 4);
@@ -1501,6 +1523,22 @@ int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, con
     return 0;
 }
 
+int fl_op_batched_matvec_f32in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const float *x, float *out) {
+    if (!ctx || !w || !x || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (w->format != FL_Q6K && w->format != FL_Q8_0) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
+    if (n_tokens < 1 || n_tokens > kMvoMaxTokens)
+        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kMvoMaxTokens);
+    MvoArgs a{};
+    a.W = w->desc();
+    a.x = x;
+    a.nw = nullptr;
+    a.M = n_tokens;
+    a.epi = EPI_STORE;
+    a.out = out;
+    HIPCHK(ctx, launch_mvo(w->format, ctx->stream, a));
+    return 0;
+}
+
 int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
     if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
     if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
@@ -1526,12 +1564,24 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
     HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
     rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (D + 2));
     if (rc) return rc;
-    HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, ctx->vx));
+    float *xa = ctx->vx;
+    HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, xa));
+    int ks_down = 0;
     for (int l = 0; l < c.num_layers; l++) {
         Layer &L = ctx->layers[l];
         int ks;
-        // attention block (model.rs:2016-2311), M tokens at positions pos0..pos0+M-1
-        HIPCHK(ctx, launch_v_normquant(pro, st, ctx->vx, L.attn_norm, eps, H, M, ctx->vxq, ctx->vxs, ctx->vxsum));
+        // attention block (model.rs:2016-2311), M tokens at positions pos0..pos0+M-1;
+        // the previous layer's down projection is added to x here
+        if (l == 0) {
+            HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.attn_norm, eps, ctx->vxq, ctx->vxs,
+                                         ctx->vxsum));
+        } else {
+            // the previous layer's down projection: partials summed once per
+            // element, then the norm reads x only
+            HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));
+            HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.attn_norm, eps, ctx->vxq, ctx->vxs,
+                                         ctx->vxsum));
+        }
         rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
         if (rc) return rc;
         HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, qd, kvd, D, ctx->rope,
@@ -1558,30 +1608,39 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
         }
         rc = verify_gemm(ctx, L.wo, M, ctx->vaq, ctx->vas, ctx->vasum, ks);
         if (rc) return rc;
-        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, ctx->vx));
-        // FFN block (model.rs:2376-2543)
-        HIPCHK(ctx, launch_v_normquant(pro, st, ctx->vx, L.ffn_norm, eps, H, M, ctx->vxq, ctx->vxs, ctx->vxsum));
+        // FFN block (model.rs:2376-2543): wo residual + FFN norm in one kernel
+        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, xa));
+        HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.ffn_norm, eps, ctx->vxq, ctx->vxs,
+                                     ctx->vxsum));
         rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
         if (rc) return rc;
         HIPCHK(ctx, launch_v_silu_quant(st, ctx->vpart, ks, M, F, ctx->vxq, ctx->vxs, ctx->vxsum));
-        rc = verify_gemm(ctx, L.down, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+        rc = verify_gemm(ctx, L.down, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks_down);
         if (rc) return rc;
-        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, ctx->vx));
     }
+    HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));
     // output projection + fused argmax per token (forward_greedy, model.rs:1898-1932)
     const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
     const bool q8out = !ctx->tied && ((O.format == FL_Q8_0 && ctx->layer_fmt == FL_Q8_0) ||
                                       (O.format == FL_Q4K && ctx->layer_fmt == FL_Q4K));
-    for (int t = 0; t < M; t++) {
-        const float *xt = ctx->vx + (size_t)t * H;
-        if (q8out) {
-            rc = launch_q8in(ctx, O, PRO_NORMQ1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, nullptr, nullptr,
-                             nullptr, ctx->vslots + t);
-        } else {
-            if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
-            rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, ctx->vslots + t);
+    if (!q8out && O.format != FL_F32) {
+        if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
+        // all M tokens in one MFMA launch (M <= 8 per launch)
+        for (int t0 = 0; t0 < M; t0 += kMvoMaxTokens) {
+            rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, xa + (size_t)t0 * H, ctx->out_norm, eps, nullptr,
+                              ctx->vslots + t0, std::min(kMvoMaxTokens, M - t0));
+            if (rc) return rc;
         }
-        if (rc) return rc;
+    } else {
+        for (int t = 0; t < M; t++) {
+            const float *xt = xa + (size_t)t * H;
+            if (q8out)
+                rc = launch_q8in(ctx, O, PRO_NORMQ1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, nullptr, nullptr,
+                                 nullptr, ctx->vslots + t);
+            else
+                rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, ctx->vslots + t);
+            if (rc) return rc;
+        }
     }
     std::vector<unsigned long long> keys(M);
     HIPCHK(ctx, hipMemcpyAsync(keys.data(), ctx->vslots, (size_t)M * 8, hipMemcpyDeviceToHost, st));

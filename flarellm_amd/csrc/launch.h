@@ -5,12 +5,41 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "attn_kernels.h"
 #include "mvs_kernels.h"
 #include "verify_args.h"
 
 namespace fl {
+
+// Persistent kernels assume every workgroup of the grid is resident at once
+// (a late second wave of workgroups would run the whole prologue again after
+// the first wave drained): clamp the grid to the kernel's occupancy x CUs.
+template <typename Kern>
+inline int resident_grid(Kern kernel, int threads, size_t lds, int want) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, size_t>, int> cache;
+    const std::pair<const void *, size_t> key((const void *)kernel, lds);
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    int cap;
+    if (it != cache.end()) {
+        cap = it->second;
+    } else {
+        int dev = 0, ncu = 0, per = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per < 1)
+            cap = want;
+        else
+            cap = per * ncu;
+        cache[key] = cap;
+    }
+    return std::max(1, std::min(want, cap));
+}
 
 // Streaming matvec plan: R rows per wave item, SU steps (1 KiB each) per
 // unit, so one tile is R*SU 16-byte pieces per lane (<= 8; two tiles in
@@ -87,11 +116,15 @@ hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &
 hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
                            int p0, int n, int D);
 
+// MFMA output projection with f32 input for up to 8 tokens (mvo.hip)
+struct MvoArgs;
+hipError_t launch_mvo(int fmt, hipStream_t st, const MvoArgs &a);
+
 // speculative verify (verify.hip)
 hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a);
 hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *tokens, int M, float *x);
-hipError_t launch_v_normquant(int pro, hipStream_t st, const float *x, const float *w, float eps, int n, int M,
-                              int8_t *q, float *s, int *sum);
+hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, const float *xin,
+                            float *xout, const float *w, float eps, int8_t *q, float *s, int *sum);
 hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
                              const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
                              float *Vst);

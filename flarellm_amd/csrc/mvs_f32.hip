@@ -5,7 +5,9 @@ namespace fl {
 
 #define C(FMT, F32IN, RR, SS)                                                                         \
     if (p.r == RR && p.su == SS) {                                                                    \
-        hipLaunchKernelGGL((k_mvs<FMT, F32IN, RR, SS>), dim3(p.grid), dim3(kMvsThreads), p.lds, st, a); \
+        hipLaunchKernelGGL((k_mvs<FMT, F32IN, RR, SS>),                                                  \
+                           dim3(resident_grid(k_mvs<FMT, F32IN, RR, SS>, kMvsThreads, p.lds, p.grid)), \
+                           dim3(kMvsThreads), p.lds, st, a);                                       \
         return hipSuccess;                                                                            \
     }
 

@@ -5,7 +5,9 @@ namespace fl {
 
 #define C(FMT, F32IN, RR, SS)                                                                         \
     if (p.r == RR && p.su == SS) {                                                                    \
-        hipLaunchKernelGGL((k_mvs<FMT, F32IN, RR, SS>), dim3(p.grid), dim3(kMvsThreads), p.lds, st, a); \
+        hipLaunchKernelGGL((k_mvs<FMT, F32IN, RR, SS>),                                                  \
+                           dim3(resident_grid(k_mvs<FMT, F32IN, RR, SS>, kMvsThreads, p.lds, p.grid)), \
+                           dim3(kMvsThreads), p.lds, st, a);                                       \
         return hipSuccess;                                                                            \
     }
 
@@ -18,7 +20,9 @@ hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
 hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
 #define G(SS, NW)                                                                               \
     if (p.su == SS && p.r == NW) {                                                              \
-        hipLaunchKernelGGL((k_mvs_gu<F_Q4K, SS, NW>), dim3(p.grid), dim3(NW * 64), p.lds, st, a); \
+        hipLaunchKernelGGL((k_mvs_gu<F_Q4K, SS, NW>),                                         \
+                           dim3(resident_grid(k_mvs_gu<F_Q4K, SS, NW>, NW * 64, p.lds, p.grid)),      \
+                           dim3(NW * 64), p.lds, st, a);                                        \
         return hipSuccess;                                                                      \
     }
     G(1, 8) G(1, 4)

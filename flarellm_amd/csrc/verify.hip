@@ -36,12 +36,13 @@ hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *to
     return hipGetLastError();
 }
 
-hipError_t launch_v_normquant(int pro, hipStream_t st, const float *x, const float *w, float eps, int n, int M,
-                              int8_t *q, float *s, int *sum) {
+hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, const float *xin,
+                            float *xout, const float *w, float eps, int8_t *q, float *s, int *sum) {
+    const dim3 grid((H + 255) / 256, M);
     if (pro == PRO_NORMQ0)
-        hipLaunchKernelGGL(k_v_normquant<PRO_NORMQ0>, dim3(M), dim3(256), 0, st, x, w, eps, n, q, s, sum);
+        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ0>, grid, dim3(256), 0, st, part, ksplit, M, H, xin, xout, w, eps, q, s, sum);
     else
-        hipLaunchKernelGGL(k_v_normquant<PRO_NORMQ1>, dim3(M), dim3(256), 0, st, x, w, eps, n, q, s, sum);
+        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ1>, grid, dim3(256), 0, st, part, ksplit, M, H, xin, xout, w, eps, q, s, sum);
     return hipGetLastError();
 }
 

@@ -186,17 +186,6 @@ __global__ __launch_bounds__(256) void k_v_embed(WDesc E, const int *tokens, flo
     }
 }
 
-// Per token: RMSNorm + Q8_0 quantization (the decode prologue's arithmetic,
-// stage_q8; PRO_NORMQ0 / PRO_NORMQ1).
-template <int PRO>
-__global__ __launch_bounds__(256) void k_v_normquant(const float *x, const float *w, float eps, int n, int8_t *q,
-                                                     float *s, int *sum) {
-    __shared__ float red[8];
-    const int t = blockIdx.x;
-    stage_q8<PRO>(x + (size_t)t * n, w, eps, n, nullptr, nullptr, nullptr, q + (size_t)t * n, s + (size_t)t * (n >> 5),
-                  sum + (size_t)t * (n >> 5), red);
-}
-
 // QKV partials -> per token: RoPE (apply_rope_with_table, model.rs:7283-7296)
 // on the pair-interleaved q / k rows at position pos0 + t; q to Q[t], K / V
 // rows (f32) to the staging rows written into the cache afterwards.
@@ -232,6 +221,35 @@ __global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int kspli
 __global__ __launch_bounds__(256) void k_v_store(const float *part, int ksplit, int M, int rows, float *out) {
     const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < rows) out[(size_t)t * rows + i] = vsum_part(part, ksplit, M, rows, t, i);
+}
+
+// Residual add + RMSNorm + Q8_0 quantization for M tokens (the decode
+// prologue's arithmetic, rmsnorm_quantize_q8_0 / rmsnorm_into + quantize,
+// model.rs:5581-5640 / 7456-7477).  Grid (slices of 256, M): every
+// workgroup of token t forms the whole updated row x_in + partials (for the
+// row's sum of squares), writes its 256-slice to x_out and quantizes it.
+// part == nullptr: no add (x_out unused).
+template <int PRO>
+__global__ __launch_bounds__(256) void k_v_resnorm(const float *part, int ksplit, int M, int H, const float *xin,
+                                                   float *xout, const float *w, float eps, int8_t *q, float *s,
+                                                   int *sum) {
+    __shared__ float red[8];
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const float *xi = xin + (size_t)t * H;
+    float ss = 0.0f, mine = 0.0f;
+    for (int j = threadIdx.x; j < H; j += 256) {
+        const float v = xi[j] + (part ? vsum_part(part, ksplit, M, H, t, j) : 0.0f);
+        ss += v * v;
+        if (j == i) mine = v;
+    }
+    ss = wg_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    if (i - (threadIdx.x & 31) >= H) return;  // whole 32-blocks past the row end
+    if (part && i < H) xout[(size_t)t * H + i] = mine;
+    const float wi = i < H ? w[i] : 0.0f;
+    const float v = (PRO == PRO_NORMQ0) ? mine * wi * inv : (mine * inv) * wi;
+    quant_block32_lanes(v, q + (size_t)t * H + (i & ~31), s + (size_t)t * (H >> 5) + (i >> 5),
+                        sum + (size_t)t * (H >> 5) + (i >> 5));
 }
 
 // x[t] += partials (residual add, model.rs:2305-2311 / 2537-2543)

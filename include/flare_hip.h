@@ -134,6 +134,13 @@ int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const fl
  * per-block integer dots, formed on int8 MFMA).  Synchronises. */
 int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
                               const float *scales, const int32_t *sums, float *out);
+/* Dequantized-weight x f32-input matvec for n_tokens (1..8) input rows at
+ * once (the speculative-verify logits path: matvec_into / matvec_argmax_f32,
+ * model.rs:7549 and 8668, per row): x [n][cols], out [n][rows], device
+ * pointers.  Q6_K and Q8_0 weights, f16 MFMA with exact weight codes and
+ * split (high + residual) f16 inputs. */
+int fl_op_batched_matvec_f32in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const float *x,
+                               float *out);
 /* Dequantized-weight x f32-input matvec (the f32 logits path,
  * matvec_into model.rs:7549 on dequantize_tensor output, gguf.rs:717). */
 int fl_op_matvec_f32in(fl_ctx *ctx, const fl_weight *w, const float *x, float *out);

@@ -55,6 +55,24 @@ def test_batched_matvec_q8in(backend, oracle, fmt, rows, cols, M):
         _close(got[m], oracle.matvec(w, fmt, rows, cols, qs[m], ss[m]))
 
 
+F32IN_SHAPES = [(FL_Q6K, 45, 4096, 8), (FL_Q6K, 1000, 256, 3), (FL_Q6K, 129, 4096, 1), (FL_Q8_0, 77, 576, 8),
+                (FL_Q8_0, 1001, 2048, 5), (FL_Q8_0, 16, 64, 1)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols,M", F32IN_SHAPES)
+def test_batched_matvec_f32in(backend, oracle, fmt, rows, cols, M):
+    """MFMA logits kernel (f16 split input, exact codes) vs the oracle's f32
+    dot over dequantized weights (matvec_f32, model.rs:7549), per token."""
+    print(f"[batched-f32in] fmt={fmt} {rows}x{cols} M={M}", flush=True)
+    w = S.quantize(S.normal(rows + 7, 0, rows * cols, 0, 0.02).reshape(rows, cols), fmt)
+    W = backend.upload(S.QWeight(w, fmt, rows, cols))
+    xs = np.stack([S.normal(70 + m, 0, cols, 0.0, 1.0) for m in range(M)]).astype(np.float32)
+    got = backend.batched_matvec_f32in(W, _t(xs)).cpu().numpy()
+    dq = oracle.dequant(w, fmt, rows, cols)
+    for m in range(M):
+        _close(got[m], oracle.matvec_f32(dq, xs[m]))
+
+
 MODELS = {
     "q8_tied": S.tiny_spec(FL_Q8_0, max_seq=128),
     "q4k_q6k_out": S.tiny_spec(FL_Q4K, embed_fmt=FL_Q6K, output_fmt=FL_Q6K, max_seq=128),
