@@ -62,12 +62,14 @@ inline void mvs_shape(int fmt, bool f32in, int S, int &r, int &su) {
 inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in) {
     MvsPlan p;
     mvs_shape(fmt, f32in, mvs_steps(fmt, cols), p.r, p.su);
-    // tuning overrides (experiments): FLARE_MVS_R / FLARE_MVS_SU / FLARE_MVS_GRID
-    if (const char *e = getenv("FLARE_MVS_R")) p.r = atoi(e);
-    if (const char *e = getenv("FLARE_MVS_SU")) p.su = atoi(e);
+    // tuning overrides for the Q8-input kernels (experiments): FLARE_MVS_R /
+    // FLARE_MVS_SU / FLARE_MVS_GRID
+    const char *er = f32in ? nullptr : getenv("FLARE_MVS_R");
+    if (er) p.r = atoi(er);
+    if (const char *e = f32in ? nullptr : getenv("FLARE_MVS_SU")) p.su = atoi(e);
     // fill the chip: halve the rows per group while fewer than 256
     // workgroups (4 waves, one group each) would run
-    while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !getenv("FLARE_MVS_R")) p.r /= 2;
+    while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !er) p.r /= 2;
     const int ngrp = (rows + p.r - 1) / std::max(1, p.r);
     p.grid = std::max(1, std::min((ngrp + 3) / 4, 1024));
     if (const char *e = getenv("FLARE_MVS_GRID")) p.grid = std::max(1, std::min(p.grid, atoi(e)));
@@ -82,8 +84,13 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in) {
 inline MvsPlan mvs_gu_plan(int fmt, int F, int cols) {
     MvsPlan p;
     const int nblk = F / 32;
-    p.r = nblk <= 256 ? 8 : 4;  // waves per workgroup
+    // waves per workgroup and steps per unit, measured on MI355X: Q4_K (C3
+    // gate/up, 448 blocks) 8 waves x 1 KiB; Q8_0 (C2, 256 blocks) 4 waves x 2 KiB
+    p.r = fmt == F_Q4K ? 8 : 4;
     p.su = (fmt == F_Q8_0 && mvs_steps(fmt, cols) >= 2) ? 2 : 1;
+    // tuning overrides (experiments): FLARE_GU_NW / FLARE_GU_SU
+    if (const char *e = getenv("FLARE_GU_NW")) p.r = atoi(e);
+    if (const char *e = getenv("FLARE_GU_SU")) p.su = atoi(e);
     p.grid = std::max(1, std::min(nblk, 1024));
     p.lds = mvs_lds_bytes(false, cols) + 32 * 4;
     return p;

@@ -29,7 +29,7 @@ hipError_t launch_mvs_gu_q8_0(const MvsPlan &p, hipStream_t st, const MvsArgs &a
                            dim3(NW * 64), p.lds, st, a);                                        \
         return hipSuccess;                                                                       \
     }
-    G(1, 8) G(2, 8) G(1, 4) G(2, 4)
+    G(1, 8) G(2, 8) G(1, 4) G(2, 4) G(1, 16) G(2, 16) G(1, 2) G(2, 2)
 #undef G
     return hipErrorNotSupported;
 }
