@@ -87,35 +87,47 @@ def _omode(oracle, kv):
             FL_KV_KIVI2: oracle.OR_KV_KIVI32}[kv]
 
 
-@pytest.mark.parametrize("name", list(MODELS))
-@pytest.mark.parametrize("kv", list(KV))
-def test_verify_matches_sequential_decode(backend, oracle, name, kv):
-    spec = MODELS[name]
-    M, n_prompt = 8, 40
-    print(f"[verify] {name} kv={kv}", flush=True)
-    model = S.make_model(spec, seed=6)
-    prompt = S.random_tokens(106, n_prompt, spec.vocab)
-    drafts = S.random_tokens(206, M, spec.vocab)
-    backend.init_gpu_kv_cache(spec, KV[kv])
+def _check_verify(backend, oracle, spec, kv, n_prompt, seed):
+    M = 8
+    model = S.make_model(spec, seed=seed)
+    prompt = S.random_tokens(seed + 100, n_prompt, spec.vocab)
+    drafts = S.random_tokens(seed + 200, M, spec.vocab)
+    backend.init_gpu_kv_cache(spec, kv)
     backend.upload_weights_to_gpu(model)
-    for pos, t in enumerate(prompt):
-        backend.forward_greedy(int(t), pos)
+    backend.generate(prompt, 1)  # positions 0..n_prompt-1
     got, vals = backend.verify(drafts, n_prompt)
-    # the GPU's own sequential decode over the same drafts
-    seq = [backend.forward_greedy(int(t), n_prompt + i) for i, t in enumerate(drafts)]
+    # the GPU's own sequential decode over the same drafts, full logits
+    seq = [backend.forward_single_token_gpu(int(t), n_prompt + i) for i, t in enumerate(drafts)]
     # oracle logits for the near-tie margin
-    om = oracle.OracleModel(model, _omode(oracle, KV[kv]))
+    om = oracle.OracleModel(model, _omode(oracle, kv))
     for pos, t in enumerate(prompt):
         om.forward_greedy(int(t), pos)
     checked = 0
     for i, t in enumerate(drafts):
         logits = om.forward_logits(int(t), n_prompt + i)
         top2 = np.sort(logits)[-2:]
-        assert abs(vals[i] - seq[i][1]) <= 1e-2 * abs(seq[i][1]) + 1e-6, (i, vals[i], seq[i])
+        # verify's winning logit equals sequential decode's logit of that token
+        assert abs(vals[i] - seq[i][got[i]]) <= 1e-2 * abs(top2[1]), (i, vals[i], seq[i][got[i]])
         if top2[1] - top2[0] > MARGIN * abs(top2[1]):
-            assert got[i] == seq[i][0] == int(np.argmax(logits)), (i, got[i], seq[i], int(np.argmax(logits)))
+            assert got[i] == int(np.argmax(seq[i])) == int(np.argmax(logits)), (i, got[i], int(np.argmax(seq[i])))
             checked += 1
     assert checked >= M // 2
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+@pytest.mark.parametrize("kv", list(KV))
+def test_verify_matches_sequential_decode(backend, oracle, name, kv):
+    print(f"[verify] {name} kv={kv}", flush=True)
+    _check_verify(backend, oracle, MODELS[name], KV[kv], 40, 6)
+
+
+@pytest.mark.parametrize("kv", ["f16", "q8", "kivi"])
+def test_verify_long_context_split_attention(backend, oracle, kv):
+    """Context above one attention split (1100 tokens): every draft query
+    merges several split partials of its own."""
+    print(f"[verify-long] kv={kv}", flush=True)
+    spec = S.tiny_spec(FL_Q8_0, heads=8, kv_heads=2, head_dim=128, hidden=512, inter=768, max_seq=1200)
+    _check_verify(backend, oracle, spec, KV[kv], 1100, 16)
 
 
 def test_verify_accepts_sequential_greedy_stream(backend, oracle):
