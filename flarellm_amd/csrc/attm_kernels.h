@@ -1,4 +1,4 @@
-// Split-K GQA decode attention on f16 MFMA (fp16 and Q8 KV caches).
+// Split-K GQA decode attention on f16 MFMA (fp16, Q8 and KIVI2 KV caches).
 //
 // Same semantics as k_attn (cpu_grouped_query_attention_into,
 // flare-core/src/model.rs:9849-9966; online softmax of
@@ -15,6 +15,11 @@
 //    [kv head][slot / 32][channel][32 slots].
 // Q8 caches: K block scale applied per (token, 32-channel block) to each
 // block's MFMA result; V scales folded into P per block.
+// KIVI2 caches: 2-bit codes are exact in f16; K (scale, min) per channel
+// folds the scale into the query operand and adds sum(q * min) per head, V
+// (scale, min) per (token, 32 channels) folds the scale into P and adds
+// sum(p * min) per (head, channel group).  Tokens above the quantized prefix
+// come from the fp16 ring exactly as for an fp16 cache.
 #pragma once
 
 #include "attn_kernels.h"
@@ -112,6 +117,81 @@ struct AttmTile<KvQ8, D> {
     }
 };
 
+// N consecutive 32-bit words (N = 1, 2, 4) in one load
+template <int N>
+__device__ __forceinline__ void ld_words(const void *p, uint32_t *w) {
+    if constexpr (N == 4) {
+        const v4i_t v = *(const v4i_t *)p;
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (N == 2) {
+        const v2i_t v = *(const v2i_t *)p;
+        w[0] = v.x; w[1] = v.y;
+    } else {
+        w[0] = *(const uint32_t *)p;
+    }
+}
+
+// KIVI2, a block of the 2-bit prefix: the lane's codes (K: 8 channels of
+// every 32-channel tile for its slot; V: 8 slots of its channel in every
+// 16-channel tile) and the block's (scale, min) pairs, all in one flight.
+template <int D>
+struct AttmKiviQ {
+    static constexpr int DT = D / 32, KW = D / 64;
+    uint32_t k[2][KW];  // [slot half] 16 bits per 32-channel tile
+    uint32_t v[DT];     // 16 bits per 16-channel tile
+    uint32_t kp[KW];    // K pairs of channels lane + 64i (the block's group)
+    uint32_t vp[DT];    // V pairs of slot tb + lane % 32, per 32-channel group
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
+        const int kg = lane >> 4, r = lane & 15;
+        const uint8_t *kc = (const uint8_t *)a.kc, *vc = (const uint8_t *)a.vc;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int t = min(tb + 16 * h + r, tlast);
+            ld_words<KW>(kc + ((size_t)kvh * a.S + t) * (D / 4) + kg * (D / 16), k[h]);
+        }
+        const size_t gi = (size_t)kvh * (a.S >> 5) + (tb >> 5);
+        ld_words<DT>(vc + gi * (size_t)(D * 8) + (kg * 16 + r) * (D / 16) * 2, v);
+#pragma unroll
+        for (int i = 0; i < KW; i++) kp[i] = a.kp[gi * D + lane + 64 * i];
+        const int t = min(tb + (lane & 31), tlast);
+        ld_words<DT>(a.vp + ((size_t)kvh * a.S + t) * DT, vp);
+    }
+};
+
+// KIVI2, a block of the fp16 ring: K rows and transposed V as for fp16
+template <int D>
+struct AttmTile<KvKivi, D> {
+    static constexpr int DT = D / 32, NT = D / 16;
+    v4i_t k[2][DT];
+    v4i_t v[NT];
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
+        const int kg = lane >> 4, r = lane & 15;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int t = min(tb + 16 * h + r, tlast);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) k[h][dt] = *(const v4i_t *)(a.rk + kivi_ring_k(kvh, t, 32 * dt + 8 * kg, D));
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) v[nt] = *(const v4i_t *)(a.rv + kivi_ring_v(kvh, tb, 16 * nt + r, D) + 8 * kg);
+    }
+};
+
+// 8 two-bit codes (bits 2j of w, w < 2^16) -> f16 0..3, exact: code 2i to
+// bits 4i, code 2i+1 to bits 16+4i, then each half-word of 0x6400 | c is
+// binary16 1024 + c, and subtracting 1024 leaves c.
+__device__ __forceinline__ v8h_t c2x8_to_h8(uint32_t w) {
+    const uint32_t t = (w & 0x3333u) | ((w & 0xCCCCu) << 14);
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) d[i] = ((t >> (4 * i)) & 0x00030003u) | 0x64006400u;
+    v8h_t r;
+    __builtin_memcpy(&r, d, 16);
+    const _Float16 k = (_Float16)1024.0f;
+    const v8h_t bias = {k, k, k, k, k, k, k, k};
+    return r - bias;
+}
+
 // One workgroup = (split s, kv head kvh, query z); waves take 32-token
 // blocks of the split's chunk round-robin.
 template <typename KT, int D, int G>
@@ -128,6 +208,12 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     __shared__ int is_last;
     __shared__ int8_t nk[D], nv[D];              // Q8 decode step: the new token's codes
     __shared__ uint16_t nks[D / 32], nvs[D / 32];  // and scales
+    constexpr bool KIVI = std::is_same<KT, KvKivi>::value;
+    __shared__ uint32_t kpar[KIVI ? NW : 1][KIVI ? D : 1];   // KIVI: K (scale, min) of the block's group
+    __shared__ float vmn[KIVI ? NW : 1][KIVI ? kAttmBlock : 1][KIVI ? DT : 1];  // KIVI: V min per (slot, 32-ch group)
+    __shared__ float kbias[KIVI ? NW : 1][G], vbias[KIVI ? NW : 1][G][DT];
+    __shared__ uint16_t nkh[KIVI ? D : 1], nvh[KIVI ? D : 1];  // KIVI decode step: the new token in binary16
+    __shared__ float qs[KIVI ? G : 1][KIVI ? D : 1];             // KIVI: the query rows
 
     AttnArgs a = a0;
     const int zq = (int)blockIdx.z;
@@ -161,8 +247,13 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
 
     // the first block's K / V loads go out before the query setup
     const int nblk = (t1 - t0 + kAttmBlock - 1) / kAttmBlock;
-    AttmTile<KT, D> tile;
-    if (wave < nblk) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
+    // KIVI: blocks [0, nqb) of the chunk come from the 2-bit prefix (qlen
+    // and t0 are multiples of 32), the rest from the fp16 ring
+    const int qlen = kivi_qlen(T);
+    const int nqb = KIVI ? min(nblk, max(0, (qlen - t0) / kAttmBlock)) : 0;
+    using Tile0 = typename std::conditional<KIVI, AttmKiviQ<D>, AttmTile<KT, D>>::type;
+    Tile0 tile;
+    if (wave < (KIVI ? nqb : nblk)) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
 
     // A operand of S: row m = 2g + (hi / lo) of head g (rows >= 2G zero)
     v8h_t aq[DT];
@@ -177,12 +268,20 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) x[i] = 0.0f;
             }
+            if constexpr (KIVI) {
+                // the f32 query in LDS (scaled per 2-bit channel in each quantized block)
+                if (!(m & 1) && (m >> 1) < G) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) qs[g][32 * dt + 8 * kg + i] = x[i];
+                }
+            }
             v8h_t hi, lo;
             split8(x, hi, lo);
             aq[dt] = (m & 1) ? lo : hi;
         }
     }
     const float scale = 1.0f / sqrtf((float)D);
+    if constexpr (KIVI) __syncthreads();  // qs
     ATTN_TS(1);
 
     // wave-private online softmax state; lane group kg holds heads 2kg, 2kg+1
@@ -192,7 +291,10 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
 
     // one 32-slot block (slots tb .. tb+31) with its tile in registers
-    auto process = [&](AttmTile<KT, D> &tile, int bi) {
+    auto process = [&](auto &tile, int bi) {
+        using TT = typename std::remove_reference<decltype(tile)>::type;
+        constexpr bool KQ = std::is_same<TT, AttmKiviQ<D>>::value;                 // 2-bit block
+        constexpr bool H16 = std::is_same<KT, __half>::value || (KIVI && !KQ);    // fp16 operands
         const int tb = t0 + bi * kAttmBlock;
         if constexpr (std::is_same<KT, KvQ8>::value) {
             // Q8 decode step: the block holding slot pos quantizes the new
@@ -236,14 +338,105 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
                 }
             }
         }
+        v8h_t ak[KQ ? DT : 1];
+        if constexpr (KIVI) if constexpr (!KQ) {
+            if (has_new && pos >= tb && pos < tb + kAttmBlock) {
+                // decode step: the new token goes into the ring (binary16); the
+                // block holding it patches its K row / V column in registers
+                const int c = lane % (D / 8);
+                nrow.build(a, kvh, c);
+                if (lane < D / 8) {
+                    nrow.store(a, kvh, pos, c);
+                    *(v4i_t *)(nkh + 8 * c) = nrow.k;
+                    *(v4i_t *)(nvh + 8 * c) = nrow.v;
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();
+                const int pi = pos - tb, th = pi >> 4;
+                if ((pi & 15) == r) {
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        if (h == th) {
+#pragma unroll
+                            for (int dt = 0; dt < DT; dt++) tile.k[h][dt] = *(const v4i_t *)(nkh + 32 * dt + 8 * kg);
+                        }
+                }
+                if ((pi >> 3) == kg) {
+                    const int e = pi & 7, sh = 16 * (e & 1);
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        const uint32_t hv = nvh[16 * nt + r];
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            if (j == (e >> 1)) {
+                                const uint32_t w = (uint32_t)tile.v[nt][j];
+                                tile.v[nt][j] = (int)((w & ~(0xFFFFu << sh)) | (hv << sh));
+                            }
+                    }
+                }
+            }
+        }
+        if constexpr (KQ) {
+            {
+                // stage the group's K (scale, min) and the slots' V (scale, min)
+#pragma unroll
+                for (int i = 0; i < TT::KW; i++) kpar[wave][lane + 64 * i] = tile.kp[i];
+                if (lane < kAttmBlock) {
+                    const bool okt = tb + lane < t1;
+#pragma unroll
+                    for (int b = 0; b < DT; b++) {
+                        const uint32_t sm = okt ? tile.vp[b] : 0u;
+                        const float sv = h2f((uint16_t)(sm & 0xFFFF));
+                        vsc[wave][lane][b] = sv;
+                        vmn[wave][lane][b] = h2f((uint16_t)(sm >> 16));
+                        float mx = row_max<16>(sv);
+                        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                        if (lane == 0) vmax[wave][b] = mx;
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();
+                // A operand (q * scale, high / residual) and the bias sum(q * min)
+                float kb = 0.0f;
+                const int gq = min(r >> 1, G - 1);
+                const float qz = (r >> 1) < G ? 1.0f : 0.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t sm = kpar[wave][32 * dt + 8 * kg + i];
+                        const float qv = qs[gq][32 * dt + 8 * kg + i] * qz;
+                        x[i] = qv * h2f((uint16_t)(sm & 0xFFFF));
+                        kb += qv * h2f((uint16_t)(sm >> 16));
+                    }
+                    v8h_t hi, lo;
+                    split8(x, hi, lo);
+                    ak[dt] = (r & 1) ? lo : hi;
+                }
+                kb += __shfl_xor(kb, 16, 64);
+                kb += __shfl_xor(kb, 32, 64);
+                if (kg == 0 && !(r & 1) && (r >> 1) < G) kbias[wave][r >> 1] = kb;
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
         // ---- scores: two 16-slot halves -------------------------------------
         float sc[2][2];  // [half][head parity] for slot tb + 16h + r
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             v4f32_t acc = v4f32_t{0.f, 0.f, 0.f, 0.f};
-            if constexpr (std::is_same<KT, __half>::value) {
+            float kbh[2] = {0.0f, 0.0f};
+            if constexpr (H16) {
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) acc = mfma16(aq[dt], as_h8(tile.k[h][dt]), acc);
+            } else if constexpr (KQ) {
+                // codes of this lane's slot: 16 bits per 32-channel tile
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+                    acc = mfma16(ak[dt], c2x8_to_h8((tile.k[h][dt >> 1] >> (16 * (dt & 1))) & 0xFFFFu), acc);
+                kbh[0] = 2 * kg < G ? kbias[wave][2 * kg] : 0.0f;
+                kbh[1] = 2 * kg + 1 < G ? kbias[wave][2 * kg + 1] : 0.0f;
             } else {
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) {
@@ -256,8 +449,8 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
             }
             const int t = tb + 16 * h + r;
             const bool ok = t < t1;
-            sc[h][0] = ok ? (acc[0] + acc[1]) * scale : -INFINITY;
-            sc[h][1] = ok ? (acc[2] + acc[3]) * scale : -INFINITY;
+            sc[h][0] = ok ? (acc[0] + acc[1] + kbh[0]) * scale : -INFINITY;
+            sc[h][1] = ok ? (acc[2] + acc[3] + kbh[1]) * scale : -INFINITY;
         }
         if (bi == wave) ATTN_TS(2);
         // ---- online softmax per head (rows of 16 lanes hold one head pair) --
@@ -307,12 +500,51 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
             float p[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) p[i] = g < G ? sp[wave][g][8 * kg + i] : 0.0f;
-            if constexpr (std::is_same<KT, __half>::value) {
+            if constexpr (H16) {
                 v8h_t hi, lo;
                 split8(p, hi, lo);
                 const v8h_t ap = (m & 1) ? lo : hi;
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) oacc[nt] = mfma16(ap, as_h8(tile.v[nt]), oacc[nt]);
+            } else if constexpr (KQ) {
+                {
+                    // codes * scale via MFMA (scales folded into P as for Q8),
+                    // plus the bias sum_t p_t min_t per (head, 32-channel group)
+                    const uint32_t *vw = tile.v;
+#pragma unroll
+                    for (int b = 0; b < DT; b++) {
+                        const float vref = vmax[wave][b];
+                        const float inv = vref > 0.0f ? 1.0f / vref : 0.0f;
+                        float pb[8], vb = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) {
+                            pb[i] = p[i] * (vsc[wave][8 * kg + i][b] * inv);
+                            vb += p[i] * vmn[wave][8 * kg + i][b];
+                        }
+                        vb += __shfl_xor(vb, 16, 64);
+                        vb += __shfl_xor(vb, 32, 64);
+                        if (kg == 0 && !(m & 1) && g < G) vbias[wave][g][b] = vb;
+                        v8h_t hi, lo;
+                        split8(pb, hi, lo);
+                        const v8h_t ap = (m & 1) ? lo : hi;
+#pragma unroll
+                        for (int u = 0; u < 2; u++) {
+                            const int nt = 2 * b + u;
+                            const v4f32_t part = mfma16(ap, c2x8_to_h8((vw[nt >> 1] >> (16 * (nt & 1))) & 0xFFFFu),
+                                                        v4f32_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                            for (int i = 0; i < 4; i++) oacc[nt][i] += part[i] * vref;
+                        }
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __builtin_amdgcn_wave_barrier();
+                    // rows 4kg + i of oacc: head 2kg + i/2, (hi, lo); the bias goes on the hi row
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        if (2 * kg < G) oacc[nt][0] += vbias[wave][2 * kg][nt >> 1];
+                        if (2 * kg + 1 < G) oacc[nt][2] += vbias[wave][2 * kg + 1][nt >> 1];
+                    }
+                }
             } else {
                 // V scales folded into P relative to the block's largest
                 // scale (keeps the f16 residual out of the subnormal range),
@@ -349,11 +581,39 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
             if (bi + 2 * NW < nblk) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
             process(tile2, bi + NW);
         }
+    } else if constexpr (KIVI) {
+        // 2-bit blocks ping-pong (small tiles), then the ring blocks
+        Tile0 tile2;
+        for (int bi = wave; bi < nqb; bi += 2 * NW) {
+            if (bi + NW < nqb) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
+            process(tile, bi);
+            if (bi + NW >= nqb) break;
+            if (bi + 2 * NW < nqb) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
+            process(tile2, bi + NW);
+        }
+        AttmTile<KvKivi, D> rt;
+        const int bi0 = nqb > wave ? wave + (nqb - wave + NW - 1) / NW * NW : wave;
+        for (int bi = bi0; bi < nblk; bi += NW) {
+            rt.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
+            process(rt, bi);
+        }
     } else {
         // Q8 (more registers per block): one tile, loaded at the top
         for (int bi = wave; bi < nblk; bi += NW) {
             if (bi != wave) tile.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
             process(tile, bi);
+        }
+    }
+    if constexpr (KIVI) {
+        // decode step that ages group qlen/32 out of the fp16 residual: split
+        // 0 moves it from the ring into the 2-bit store (its tokens are read
+        // from the ring by every split of this step, from the store after it)
+        if (has_new && s == 0 && kivi_qlen(T + 1) > qlen) {
+            const __half *rk = a.rk, *rv = a.rv;
+            auto src = [&](int t, int ch, bool is_v) -> float {
+                return __half2float(is_v ? rv[kivi_ring_v(kvh, t, ch, D)] : rk[kivi_ring_k(kvh, t, ch, D)]);
+            };
+            kivi_quantize_group(a, D, kvh, qlen / kKiviGroup, src, &red[0][0]);
         }
     }
 

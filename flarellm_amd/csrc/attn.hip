@@ -34,15 +34,17 @@ hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &
     if (nq < 1) return hipErrorInvalidValue;
     if (nq > 1 && a.knew) return hipErrorInvalidValue;  // new-token stores are single-query
     // model caches in fp16 / Q8 (V in transposed blocks): the MFMA kernel
-    if ((kvfmt == KV_F16 && a.v_tblk) || kvfmt == KV_Q8) {
-        if (!a.v_tblk || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32) return hipErrorInvalidValue;
-        return kvfmt == KV_F16 ? launch_attm_t<__half>(D, G, st, a, nq) : launch_attm_t<KvQ8>(D, G, st, a, nq);
+    if ((kvfmt == KV_F16 && a.v_tblk) || kvfmt == KV_Q8 || kvfmt == KV_KIVI) {
+        if ((kvfmt != KV_KIVI && !a.v_tblk) || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32)
+            return hipErrorInvalidValue;
+        if (kvfmt == KV_F16) return launch_attm_t<__half>(D, G, st, a, nq);
+        if (kvfmt == KV_Q8) return launch_attm_t<KvQ8>(D, G, st, a, nq);
+        return launch_attm_t<KvKivi>(D, G, st, a, nq);
     }
     if (a.nsplit < 1 || a.nsplit > kAttnMaxSplit) return hipErrorInvalidValue;
     switch (kvfmt) {
     case KV_F32: return launch_attn_t<float>(D, G, st, a, nq);
     case KV_F16: return launch_attn_t<__half>(D, G, st, a, nq);
-    case KV_KIVI: return launch_attn_t<KvKivi>(D, G, st, a, nq);
     }
     return hipErrorNotSupported;
 }
@@ -87,16 +89,16 @@ __global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *kr
 // rounded to binary16 first, as the ring would hold them.
 __global__ __launch_bounds__(256) void k_kv_kivi_groups(AttnArgs a, const float *krows, const float *vrows, int p0,
                                                         int n, int D, int g0) {
+    __shared__ float lds[3 * kKiviGroup * 4];
     const int gi = g0 + (int)blockIdx.x, kvh = (int)blockIdx.y;
     auto src = [&](int t, int ch, bool is_v) -> float {
         if (t >= p0) {
             const float *r = is_v ? vrows : krows;
             return __half2float(__float2half(r[((size_t)(t - p0) * a.nkv + kvh) * D + ch]));
         }
-        const __half *r = is_v ? a.rv : a.rk;
-        return __half2float(r[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch]);
+        return is_v ? __half2float(a.rv[kivi_ring_v(kvh, t, ch, D)]) : __half2float(a.rk[kivi_ring_k(kvh, t, ch, D)]);
     };
-    kivi_quantize_group(a, D, kvh, gi, src);
+    kivi_quantize_group(a, D, kvh, gi, src, lds);
 }
 
 // KIVI step 2: the newest rows (at most kKiviRing) into the fp16 ring.
@@ -107,7 +109,8 @@ __global__ __launch_bounds__(256) void k_kv_kivi_ring(AttnArgs a, const float *k
     for (int e = threadIdx.x; e < 2 * D; e += blockDim.x) {
         const int isv = e >= D, ch = e % D;
         const float v = (isv ? vrows : krows)[((size_t)r * a.nkv + kvh) * D + ch];
-        (isv ? a.rv : a.rk)[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch] = __float2half(v);
+        if (isv) a.rv[kivi_ring_v(kvh, t, ch, D)] = __float2half(v);
+        else a.rk[kivi_ring_k(kvh, t, ch, D)] = __float2half(v);
     }
 }
 

@@ -55,6 +55,7 @@ constexpr int kKiviResidual = 128;  // at least this many newest tokens are fp16
 // ring slots per kv head: the window plus two groups, so a verify batch of up
 // to 32 tokens still finds every query's window tokens in the ring
 constexpr int kKiviRing = kKiviResidual + 2 * kKiviGroup;
+static_assert(kKiviRing % 32 == 0, "ring blocks of 32 slots");
 // Tokens [0, kivi_qlen(T)) of a T-token cache are read from the 2-bit groups,
 // [kivi_qlen(T), T) from the ring (between 129 and 160 tokens once T > 128).
 __host__ __device__ inline int kivi_qlen(int T) {
@@ -131,9 +132,6 @@ struct KiviQ {
     }
     __device__ __forceinline__ uint32_t packed() const { return (uint32_t)f2h(scale) | ((uint32_t)f2h(mn) << 16); }
 };
-__device__ __forceinline__ float kivi_deq(uint32_t code, uint32_t sm) {
-    return (float)code * h2f((uint16_t)(sm & 0xFFFF)) + h2f((uint16_t)(sm >> 16));
-}
 
 // One token's K and V elements [8c, 8c+8) for kv head kvh, kept raw in
 // registers and decoded at use.
@@ -142,7 +140,7 @@ struct KVRow;
 template <>
 struct KVRow<float> {
     v4f_t k0, k1, v0, v1;
-    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c) {
         const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
         const v4f_t *kp = (const v4f_t *)((const float *)a.kc + o), *vp = (const v4f_t *)((const float *)a.vc + o);
         k0 = kp[0]; k1 = kp[1]; v0 = vp[0]; v1 = vp[1];
@@ -157,7 +155,7 @@ struct KVRow<float> {
 template <>
 struct KVRow<__half> {
     v4i_t k, v;
-    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int) {
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c) {
         const size_t o = (size_t)kvh * a.head_stride + (size_t)t * a.tok_stride + 8 * c;
         k = *(const v4i_t *)((const __half *)a.kc + o);
         v = *(const v4i_t *)((const __half *)a.vc + o);
@@ -165,54 +163,6 @@ struct KVRow<__half> {
     __device__ __forceinline__ void getk(float *o) const { h8_to_f32(k, o); }
     __device__ __forceinline__ void getv(float *o) const { h8_to_f32(v, o); }
 };
-// KIVI: tokens below qlen from the 2-bit groups, the rest from the fp16 ring.
-// Quantized token: x.x = K codes | V codes << 16 (8 channels x 2 bits each),
-// x.y = V (scale, min) of the channel group; y / z = K (scale, min) of the 8
-// channels.  Ring token: x = K halves, y = V halves.
-template <>
-struct KVRow<KvKivi> {
-    v4i_t x, y, z;
-    bool ring;
-    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int t, int c, int qlen) {
-        const int D = (int)a.tok_stride;
-        ring = t >= qlen;
-        if (ring) {
-            const size_t o = ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + 8 * c;
-            x = *(const v4i_t *)(a.rk + o);
-            y = *(const v4i_t *)(a.rv + o);
-        } else {
-            const size_t ro = ((size_t)kvh * a.S + t) * (D >> 2) + 2 * c;
-            const uint32_t kc = *(const uint16_t *)((const uint8_t *)a.kc + ro);
-            const uint32_t vc = *(const uint16_t *)((const uint8_t *)a.vc + ro);
-            x.x = (int)(kc | (vc << 16));
-            x.y = (int)a.vp[((size_t)kvh * a.S + t) * (D >> 5) + (c >> 2)];
-            const v4i_t *kp = (const v4i_t *)(a.kp + ((size_t)kvh * (a.S >> 5) + (t >> 5)) * D + 8 * c);
-            y = kp[0];
-            z = kp[1];
-        }
-    }
-    __device__ __forceinline__ void getk(float *o) const {
-        if (ring) {
-            h8_to_f32(x, o);
-        } else {
-            const uint32_t codes = (uint32_t)x.x;
-            const uint32_t sm[8] = {(uint32_t)y.x, (uint32_t)y.y, (uint32_t)y.z, (uint32_t)y.w,
-                                    (uint32_t)z.x, (uint32_t)z.y, (uint32_t)z.z, (uint32_t)z.w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = kivi_deq((codes >> (2 * i)) & 3u, sm[i]);
-        }
-    }
-    __device__ __forceinline__ void getv(float *o) const {
-        if (ring) {
-            h8_to_f32(y, o);
-        } else {
-            const uint32_t codes = (uint32_t)x.x >> 16, sm = (uint32_t)x.y;
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = kivi_deq((codes >> (2 * i)) & 3u, sm);
-        }
-    }
-};
-
 // The new token's row for the Q8 / KIVI decode step: every thread builds the
 // stored form of elements [8c, 8c+8) from the f32 QKV output (Q8: the four
 // lanes of a 32-block agree on its scale through DPP; KIVI: binary16), so the
@@ -220,7 +170,6 @@ struct KVRow<KvKivi> {
 template <typename KT>
 struct NewRow {
     __device__ __forceinline__ void build(const AttnArgs &, int, int) {}
-    __device__ __forceinline__ void apply(KVRow<KT> &) const {}
     __device__ __forceinline__ void store(const AttnArgs &, int, int, int) const {}
 };
 __device__ __forceinline__ void q8_block8(const float *x, v2i_t &q, uint16_t &s) {
@@ -271,9 +220,31 @@ struct NewRow<KvQ8> {
         }
     }
 };
+// KIVI code placement.
+//  K (token rows of D/4 bytes): channel c = 32dt + 8kg + j sits at byte
+//    kg*(D/16) + 2dt + j/4, bits 2(j%4), so the codes an MFMA lane group kg
+//    needs for one token (8 channels of every 32-channel tile) are contiguous.
+//  V (D*8 bytes per 32-token group): channel c = 16nt + r and group token
+//    8kg + j sit at byte ((kg*16 + r)*(D/16) + nt)*2 + j/4, bits 2(j%4): one
+//    lane (kg, r) reads the 8 tokens of its channel in every 16-channel tile.
+__host__ __device__ inline int kivi_kbyte(int c, int D) {
+    return ((c & 31) >> 3) * (D / 16) + 2 * (c >> 5) + ((c & 7) >> 2);
+}
+__host__ __device__ inline int kivi_vbyte(int c, int tl, int D) {
+    return (((tl >> 3) * 16 + (c & 15)) * (D / 16) + (c >> 4)) * 2 + ((tl & 7) >> 2);
+}
+// ring slot of token t; the ring V is stored in 32-slot transposed blocks
+__host__ __device__ inline size_t kivi_ring_k(int kvh, int t, int c, int D) {
+    return ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + c;
+}
+__host__ __device__ inline size_t kivi_ring_v(int kvh, int t, int c, int D) {
+    const int sl = t % kKiviRing;
+    return (size_t)kvh * kKiviRing * D + ((size_t)(sl >> 5) * D + c) * 32 + (sl & 31);
+}
+
 template <>
 struct NewRow<KvKivi> {
-    v4i_t k, v;
+    v4i_t k, v;  // binary16 K / V of channels [8c, 8c+8)
     __device__ __forceinline__ void build(const AttnArgs &a, int kvh, int c) {
         const int D = (int)a.tok_stride;
         float kx[8], vx[8];
@@ -285,62 +256,82 @@ struct NewRow<KvKivi> {
         k = f32_to_h8(kx);
         v = f32_to_h8(vx);
     }
-    __device__ __forceinline__ void apply(KVRow<KvKivi> &row) const {
-        row.ring = true;
-        row.x = k;
-        row.y = v;
-    }
     __device__ __forceinline__ void store(const AttnArgs &a, int kvh, int t, int c) const {
         const int D = (int)a.tok_stride;
-        const size_t o = ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + 8 * c;
-        *(v4i_t *)(a.rk + o) = k;
-        *(v4i_t *)(a.rv + o) = v;
+        *(v4i_t *)(a.rk + kivi_ring_k(kvh, t, 8 * c, D)) = k;
+        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            ((uint16_t *)a.rv)[kivi_ring_v(kvh, t, 8 * c + i, D)] = (uint16_t)((w[i >> 1] >> (16 * (i & 1))) & 0xFFFF);
     }
 };
 
 // Quantize KIVI group gi of kv head kvh (tokens [32gi, 32gi+32)) into the
-// 2-bit store.  src(t, ch) returns the fp16-rounded value of token t, channel
-// ch (is_v selects V).  Uses threads [0, D/4) for K (4 channels each, per
-// channel over the 32 tokens) and [128, 128 + D) for V (one token x one
-// 32-channel group each).  No barrier inside: the caller's threads run it once.
+// 2-bit store.  src(t, ch, is_v) returns the binary16-rounded value of token
+// t, channel ch.  Every thread of the workgroup must call it (it holds
+// barriers); lds: 3 * 32 * (D/32) floats of workgroup scratch.
+//  K: per channel over the 32 tokens (4 channels = one code byte per thread).
+//  V: per token over each 32-channel group, then one code byte (4 tokens of
+//     one channel) per thread.
 template <typename Src>
-__device__ __forceinline__ void kivi_quantize_group(const AttnArgs &a, int D, int kvh, int gi, Src src) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void kivi_quantize_group(const AttnArgs &a, int D, int kvh, int gi, Src src, float *lds) {
+    const int tid = threadIdx.x, nt = blockDim.x, DT = D >> 5;
     const int t0 = gi * kKiviGroup;
-    if (tid < D / 4) {
+    for (int idx = tid; idx < D / 4; idx += nt) {
         KiviQ qz[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float lo = INFINITY, hi = -INFINITY;
             for (int t = 0; t < kKiviGroup; t++) {
-                const float v = src(t0 + t, 4 * tid + i, false);
+                const float v = src(t0 + t, 4 * idx + i, false);
                 lo = v < lo ? v : lo;
                 hi = v > hi ? v : hi;
             }
             qz[i].init(lo, hi);
-            a.kp[((size_t)kvh * (a.S >> 5) + gi) * D + 4 * tid + i] = qz[i].packed();
+            a.kp[((size_t)kvh * (a.S >> 5) + gi) * D + 4 * idx + i] = qz[i].packed();
         }
+        const int kb = kivi_kbyte(4 * idx, D);
         for (int t = 0; t < kKiviGroup; t++) {
             uint32_t b = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) b |= qz[i].code(src(t0 + t, 4 * tid + i, false)) << (2 * i);
-            ((uint8_t *)a.kc)[((size_t)kvh * a.S + t0 + t) * (D >> 2) + tid] = (uint8_t)b;
+            for (int i = 0; i < 4; i++) b |= qz[i].code(src(t0 + t, 4 * idx + i, false)) << (2 * i);
+            ((uint8_t *)a.kc)[((size_t)kvh * a.S + t0 + t) * (D >> 2) + kb] = (uint8_t)b;
         }
-    } else if (tid >= 128 && tid < 128 + D) {
-        const int t = t0 + ((tid - 128) % kKiviGroup), cg = (tid - 128) / kKiviGroup;
+    }
+    // V parameters per (token, 32-channel group)
+    for (int idx = tid; idx < kKiviGroup * DT; idx += nt) {
+        const int tl = idx % kKiviGroup, cg = idx / kKiviGroup;
         float lo = INFINITY, hi = -INFINITY;
         for (int i = 0; i < kKiviGroup; i++) {
-            const float v = src(t, 32 * cg + i, true);
+            const float v = src(t0 + tl, 32 * cg + i, true);
             lo = v < lo ? v : lo;
             hi = v > hi ? v : hi;
         }
         KiviQ qz;
         qz.init(lo, hi);
-        a.vp[((size_t)kvh * a.S + t) * (D >> 5) + cg] = qz.packed();
-        uint32_t w[2] = {0u, 0u};
-        for (int i = 0; i < kKiviGroup; i++) w[i >> 4] |= qz.code(src(t, 32 * cg + i, true)) << (2 * (i & 15));
-        *(v2i_t *)((uint8_t *)a.vc + ((size_t)kvh * a.S + t) * (D >> 2) + 8 * cg) = v2i_t{(int)w[0], (int)w[1]};
+        a.vp[((size_t)kvh * a.S + t0 + tl) * DT + cg] = qz.packed();
+        lds[3 * idx] = qz.mn;
+        lds[3 * idx + 1] = qz.inv;
+        lds[3 * idx + 2] = qz.scale;
     }
+    __syncthreads();
+    // V codes: one byte = 4 tokens of one channel
+    uint8_t *vg = (uint8_t *)a.vc + ((size_t)kvh * (a.S >> 5) + gi) * (size_t)(D * 8);
+    for (int idx = tid; idx < D * 8; idx += nt) {
+        const int c = idx >> 3, q = idx & 7;
+        uint32_t b = 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const int tl = 4 * q + jj, li = (c >> 5) * kKiviGroup + tl;
+            KiviQ qz;
+            qz.mn = lds[3 * li];
+            qz.inv = lds[3 * li + 1];
+            qz.scale = lds[3 * li + 2];
+            b |= qz.code(src(t0 + tl, c, true)) << (2 * jj);
+        }
+        vg[kivi_vbyte(c, 4 * q, D)] = (uint8_t)b;
+    }
+    __syncthreads();
 }
 
 constexpr int kAttnThreads = 256;  // 4 waves per workgroup
@@ -404,24 +395,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a0) {
     if (t0 >= T) return;
     const int t1 = min(T, t0 + CH);
     const int nact = (T + CH - 1) / CH;
-    const int qlen = kivi_qlen(T);
-
-    // the new token (Q8 / KIVI decode step) in its stored form
-    NewRow<KT> nrow;
-    const bool has_new = a.knew != nullptr;
-    if (has_new) nrow.build(a, kvh, c);
-
     KVRow<KT> rows[NP];
     auto fetch = [&](int tb) {
 #pragma unroll
         for (int p = 0; p < NP; p++) {
             const int tu = tb + tk + p * TPP;
             const int t = min(tu, t1 - 1);
-            rows[p].load(a, kvh, t, c, qlen);
-            if (has_new && tu == pos) {
-                nrow.apply(rows[p]);
-                nrow.store(a, kvh, pos, c);
-            }
+            rows[p].load(a, kvh, t, c);
         }
     };
     fetch(t0);
@@ -501,19 +481,6 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a0) {
         }
     }
     ATTN_TS(4);
-    if constexpr (std::is_same<KT, KvKivi>::value) {
-        // decode step T: the group that leaves the ring before step T+1 is
-        // quantized now (by split 0 of each kv head; no workgroup of this
-        // launch reads the 2-bit store of that group)
-        const int qn = kivi_qlen(T + 1);
-        if (has_new && s == 0 && qn > qlen) {
-            auto src = [&](int t, int ch, bool is_v) -> float {
-                const __half *r = is_v ? a.rv : a.rk;
-                return __half2float(r[((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + ch]);
-            };
-            kivi_quantize_group(a, D, kvh, qn / kKiviGroup - 1, src);
-        }
-    }
     // reduce o over the WPT token rows of the wave, then over the waves
 #pragma unroll
     for (int g = 0; g < G; g++)

@@ -917,7 +917,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         rope_row_host(c.head_dim, (int)p, c.rope_theta, &tab[p * half], &tab[S * half + p * half]);
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
-    if (kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) {
+    if (kv_format == FL_KV_F16 || kv_format == FL_KV_Q8 || kv_format == FL_KV_KIVI2) {
         // MFMA kernel: chunks of at least 512 slots (two 32-slot blocks per
         // wave, the second in flight while the first computes), at most
         // kAttmMaxSplit splits per kv head; up to kAttmSingle tokens the
@@ -931,7 +931,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     }
     if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
         const int ns = atoi(ev);
-        if (ns > 0 && ns <= ((kv_format == FL_KV_F16 || kv_format == FL_KV_Q8) ? kAttmMaxSplit : kAttnMaxSplit))
+        if (ns > 0 && ns <= (kv_format != FL_KV_F32 ? kAttmMaxSplit : kAttnMaxSplit))
             ctx->nsplit = ns;
     }
     const int G = c.num_heads / c.num_kv_heads;
