@@ -232,9 +232,9 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
     ATTN_TS(0);
     const int pos = *a.posp + zq, T = pos + 1;
-    // up to kAttmSingle tokens: one split (no cross-workgroup merge);
+    // up to a.single tokens: one split (no cross-workgroup merge);
     // beyond: chunks of at least chmin slots over the nsplit workgroups
-    int CH = T <= kAttmSingle ? T : max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
+    int CH = T <= a.single ? T : max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
     CH = (CH + kAttmBlock * NW - 1) / (kAttmBlock * NW) * (kAttmBlock * NW);
     const int t0 = s * CH;
     if (t0 >= T) return;
@@ -662,6 +662,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     }
     float *mo = &red[0][0];  // final output of this kv head (for the Q8 copy)
     if (nact == 1) {
+        ATTN_TS(4);
         __syncthreads();  // red is overwritten below
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
@@ -756,6 +757,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         ATTN_TSL(8);
     }
     __syncthreads();
+    if (nact == 1) ATTN_TS(6);
     if (a.oq) {
         // Q8_0 copy of this kv head's G*D outputs (quantize_input_q8_0_into), 32 lanes per block
         const int nb = G * D / 32;
@@ -765,6 +767,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         }
     }
     if (nact > 1) ATTN_TSL(9);
+    else ATTN_TS(7);
 }
 
 }  // namespace fl

@@ -23,6 +23,7 @@ struct AttnArgs {
     const int *posp;     // attends slots 0..*posp
     int nkv, nsplit;     // grid = (nsplit, nkv)
     int chmin;           // minimum tokens per split (a multiple of attn_tpp(D))
+    int single;          // MFMA kernel: contexts up to this many tokens run as one split
     float *part;         // [nkv][nsplit][G][D+2] split partials
     int *counters;       // [nkv] arrival counters (zero between launches)
     float *out;          // [nh*D]

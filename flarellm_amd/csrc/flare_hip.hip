@@ -249,7 +249,7 @@ struct fl_ctx {
     float *kvstage = nullptr;                       // host rows staged for fl_kv_write(_batch): 2 x cap x nkv*D
     size_t kvstage_rows = 0;
     float *rope = nullptr;
-    int nsplit = 1, chmin = 1;
+    int nsplit = 1, chmin = 1, single = kAttmSingle;
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
     float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
@@ -851,6 +851,7 @@ int fl_op_attention(fl_ctx *ctx, const float *q, const void *k_cache, const void
     a.nkv = num_kv_heads;
     a.nsplit = ns;
     a.chmin = chmin;
+    a.single = kAttmSingle;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = out;
@@ -924,6 +925,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         // kernel runs one split
         ctx->chmin = 2 * kAttmBlock * (kAttmThreads / 64);
         if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(256, atoi(ev) / 256 * 256);
+        if (const char *ev = getenv("FLARE_ATTN_SINGLE")) ctx->single = std::max(0, atoi(ev));  // tuning override
         ctx->nsplit = std::max(1, std::min(kAttmMaxSplit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin));
     } else {
         choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
@@ -948,7 +950,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->hsum, F / 32 * 4);
     ALLOC(ctx, ctx->logits, (size_t)c.vocab_size * 4);
     ALLOC(ctx, ctx->bench_out, std::max({(size_t)c.vocab_size, H, qd + 2 * kvd, 2 * F}) * 4);
-    ALLOC(ctx, ctx->bench_trace, (64 + 2048) * 8);
+    ALLOC(ctx, ctx->bench_trace, (64 + 3072) * 8);
     ALLOC(ctx, ctx->st, sizeof(DevState));
     ALLOC(ctx, ctx->tokens, S * 4);
     HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
@@ -1160,6 +1162,7 @@ static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
     a.posp = &ctx->st->pos;
     a.nsplit = ctx->nsplit;
     a.chmin = ctx->chmin;
+    a.single = ctx->single;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = nullptr;  // the wo matvec reads the Q8_0 copy only
@@ -1402,6 +1405,7 @@ int fl_gqa_from_cache(fl_ctx *ctx, int layer, const float *q, int seq_len, float
     a.posp = ctx->d_pos;
     a.nsplit = ctx->nsplit;
     a.chmin = ctx->chmin;
+    a.single = ctx->single;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = ctx->attn;
@@ -1425,6 +1429,7 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
         a.posp = ctx->d_pos;
         a.nsplit = ctx->nsplit;
         a.chmin = ctx->chmin;
+        a.single = ctx->single;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = ctx->attn;
@@ -1593,6 +1598,7 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
         a.posp = ctx->vpos;
         a.nsplit = ctx->nsplit;
         a.chmin = ctx->chmin;
+        a.single = ctx->single;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = nullptr;
@@ -1703,7 +1709,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
     }
     if (which <= 4 && getenv("FLARE_MV_TRACE_PRINT")) {
         // workgroup 0 phases, then the spread of workgroup start / end times
-        std::vector<long long> tr(64 + 2048, 0);
+        std::vector<long long> tr(64 + 3072, 0);
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
         HIPCHK(ctx, hipMemcpy(tr.data(), ctx->bench_trace, tr.size() * 8, hipMemcpyDeviceToHost));
         fprintf(stderr, "mv trace which=%d (10ns ticks from wg0 start):", which);
@@ -1721,6 +1727,16 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         }
         if (n) fprintf(stderr, " | %d wgs: starts %lld..%lld ends %lld..%lld", n, s0 - tr[0], s1 - tr[0], e0 - tr[0], e1 - tr[0]);
         fprintf(stderr, "\n");
+        if (const char *dump = getenv("FLARE_MV_TRACE_DUMP")) {
+            // raw per-workgroup (start, end) ticks, one line per launch
+            if (FILE *f = fopen(dump, "a")) {
+                fprintf(f, "%d", which);
+                for (int b = 0; b < 1024; b++) fprintf(f, " %lld %lld %lld", tr[64 + 2 * b] ? tr[64 + 2 * b] - tr[0] : -1,
+                                                        tr[65 + 2 * b] ? tr[65 + 2 * b] - tr[0] : -1, tr[64 + 2048 + b]);
+                fprintf(f, "\n");
+                fclose(f);
+            }
+        }
         HIPCHK(ctx, hipMemset(ctx->bench_trace, 0, tr.size() * 8));
     }
     if (which == 5 && getenv("FLARE_ATTN_TRACE_PRINT")) {

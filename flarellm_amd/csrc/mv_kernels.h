@@ -38,6 +38,9 @@ struct QkvEpi {
     do {                                                                                  \
         if (a.trace && threadIdx.x == 0 && blockIdx.x < 1024)                            \
             a.trace[64 + 2 * blockIdx.x + (i)] = (long long)__builtin_amdgcn_s_memrealtime(); \
+        if (a.trace && threadIdx.x == 0 && blockIdx.x < 1024 && (i) == 0)                \
+            a.trace[64 + 2048 + blockIdx.x] = ((long long)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11)) << 32) | \
+                (long long)__builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11)); \
     } while (0)
 #else
 #define MV_TS(i) \
@@ -274,13 +277,32 @@ __device__ __forceinline__ void store_rows(const float *acc, int row0, int rows,
     }
 }
 
+// Lane r's row of a finished group (every lane holds all R sums): a chain of
+// selects rather than a dynamically indexed private array.
+template <int R>
+__device__ __forceinline__ float lane_row(const float *acc, int gl) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; r++)
+        if (gl == r) v = acc[r];
+    return v;
+}
+
+// RoPE (cos, sin) of the pair that lane p < R/2 stores for rows n = row0 + 2p
+// (q and k rows only).
+__device__ __forceinline__ void qkv_rope_cs(const QkvEpi &e, int n, int pos, float &c, float &sn) {
+    const int half = e.hd >> 1, i = (n % e.hd) >> 1;
+    c = e.rope[(size_t)pos * half + i];
+    sn = e.rope[e.sin_off + (size_t)pos * half + i];
+}
+
 // EPI_QKV store of one rotate-half pair (rows n, n+1 in the pair-interleaved
-// order of the fused QKV weight).
-__device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const QkvEpi &e, int pos, float *q) {
+// order of the fused QKV weight); (c, sn) = qkv_rope_cs of the pair.
+__device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const QkvEpi &e, int pos, float *q,
+                                               float c, float sn) {
     const int D = e.hd, half = D >> 1;
     const int j = n % D, i = j >> 1;  // pair index within the head
     if (n < e.nq + e.nk) {
-        const float c = e.rope[(size_t)pos * half + i], sn = e.rope[e.sin_off + (size_t)pos * half + i];
         const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
         if (n < e.nq) {
             const int h = n / D;
@@ -327,13 +349,19 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
 }
 
 // EPI_QKV store of a finished row group (R even); lane p < R/2 stores pair p.
+// pre: lane p's (cos, sin) already loaded (pre_ok), else loaded here
 template <int R>
 __device__ __forceinline__ void store_qkv(const float *acc, int row0, int rows, int gl, const QkvEpi &e, int pos,
-                                          float *q) {
+                                          float *q, bool pre_ok, float pc, float ps) {
     static_assert(R % 2 == 0, "EPI_QKV needs row pairs");
 #pragma unroll
     for (int p = 0; p < R / 2; p++)
-        if (gl == p && row0 + 2 * p < rows) store_qkv_pair(acc[2 * p], acc[2 * p + 1], row0 + 2 * p, e, pos, q);
+        if (gl == p && row0 + 2 * p < rows) {
+            const int n = row0 + 2 * p;
+            float c = pc, sn = ps;
+            if (!pre_ok && n < e.nq + e.nk) qkv_rope_cs(e, n, pos, c, sn);
+            store_qkv_pair(acc[2 * p], acc[2 * p + 1], n, e, pos, q, c, sn);
+        }
 }
 
 }  // namespace fl

@@ -315,8 +315,32 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     Stage<F32IN, kMvsThreads> stg;
     stg.issue(a);                  // 1. activation loads
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
-    if (nunits > 0) load(ta, 0);   // 2. first weight pieces
+    load(ta, 0);                   // 2. first weight pieces (unconditional: clamped rows are valid, and
+                                   // the prologue below then waits for the activation loads only)
     const int qpos = a.epi == EPI_QKV ? *a.qkv.posp : 0;
+    // epilogue operands of the wave's first row group, in flight with the
+    // first tile: the residual rows (EPI_ADD, lane r = row r) or lane p's
+    // RoPE (cos, sin) (EPI_QKV)
+    // Both loads are issued on every path (valid addresses, clamped or a
+    // stand-in), so the compiler's wait counts stay static and the prologue
+    // waits for the activation loads only.
+    float pre0, pre1;
+    {
+        const int row0f = min(gw * R, W.rows - 1);
+        const float *p0 = (const float *)W.q, *p1 = (const float *)W.q;
+        if (a.epi == EPI_ADD) {
+            p0 = a.out + min(row0f + min(lane, R - 1), W.rows - 1);
+            p1 = p0;
+        }
+        if (a.epi == EPI_QKV) {
+            const int half = a.qkv.hd >> 1;
+            const int n = min(row0f + 2 * min(lane, R / 2 - 1), W.rows - 1);
+            p0 = a.qkv.rope + (size_t)qpos * half + ((n % a.qkv.hd) >> 1);
+            p1 = p0 + a.qkv.sin_off;
+        }
+        pre0 = *p0;
+        pre1 = *p1;
+    }
     MV_TS(1);
     stg.finish(a, smem);           // 3. prologue arithmetic (ends with a barrier)
     MV_TS(2);
@@ -343,8 +367,12 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
             const int row0 = rg * R;
             if (a.epi == EPI_ARGMAX) {
                 best = umax64(best, rows_best<R>(acc, row0, W.rows));
+            } else if (a.epi == EPI_ADD) {
+                // residual add (model.rs:2305-2311, 2537-2543): lane r adds row r
+                const float v = lane_row<R>(acc, lane);
+                if (lane < R && row0 + lane < W.rows) a.out[row0 + lane] = (k == 0 ? pre0 : a.out[row0 + lane]) + v;
             } else if constexpr (R % 2 == 0) {
-                if (a.epi == EPI_QKV) store_qkv<R>(acc, row0, W.rows, lane, a.qkv, qpos, a.out);
+                if (a.epi == EPI_QKV) store_qkv<R>(acc, row0, W.rows, lane, a.qkv, qpos, a.out, k == 0, pre0, pre1);
                 else store_rows<R>(acc, row0, W.rows, lane, a.epi, a.out);
             } else {
                 store_rows<R>(acc, row0, W.rows, lane, a.epi, a.out);
@@ -415,7 +443,7 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     Stage<false, NT> stg;
     stg.issue(a);
     FLARE_STAGE_BARRIER();
-    if (nunits > 0) load(ta, 0);
+    load(ta, 0);  // unconditional, so the prologue waits for the activation loads only
     MV_TS(1);
     stg.finish(a, smem);
     MV_TS(2);

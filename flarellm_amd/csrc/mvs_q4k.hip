@@ -12,7 +12,7 @@ namespace fl {
     }
 
 hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
-    C(F_Q4K, false, 4, 1) C(F_Q4K, false, 2, 1) C(F_Q4K, false, 2, 2)
+    C(F_Q4K, false, 4, 1) C(F_Q4K, false, 2, 1) C(F_Q4K, false, 2, 2) C(F_Q4K, false, 1, 2) C(F_Q4K, false, 1, 4)
     return hipErrorNotSupported;
 }
 #undef C
