@@ -194,10 +194,10 @@ __device__ __forceinline__ v8h_t c2x8_to_h8(uint32_t w) {
 
 // One workgroup = (split s, kv head kvh, query z); waves take 32-token
 // blocks of the split's chunk round-robin.
-template <typename KT, int D, int G>
-__global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
-    constexpr int DT = D / 32, NT = D / 16, NW = kAttmThreads / 64;
-    constexpr int OPT = (G * D + kAttmThreads - 1) / kAttmThreads;
+template <typename KT, int D, int G, int NTH = kAttmThreads>
+__global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
+    constexpr int DT = D / 32, NT = D / 16, NW = NTH / 64;
+    constexpr int OPT = (G * D + NTH - 1) / NTH;
     static_assert(2 * G <= 16, "query heads (hi/lo rows) exceed the MFMA tile");
     __shared__ float sp[NW][G][kAttmBlock];  // p of the current block (per wave)
     __shared__ float vsc[NW][kAttmBlock][DT];  // Q8: V scales of the block's slots
@@ -650,7 +650,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     float res[OPT];
 #pragma unroll
     for (int k = 0; k < OPT; k++) {
-        const int i = tid + k * kAttmThreads;
+        const int i = tid + k * NTH;
         float O = 0.0f;
         if (i < G * D) {
             const int g = i / D;
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         __syncthreads();  // red is overwritten below
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
-            const int i = tid + k * kAttmThreads;
+            const int i = tid + k * NTH;
             if (i < G * D) {
                 const float v = res[k] * (1.0f / Lx[i / D]);
                 mo[i] = v;
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         float *mypart = a.part + ((size_t)kvh * a.nsplit + s) * P;
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
-            const int i = tid + k * kAttmThreads;
+            const int i = tid + k * NTH;
             if (i < G * D) st_agent(mypart + i, res[k]);
         }
         if (tid < G) {
@@ -713,7 +713,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         for (int j0 = 0; j0 < nact; j0 += MB) {
 #pragma unroll
             for (int k = 0; k < OPT; k++) {
-                const int i = min(tid + k * kAttmThreads, G * D - 1), g = i / D;
+                const int i = min(tid + k * NTH, G * D - 1), g = i / D;
                 float mv[MB], lv[MB], ov[MB];
 #pragma unroll
                 for (int k2 = 0; k2 < MB; k2++) {
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
         __syncthreads();  // red (mo) is rewritten below
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
-            const int i = tid + k * kAttmThreads;
+            const int i = tid + k * NTH;
             if (i < G * D) {
                 const float v = O[k];
                 mo[i] = v;
@@ -761,7 +761,7 @@ __global__ __launch_bounds__(kAttmThreads) void k_attm(AttnArgs a0) {
     if (a.oq) {
         // Q8_0 copy of this kv head's G*D outputs (quantize_input_q8_0_into), 32 lanes per block
         const int nb = G * D / 32;
-        for (int b = tid >> 5; b < nb; b += kAttmThreads / 32) {
+        for (int b = tid >> 5; b < nb; b += NTH / 32) {
             const int gb = kvh * nb + b;
             quant_block32_lanes(mo[b * 32 + (tid & 31)], a.oq + gb * 32, a.os + gb, a.osum + gb);
         }

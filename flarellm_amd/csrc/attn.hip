@@ -21,7 +21,10 @@ template <typename KT>
 static hipError_t launch_attm_t(int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
 #define C(DD, GG)                                                                                  \
     if (D == DD && G == GG) {                                                                      \
-        hipLaunchKernelGGL((k_attm<KT, DD, GG>), dim3(a.nsplit, a.nkv, nq), dim3(kAttmThreads), 0, st, a); \
+        if (a.waves == 4)                                                                          \
+            hipLaunchKernelGGL((k_attm<KT, DD, GG, 256>), dim3(a.nsplit, a.nkv, nq), dim3(256), 0, st, a); \
+        else                                                                                       \
+            hipLaunchKernelGGL((k_attm<KT, DD, GG>), dim3(a.nsplit, a.nkv, nq), dim3(kAttmThreads), 0, st, a); \
         return hipSuccess;                                                                         \
     }
     C(64, 1) C(64, 2) C(64, 3) C(64, 4) C(64, 8)

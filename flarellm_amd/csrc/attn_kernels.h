@@ -24,6 +24,7 @@ struct AttnArgs {
     int nkv, nsplit;     // grid = (nsplit, nkv)
     int chmin;           // minimum tokens per split (a multiple of attn_tpp(D))
     int single;          // MFMA kernel: contexts up to this many tokens run as one split
+    int waves;           // MFMA kernel: waves per workgroup (4 or 8; other values mean 8)
     float *part;         // [nkv][nsplit][G][D+2] split partials
     int *counters;       // [nkv] arrival counters (zero between launches)
     float *out;          // [nh*D]

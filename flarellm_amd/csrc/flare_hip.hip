@@ -249,7 +249,7 @@ struct fl_ctx {
     float *kvstage = nullptr;                       // host rows staged for fl_kv_write(_batch): 2 x cap x nkv*D
     size_t kvstage_rows = 0;
     float *rope = nullptr;
-    int nsplit = 1, chmin = 1, single = kAttmSingle;
+    int nsplit = 1, chmin = 1, single = kAttmSingle, attn_waves = 8;
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
     float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
@@ -919,12 +919,18 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->rope, tab.size() * 4);
     HIPCHK(ctx, hipMemcpy(ctx->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
     if (kv_format == FL_KV_F16 || kv_format == FL_KV_Q8 || kv_format == FL_KV_KIVI2) {
-        // MFMA kernel: chunks of at least 512 slots (two 32-slot blocks per
-        // wave, the second in flight while the first computes), at most
-        // kAttmMaxSplit splits per kv head; up to kAttmSingle tokens the
-        // kernel runs one split
-        ctx->chmin = 2 * kAttmBlock * (kAttmThreads / 64);
-        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(256, atoi(ev) / 256 * 256);
+        // MFMA kernel: at most kAttmMaxSplit splits per kv head, chunks of at
+        // least chmin slots.  Measured on MI355X (Llama-3.2-1B D=64 at ~800 tokens, Llama-3-8B
+        // D=128 at ~4k): split every context longer than one block per wave,
+        // 4-wave workgroups for D=64 and 8-wave ones for D=128.  More,
+        // smaller splits spread the K/V stream over more CUs; the split merge
+        // (publish, count, one round trip of partial loads) costs ~3-4 us.
+        ctx->attn_waves = c.head_dim <= 64 ? 4 : 8;
+        ctx->single = 0;
+        if (const char *ev = getenv("FLARE_ATTN_WAVES")) ctx->attn_waves = atoi(ev) == 4 ? 4 : 8;  // tuning override
+        const int pass = kAttmBlock * ctx->attn_waves;  // tokens of one block per wave
+        ctx->chmin = pass;
+        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(pass, atoi(ev) / pass * pass);
         if (const char *ev = getenv("FLARE_ATTN_SINGLE")) ctx->single = std::max(0, atoi(ev));  // tuning override
         ctx->nsplit = std::max(1, std::min(kAttmMaxSplit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin));
     } else {
@@ -1163,6 +1169,7 @@ static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
     a.nsplit = ctx->nsplit;
     a.chmin = ctx->chmin;
     a.single = ctx->single;
+    a.waves = ctx->attn_waves;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = nullptr;  // the wo matvec reads the Q8_0 copy only
@@ -1406,6 +1413,7 @@ int fl_gqa_from_cache(fl_ctx *ctx, int layer, const float *q, int seq_len, float
     a.nsplit = ctx->nsplit;
     a.chmin = ctx->chmin;
     a.single = ctx->single;
+    a.waves = ctx->attn_waves;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = ctx->attn;
@@ -1430,6 +1438,7 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
         a.nsplit = ctx->nsplit;
         a.chmin = ctx->chmin;
         a.single = ctx->single;
+        a.waves = ctx->attn_waves;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = ctx->attn;
@@ -1599,6 +1608,7 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
         a.nsplit = ctx->nsplit;
         a.chmin = ctx->chmin;
         a.single = ctx->single;
+        a.waves = ctx->attn_waves;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = nullptr;
