@@ -1723,7 +1723,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
         HIPCHK(ctx, hipMemcpy(tr.data(), ctx->bench_trace, tr.size() * 8, hipMemcpyDeviceToHost));
         fprintf(stderr, "mv trace which=%d (10ns ticks from wg0 start):", which);
-        for (int i = 1; i < 6; i++) fprintf(stderr, " %lld", tr[i] - tr[0]);
+        for (int i = 1; i < 11; i++) fprintf(stderr, " %lld", tr[i] ? tr[i] - tr[0] : -1);
         long long s0 = 0, s1 = 0, e0 = 0, e1 = 0;
         int n = 0;
         for (int b = 0; b < 1024; b++) {

@@ -52,7 +52,9 @@ struct MvsPlan {
 // (R, SU) per format and step count: tiles of 2-8 pieces, chosen so the
 // kernel stays within ~160 VGPRs (>= 3 waves per SIMD)
 inline void mvs_shape(int fmt, bool f32in, int S, int &r, int &su) {
-    if (fmt == F_Q8_0 && f32in) { r = 2; su = 1; return; }
+    // f32 input (logits), measured on MI355X: Q8_0 2 rows x 2 KiB, Q6_K 2 rows x 1 KiB
+    if (fmt == F_Q8_0 && f32in) { r = 2; su = S >= 2 ? 2 : 1; return; }
+    if (fmt == F_Q6K && f32in) { r = 2; su = 1; return; }
     if (S <= 1) { r = 4; su = 1; return; }
     if (fmt == F_Q4K || fmt == F_Q6K) { r = 2; su = 2; return; }
     if (S == 2 || S == 3) { r = 4; su = 2; return; }
@@ -64,9 +66,10 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in) {
     mvs_shape(fmt, f32in, mvs_steps(fmt, cols), p.r, p.su);
     // tuning overrides for the Q8-input kernels (experiments): FLARE_MVS_R /
     // FLARE_MVS_SU / FLARE_MVS_GRID
-    const char *er = f32in ? nullptr : getenv("FLARE_MVS_R");
+    // (FLARE_MVF_R / FLARE_MVF_SU for the f32-input kernels)
+    const char *er = getenv(f32in ? "FLARE_MVF_R" : "FLARE_MVS_R");
     if (er) p.r = atoi(er);
-    if (const char *e = f32in ? nullptr : getenv("FLARE_MVS_SU")) p.su = atoi(e);
+    if (const char *e = getenv(f32in ? "FLARE_MVF_SU" : "FLARE_MVS_SU")) p.su = atoi(e);
     // fill the chip: halve the rows per group while fewer than 256
     // workgroups (4 waves, one group each) would run
     while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !er) p.r /= 2;

@@ -42,7 +42,15 @@ struct QkvEpi {
             a.trace[64 + 2048 + blockIdx.x] = ((long long)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11)) << 32) | \
                 (long long)__builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11)); \
     } while (0)
+#define ST_TS(i)                                                                          \
+    do {                                                                                  \
+        if (tr && blockIdx.x == 0 && threadIdx.x == 0)                                    \
+            tr[i] = (long long)__builtin_amdgcn_s_memrealtime();                          \
+    } while (0)
 #else
+#define ST_TS(i) \
+    do {         \
+    } while (0)
 #define MV_TS(i) \
     do {         \
     } while (0)
@@ -93,8 +101,9 @@ struct StageQ8 {
     }
 
     __device__ __forceinline__ void finish(int pro, int n, float eps, const float *x, const float *w,
-                                           int8_t *lq, float *ls, int *lsum, float *red) {
+                                           int8_t *lq, float *ls, int *lsum, float *red, long long *tr = nullptr) {
         const int t = threadIdx.x;
+        ST_TS(7);
         if (pro == PRO_LOADQ) {
             const int n16 = n >> 4, nb = n >> 5;
 #pragma unroll
@@ -130,7 +139,9 @@ struct StageQ8 {
 #pragma unroll
         for (int j = 0; j < 16; j++)
             if (j < E) ss += xs[j] * xs[j];
+        ST_TS(8);
         ss = wg_sum(ss, red);
+        ST_TS(9);
         const float rms = sqrtf(ss / (float)n + eps);
         const float inv = 1.0f / rms;
         float v[16];
@@ -176,6 +187,7 @@ struct StageQ8 {
                 lsum[t >> 1] = qsum;
             }
         }
+        ST_TS(10);
         __syncthreads();
     }
 };

@@ -158,63 +158,105 @@ __device__ __forceinline__ float pc_dot_q8(const Pc<F_Q4K> &P, const WDesc &W, c
 }
 
 // ---- f32 input (activations in LDS as floats) ------------------------------
-// dequant (quantize.rs) then matvec_argmax_f32's f32 dot (model.rs:8668-8689)
-__device__ __forceinline__ float pc_dot_f32(const Pc<F_Q8_0> &P, const WDesc &W, const float *lx, int step,
-                                            int lane) {
-    const int K = W.cols, off0 = step * 1024 + 16 * lane;
-    const int off = min(off0, K - 16);
-    const float scale = h2f((uint16_t)P.sc);
+// dequant (quantize.rs) then matvec_argmax_f32's f32 dot (model.rs:8668-8689).
+// LDS holds x[K] and gx[K/16] = the sum of each 16-element group of x.  A
+// lane's 16 consecutive weights share one scale, so their dot is formed as
+// scale * (sum c_j x_j - bias * gx) with c_j the unsigned code (converted to
+// float by one instruction) and bias the code offset (Q8_0: 128 after the
+// sign bias, Q6_K: 32): the same value as sum (scale * q_j) * x_j up to fp32
+// rounding (the accumulation order differs from the reference's sequential
+// sum in any case; parity is 1e-3 relative).  The lane's x values are loaded
+// once per step and shared by the R rows of the tile.
+template <int FMT>
+struct XIn;
+
+template <>
+struct XIn<F_Q8_0> {
+    v4f_t x[4];
+    float g;
+    bool ok;
+    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+        const int K = W.cols, off0 = step * 1024 + 16 * lane;
+        const int off = min(off0, K - 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = *(const v4f_t *)(lx + off + 4 * j);
+        g = lx[K + (off >> 4)];
+        ok = off0 < K;
+    }
+};
+
+__device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q8_0> &P, const XIn<F_Q8_0> &X) {
     float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const v4f_t x = *(const v4f_t *)(lx + off + 4 * j);
-        float q[4];
-        i8x4_to_f32(P.q[j], q);
+        const uint32_t u = (uint32_t)P.q[j] ^ 0x80808080u;  // int8 + 128, per byte
 #pragma unroll
-        for (int k = 0; k < 4; k++) a += (q[k] * scale) * x[k];
+        for (int k = 0; k < 4; k++) a = __builtin_fmaf((float)((u >> (8 * k)) & 0xFFu), X.x[j][k], a);
     }
-    return off0 < K ? a : 0.0f;
+    const float scale = h2f((uint16_t)P.sc);
+    return X.ok ? scale * (a - 128.0f * X.g) : 0.0f;
 }
 
 // dequant_q6k_block (quantize.rs:343-384, llama.cpp layout): w = d*sc*q.
 // Lane bytes: ql[hf*64 + qq*16 + i]; qq<2 -> q1 (low) / q3 (high), qq>=2 ->
 // q2 / q4; the 2 qh bits sit at shift 2*(qq>>1) and +4.
-__device__ __forceinline__ float pc_dot_f32(const Pc<F_Q6K> &P, const WDesc &W, const float *lx, int step,
-                                            int lane) {
-    const int span = (W.cols >> 8) * 128, off0 = step * 1024 + 16 * lane;
-    const int off = min(off0, span - 16);
-    const int sb = off >> 7, o = off & 127, hf = o >> 6, qq = (o >> 4) & 3;
-    const int e_lo = sb * 256 + hf * 128 + (qq >> 1) * 32 + (qq & 1) * 16;
-    const int sh = 2 * (qq >> 1);
-    const float d = h2f((uint16_t)P.d);
-    const float ds_lo = d * (float)(int8_t)(P.sc & 0xFF), ds_hi = d * (float)(int8_t)(P.sc >> 8);
-    float a = 0.0f;
+template <>
+struct XIn<F_Q6K> {
+    v4f_t xl[4], xh[4];
+    float glo, ghi;
+    int sh;
+    bool ok;
+    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+        const int K = W.cols, span = (K >> 8) * 128, off0 = step * 1024 + 16 * lane;
+        const int off = min(off0, span - 16);
+        const int sb = off >> 7, o = off & 127, hf = o >> 6, qq = (o >> 4) & 3;
+        const int e_lo = sb * 256 + hf * 128 + (qq >> 1) * 32 + (qq & 1) * 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            xl[j] = *(const v4f_t *)(lx + e_lo + 4 * j);
+            xh[j] = *(const v4f_t *)(lx + e_lo + 64 + 4 * j);
+        }
+        glo = lx[K + (e_lo >> 4)];
+        ghi = lx[K + (e_lo >> 4) + 4];
+        sh = 2 * (qq >> 1);
+        ok = off0 < span;
+    }
+};
+
+__device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q6K> &P, const XIn<F_Q6K> &X) {
+    float slo = 0.0f, shi = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const v4f_t xl = *(const v4f_t *)(lx + e_lo + 4 * j);
-        const v4f_t xh = *(const v4f_t *)(lx + e_lo + 64 + 4 * j);
         // four 6-bit codes per word, assembled byte-wise: nibble | 2 qh bits << 4
         const uint32_t lw = (uint32_t)P.ql[j], hw = (uint32_t)P.qh[j];
-        const uint32_t clo = (lw & 0x0F0F0F0Fu) | (((hw >> sh) & 0x03030303u) << 4);
-        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (sh + 4)) & 0x03030303u) << 4);
+        const uint32_t clo = (lw & 0x0F0F0F0Fu) | (((hw >> X.sh) & 0x03030303u) << 4);
+        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (X.sh + 4)) & 0x03030303u) << 4);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float q_lo = (float)((clo >> (8 * k)) & 0xFFu) - 32.0f;
-            const float q_hi = (float)((chi >> (8 * k)) & 0xFFu) - 32.0f;
-            a += (ds_lo * q_lo) * xl[k];
-            a += (ds_hi * q_hi) * xh[k];
+            slo = __builtin_fmaf((float)((clo >> (8 * k)) & 0xFFu), X.xl[j][k], slo);
+            shi = __builtin_fmaf((float)((chi >> (8 * k)) & 0xFFu), X.xh[j][k], shi);
         }
     }
-    return off0 < span ? a : 0.0f;
+    const float d = h2f((uint16_t)P.d);
+    const float ds_lo = d * (float)(int8_t)(P.sc & 0xFF), ds_hi = d * (float)(int8_t)(P.sc >> 8);
+    return X.ok ? ds_lo * (slo - 32.0f * X.glo) + ds_hi * (shi - 32.0f * X.ghi) : 0.0f;
 }
 
-__device__ __forceinline__ float pc_dot_f32(const Pc<F_F32> &P, const WDesc &W, const float *lx, int step,
-                                            int lane) {
-    const int K = W.cols, off0 = step * 1024 + 16 * lane;
-    const int off = min(off0, 4 * K - 16);
-    const v4f_t x = *(const v4f_t *)(lx + (off >> 2));
-    const float a = P.w.x * x.x + P.w.y * x.y + P.w.z * x.z + P.w.w * x.w;
-    return off0 < 4 * K ? a : 0.0f;
+template <>
+struct XIn<F_F32> {
+    v4f_t x;
+    bool ok;
+    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+        const int K = W.cols, off0 = step * 1024 + 16 * lane;
+        const int off = min(off0, 4 * K - 16);
+        x = *(const v4f_t *)(lx + (off >> 2));
+        ok = off0 < 4 * K;
+    }
+};
+
+__device__ __forceinline__ float pc_dot_f32x(const Pc<F_F32> &P, const XIn<F_F32> &X) {
+    const float a = P.w.x * X.x.x + P.w.y * X.x.y + P.w.z * X.x.z + P.w.w * X.x.w;
+    return X.ok ? a : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -240,8 +282,9 @@ struct MvsArgs {
     long long *trace;
 };
 
+// f32 input: x[K] | gx[K/16] | red[64]; Q8 input: q[K] | scales, sums [K/32] | red
 __host__ __device__ inline size_t mvs_lds_bytes(bool f32in, int K) {
-    return f32in ? (size_t)K * 4 + 64 * 4 : (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64;
+    return f32in ? (size_t)K * 4 + (size_t)(K / 16) * 4 + 64 * 4 : (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64;
 }
 
 // prologue staging shared by both kernels: x (Q8 or f32) into LDS
@@ -257,7 +300,7 @@ struct Stage<false, NT> {
         float *ls = (float *)(smem + K);
         int *lsum = (int *)(ls + (K >> 5));
         float *red = (float *)(lsum + (K >> 5));
-        s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red);
+        s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red, a.trace);
     }
 };
 template <int NT>
@@ -267,14 +310,24 @@ struct Stage<true, NT> {
     __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
         const int K = a.W.cols;
         float *lx = (float *)smem;
-        s.finish(a.pro, K, a.eps, a.x, a.nw, lx, lx + K);
+        s.finish(a.pro, K, a.eps, a.x, a.nw, lx, lx + K + K / 16);
+        // gx: sums of the 16-element groups of x (sequential fp32 per group)
+        for (int gi = threadIdx.x; gi < K / 16; gi += NT) {
+            float g = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) g += lx[16 * gi + i];
+            lx[K + gi] = g;
+        }
+        __syncthreads();
     }
 };
 
 template <int FMT, bool F32IN>
 __device__ __forceinline__ float pc_dot(const Pc<FMT> &P, const WDesc &W, const char *smem, int step, int lane) {
     if constexpr (F32IN) {
-        return pc_dot_f32(P, W, (const float *)smem, step, lane);
+        XIn<FMT> X;
+        X.load(W, (const float *)smem, step, lane);
+        return pc_dot_f32x(P, X);
     } else {
         const int K = W.cols;
         const int8_t *lq = (const int8_t *)smem;
@@ -351,15 +404,23 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     unsigned long long best = 0;
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
         const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
-#pragma unroll
-        for (int r = 0; r < R; r++)
+        if constexpr (F32IN) {
+            // one step at a time: the lane's activation floats are loaded
+            // once and shared by the R rows (not hoisted for the whole tile)
 #pragma unroll
             for (int s = 0; s < SU; s++) {
-                acc[r] += pc_dot<FMT, F32IN>(T[r][s], W, smem, rr * SU + s, lane);
-                // one piece at a time: keeps the 16 activation floats of an
-                // f32 piece from being hoisted for the whole tile
-                if constexpr (F32IN) __builtin_amdgcn_sched_barrier(0);
+                XIn<FMT> X;
+                X.load(W, (const float *)smem, rr * SU + s, lane);
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[r] += pc_dot_f32x(T[r][s], X);
+                __builtin_amdgcn_sched_barrier(0);
             }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int s = 0; s < SU; s++) acc[r] += pc_dot<FMT, F32IN>(T[r][s], W, smem, rr * SU + s, lane);
+        }
         if (u == 0) MV_TS(3);
         if (rr == NR - 1) {
 #pragma unroll

@@ -13,7 +13,7 @@ namespace fl {
 
 hipError_t launch_mvs_q8_0(bool f32in, const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
     if (f32in) {
-        C(F_Q8_0, true, 2, 1)
+        C(F_Q8_0, true, 2, 1) C(F_Q8_0, true, 4, 1) C(F_Q8_0, true, 2, 2) C(F_Q8_0, true, 4, 2)
     } else {
         C(F_Q8_0, false, 4, 1) C(F_Q8_0, false, 4, 2) C(F_Q8_0, false, 2, 1) C(F_Q8_0, false, 2, 2) C(F_Q8_0, false, 2, 4) C(F_Q8_0, false, 1, 4) C(F_Q8_0, false, 1, 8)
     }
