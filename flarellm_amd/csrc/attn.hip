@@ -59,9 +59,10 @@ hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &
 
 // Q8: one thread per (token, kv head, 32-block); quantize_input_q8_0_into
 // arithmetic with the scale stored as binary16.
-__global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *krows, const float *vrows, int p0,
-                                                     int n, int D) {
-    const int nb = D / 32;
+// p0p (optional): the first position read from the device (captured verify).
+__global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *krows, const float *vrows, int p0h,
+                                                     const int *p0p, int n, int D) {
+    const int nb = D / 32, p0 = p0p ? *p0p : p0h;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long total = (long long)n * a.nkv * nb * 2;
     if (i >= total) return;
@@ -118,8 +119,9 @@ __global__ __launch_bounds__(256) void k_kv_kivi_ring(AttnArgs a, const float *k
 }
 
 // F32 / F16: plain copy (binary16 RNE for F16, as half::f16::from_f32).
-__global__ __launch_bounds__(256) void k_kv_plain_write(AttnArgs a, const float *krows, const float *vrows, int p0,
-                                                        int n, int D, int f16) {
+__global__ __launch_bounds__(256) void k_kv_plain_write(AttnArgs a, const float *krows, const float *vrows, int p0h,
+                                                        const int *p0p, int n, int D, int f16) {
+    const int p0 = p0p ? *p0p : p0h;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long per = (long long)a.nkv * D;
     if (i >= (long long)n * per * 2) return;
@@ -135,21 +137,22 @@ __global__ __launch_bounds__(256) void k_kv_plain_write(AttnArgs a, const float 
 }
 
 hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
-                           int p0, int n, int D) {
+                           int p0, int n, int D, const int *p0p) {
     if (n <= 0) return hipSuccess;
     if (kvfmt == KV_F32 || kvfmt == KV_F16) {
         const long long total = (long long)n * a.nkv * D * 2;
         hipLaunchKernelGGL(k_kv_plain_write, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, krows,
-                           vrows, p0, n, D, kvfmt == KV_F16 ? 1 : 0);
+                           vrows, p0, p0p, n, D, kvfmt == KV_F16 ? 1 : 0);
         return hipGetLastError();
     }
     if (kvfmt == KV_Q8) {
         const long long total = (long long)n * a.nkv * (D / 32) * 2;
         hipLaunchKernelGGL(k_kv_q8_write, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, krows, vrows,
-                           p0, n, D);
+                           p0, p0p, n, D);
         return hipGetLastError();
     }
     if (kvfmt != KV_KIVI) return hipErrorNotSupported;
+    if (p0p) return hipErrorInvalidValue;  // KIVI group work is planned from the host position
     // groups [0, kivi_qlen(T + 1)) are quantized once T tokens are written
     const int g0 = kivi_qlen(p0 + 1) / kKiviGroup, g1 = kivi_qlen(p0 + n + 1) / kKiviGroup;
     if (g1 > g0) {

@@ -260,6 +260,7 @@ struct fl_ctx {
     DevState *st = nullptr;
     int *tokens = nullptr;
     hipGraph_t graph = nullptr;
+    std::map<int, hipGraphExec_t> vgraphs;  // captured verify passes, by batch size
     hipGraphExec_t gexec = nullptr;
     bool graph_ready = false;
     // speculative verify buffers (allocated on first fl_verify)
@@ -556,8 +557,21 @@ static double attn_bytes(const fl_ctx *ctx, int T) {
     }
 }
 
+// Captured graphs hold device pointers: drop them whenever a buffer they use
+// is reallocated or the model changes (they are captured again on next use).
+static void drop_graphs(fl_ctx *c) {
+    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->gexec = nullptr;
+    c->graph = nullptr;
+    c->graph_ready = false;
+    for (auto &kv : c->vgraphs) (void)hipGraphExecDestroy(kv.second);
+    c->vgraphs.clear();
+}
+
 static int ensure_part(fl_ctx *ctx, size_t floats) {
     if (ctx->part_cap >= floats) return 0;
+    drop_graphs(ctx);
     if (ctx->d_part) (void)hipFree(ctx->d_part);
     ctx->d_part = nullptr;
     ctx->part_cap = 0;
@@ -605,11 +619,7 @@ int fl_ctx_create(int device, fl_ctx **out) {
 }
 
 static void model_release(fl_ctx *c) {
-    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
-    if (c->graph) (void)hipGraphDestroy(c->graph);
-    c->gexec = nullptr;
-    c->graph = nullptr;
-    c->graph_ready = false;
+    drop_graphs(c);
     for (auto &l : c->layers) {
         weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
         if (l.attn_norm) (void)hipFree(l.attn_norm);
@@ -943,7 +953,9 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
             ctx->nsplit = ns;
     }
     const int G = c.num_heads / c.num_kv_heads;
-    int rc = ensure_part(ctx, (size_t)c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    // split partials for up to kVerifyMaxTokens queries (decode uses 1), so
+    // a verify batch never reallocates them
+    int rc = ensure_part(ctx, (size_t)kVerifyMaxTokens * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
     if (rc) return rc;
     ALLOC(ctx, ctx->x, H * 4);
     ALLOC(ctx, ctx->qkv, (qd + 2 * kvd) * 4);
@@ -997,9 +1009,7 @@ int fl_upload_weights(fl_ctx *ctx, const fl_raw_weight *layers, const float *con
     if (output && (weight_cols(output) != H || output->num_rows != c.vocab_size))
         return fail(ctx, FL_E_INVALID, "output shape");
     ctx->have_weights = false;
-    if (ctx->gexec) { (void)hipGraphExecDestroy(ctx->gexec); ctx->gexec = nullptr; }
-    if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
-    ctx->graph_ready = false;
+    drop_graphs(ctx);
     for (auto &l : ctx->layers) {
         weight_release(l.qkv); weight_release(l.wo); weight_release(l.gu); weight_release(l.down);
         if (l.attn_norm) (void)hipFree(l.attn_norm);
@@ -1553,31 +1563,17 @@ int fl_op_batched_matvec_f32in(fl_ctx *ctx, const fl_weight *w, int n_tokens, co
     return 0;
 }
 
-int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
-    if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
-    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+// The verify pass for M tokens at the device positions vpos.. (tokens in
+// vtok, vslots cleared); dev_pos: the cache writers read the position from the
+// device too (graph capture), pos0 is then only used for planning checks.
+static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
     const fl_model_config &c = ctx->cfg;
-    const int M = n_tokens;
-    if (M < 1 || M > kVerifyMaxTokens) return fail(ctx, FL_E_INVALID, "verify batch of %d tokens (1..%d)", M, kVerifyMaxTokens);
-    if (pos0 < 0 || pos0 + M > c.max_seq_len)
-        return fail(ctx, FL_E_INVALID, "positions [%d, %d) outside the KV cache (max_seq_len %d)", pos0, pos0 + M,
-                    c.max_seq_len);
-    if (M * c.num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
-    for (int i = 0; i < M; i++)
-        if ((int)tokens[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", tokens[i]);
-    int rc = verify_alloc(ctx);
-    if (rc) return rc;
+    int rc;
     const int H = c.hidden_dim, D = c.head_dim, G = c.num_heads / c.num_kv_heads;
     const int qd = c.num_heads * D, kvd = c.num_kv_heads * D, F = c.intermediate_dim;
     const float eps = c.rms_norm_eps;
     const int pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
     hipStream_t st = ctx->stream;
-    std::vector<int> tk(tokens, tokens + M);
-    HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data(), (size_t)M * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, &pos0, 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
-    rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (D + 2));
-    if (rc) return rc;
     float *xa = ctx->vx;
     HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, xa));
     int ks_down = 0;
@@ -1602,7 +1598,8 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
                                       (long long)c.max_seq_len * (D / 2), ctx->vpos, ctx->vq, ctx->vk, ctx->vv));
         AttnArgs a{};
         kv_layer_args(ctx, l, a);
-        HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D));
+        HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D,
+                                    dev_pos ? ctx->vpos : nullptr));
         a.q = ctx->vq;
         a.posp = ctx->vpos;
         a.nsplit = ctx->nsplit;
@@ -1657,6 +1654,58 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
                 rc = launch_f32in(ctx, O, 1, EPI_ARGMAX, xt, ctx->out_norm, eps, nullptr, ctx->vslots + t);
             if (rc) return rc;
         }
+    }
+    return 0;
+}
+
+int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
+    if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    const int M = n_tokens;
+    if (M < 1 || M > kVerifyMaxTokens) return fail(ctx, FL_E_INVALID, "verify batch of %d tokens (1..%d)", M, kVerifyMaxTokens);
+    if (pos0 < 0 || pos0 + M > c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "positions [%d, %d) outside the KV cache (max_seq_len %d)", pos0, pos0 + M,
+                    c.max_seq_len);
+    if (M * c.num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
+    for (int i = 0; i < M; i++)
+        if ((int)tokens[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", tokens[i]);
+    int rc = verify_alloc(ctx);
+    if (rc) return rc;
+    hipStream_t st = ctx->stream;
+    const int G = c.num_heads / c.num_kv_heads;
+    std::vector<int> tk(tokens, tokens + M);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data(), (size_t)M * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, &pos0, 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
+    rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    if (rc) return rc;
+    // F32 / F16 / Q8 caches: one captured graph per batch size (the positions
+    // are read from the device); KIVI plans its group work from the host.
+    // FLARE_NO_VERIFY_GRAPH (read per call): enqueue the kernels directly
+    const bool graph = use_graph() && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr;
+    if (graph && ctx->kv_format != FL_KV_KIVI2) {
+        auto it = ctx->vgraphs.find(M);
+        if (it == ctx->vgraphs.end()) {
+            HIPCHK(ctx, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            rc = enqueue_verify(ctx, M, pos0, true);
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (rc) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            if (e != hipSuccess) return fail(ctx, FL_E_HIP, "verify graph capture failed: %s", hipGetErrorString(e));
+            hipGraphExec_t ge = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ei != hipSuccess) return fail(ctx, FL_E_HIP, "verify graph instantiate: %s", hipGetErrorString(ei));
+            it = ctx->vgraphs.emplace(M, ge).first;
+        }
+        HIPCHK(ctx, hipGraphLaunch(it->second, st));
+    } else {
+        rc = enqueue_verify(ctx, M, pos0, false);
+        if (rc) return rc;
     }
     std::vector<unsigned long long> keys(M);
     HIPCHK(ctx, hipMemcpyAsync(keys.data(), ctx->vslots, (size_t)M * 8, hipMemcpyDeviceToHost, st));

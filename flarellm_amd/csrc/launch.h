@@ -123,8 +123,9 @@ enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2, KV_KIVI = 3 };  // == FL_KV_*
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq = 1);
 // Write n token rows (device f32 [n][nkv][D]) at positions p0.. into a Q8 or
 // KIVI cache (quantizing the KIVI groups that leave the ring).
+// p0p (optional, F32 / F16 / Q8): read the first position from the device instead of p0.
 hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
-                           int p0, int n, int D);
+                           int p0, int n, int D, const int *p0p = nullptr);
 
 // MFMA output projection with f32 input for up to 8 tokens (mvo.hip)
 struct MvoArgs;

@@ -145,3 +145,30 @@ def test_verify_accepts_sequential_greedy_stream(backend, oracle):
     drafts = stream[:8].astype(np.uint32)
     got, _ = backend.verify(drafts, len(prompt))
     assert got.tolist() == stream[1:9].tolist()
+
+
+@pytest.mark.parametrize("kv", ["f16", "q8"])
+def test_verify_graph_replays_match_eager(backend, oracle, kv, monkeypatch):
+    """The captured verify graph (F16 / Q8 caches) against the same pass
+    enqueued kernel by kernel: identical tokens and logits on every replay,
+    with the program's own decode steps and synchronizations in between, at
+    two batch sizes and two positions (the position is read on the device)."""
+    print(f"[verify-graph] kv={kv}", flush=True)
+    spec = MODELS["q8_hd128"]
+    model = S.make_model(spec, seed=21)
+    prompt = S.random_tokens(121, 30, spec.vocab)
+    backend.init_gpu_kv_cache(spec, KV[kv])
+    backend.upload_weights_to_gpu(model)
+    backend.generate(prompt, 1)
+    for M, pos in ((8, 30), (5, 30), (8, 33)):
+        drafts = S.random_tokens(200 + M + pos, M, spec.vocab)
+        monkeypatch.setenv("FLARE_NO_VERIFY_GRAPH", "1")
+        want, wv = backend.verify(drafts, pos)
+        monkeypatch.delenv("FLARE_NO_VERIFY_GRAPH")
+        for rep in range(3):
+            got, gv = backend.verify(drafts, pos)
+            assert got.tolist() == want.tolist(), (M, pos, rep)
+            assert np.array_equal(gv, wv), (M, pos, rep)
+            # eager work between replays (rewrites the first slots it verified)
+            backend.forward_greedy(int(drafts[0]), pos)
+            backend.sync()
