@@ -338,12 +338,90 @@ __device__ __forceinline__ float pc_dot(const Pc<FMT> &P, const WDesc &W, const 
 }
 
 // ---------------------------------------------------------------------------
+// Register-resident activation (Q8_0 weights, norm prologue, whole row in one
+// unit: S <= SU steps).  Lane l of a wave reads exactly the activations
+// [1024 s + 16 l, +16) of every step s, and a 32-block is a lane pair, so each
+// wave normalizes and quantizes x itself: sum of squares by a wave reduction,
+// block amax by a lane-pair exchange, codes and block scales kept in
+// registers.  No LDS staging and no workgroup barrier: a wave starts on its
+// weights as soon as its own activations have arrived.
+// (rmsnorm_quantize_q8_0_scalar model.rs:5610-5640 / rmsnorm_scalar_into +
+// quantize_input_q8_0_into 7456-7477, 5534-5571)
+// ---------------------------------------------------------------------------
+template <int SX>
+struct RegX8 {
+    v4f_t xv[SX][4], wv[SX][4];
+    v4i_t q[SX];
+    float sc[SX];
+    __device__ __forceinline__ void issue(const MvsArgs &a, int lane) {
+        const int K = a.W.cols;
+#pragma unroll
+        for (int s = 0; s < SX; s++) {
+            const int off = min(s * 1024 + 16 * lane, K - 16);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                xv[s][j] = *(const v4f_t *)(a.x + off + 4 * j);
+                wv[s][j] = *(const v4f_t *)(a.nw + off + 4 * j);
+            }
+        }
+    }
+    __device__ __forceinline__ void finish(const MvsArgs &a, int lane) {
+        const int K = a.W.cols;
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SX; s++) {
+            if (s * 1024 + 16 * lane < K) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) ss += xv[s][j][k] * xv[s][j][k];
+            }
+        }
+        ss = wave_sum(ss);
+        const float rms = sqrtf(ss / (float)K + a.eps);
+        const float inv = 1.0f / rms;
+#pragma unroll
+        for (int s = 0; s < SX; s++) {
+            float v[16];
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float x = xv[s][j][k], w = wv[s][j][k];
+                    v[4 * j + k] = a.pro == PRO_NORMQ0 ? x * w * inv : (x * inv) * w;
+                    amax = fmaxf(amax, fabsf(v[4 * j + k]));
+                }
+            amax = fmaxf(amax, __int_as_float(xpair(__float_as_int(amax))));  // the block's other half
+            const float d = amax / 127.0f;
+            const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+            uint32_t pk[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 16; i++) pk[i >> 2] |= (uint32_t)(uint8_t)sat_i8(roundf(v[i] * id)) << (8 * (i & 3));
+            q[s] = v4i_t{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+            sc[s] = d;
+        }
+    }
+};
+
+// matvec_q8_0_preq_into per-block term with the activation codes in registers
+__device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W, const v4i_t &xq, float xs, int step,
+                                            int lane) {
+    int d = dot16(P.q, xq, 0);
+    d += xpair(d);
+    const float t = (h2f((uint16_t)P.sc) * xs) * (float)d;
+    return (step * 1024 + 16 * lane < W.cols && !(lane & 1)) ? t : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
 // k_mvs: generic persistent streaming matvec
 // ---------------------------------------------------------------------------
 constexpr int kMvsThreads = 256;
 
-template <int FMT, bool F32IN, int R, int SU>
+// RX: register-resident activation (Q8_0, norm prologue, S <= SU; RegX8)
+template <int FMT, bool F32IN, int R, int SU, bool RX = false>
 __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
+    static_assert(!RX || (FMT == F_Q8_0 && !F32IN), "register activation: Q8_0 weights, Q8 input");
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
     const int K = W.cols;
@@ -366,7 +444,9 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     MV_TS(0);
     MV_TSB(0);
     Stage<F32IN, kMvsThreads> stg;
-    stg.issue(a);                  // 1. activation loads
+    RegX8<RX ? SU : 1> rx;
+    if constexpr (RX) rx.issue(a, lane);
+    else stg.issue(a);             // 1. activation loads
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
     load(ta, 0);                   // 2. first weight pieces (unconditional: clamped rows are valid, and
                                    // the prologue below then waits for the activation loads only)
@@ -395,7 +475,8 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         pre1 = *p1;
     }
     MV_TS(1);
-    stg.finish(a, smem);           // 3. prologue arithmetic (ends with a barrier)
+    if constexpr (RX) rx.finish(a, lane);
+    else stg.finish(a, smem);      // 3. prologue arithmetic (ends with a barrier)
     MV_TS(2);
 
     float acc[R];
@@ -415,6 +496,12 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
                 for (int r = 0; r < R; r++) acc[r] += pc_dot_f32x(T[r][s], X);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        } else if constexpr (RX) {
+            // one unit covers the row (NR == 1): step s is compile-time
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int s = 0; s < SU; s++) acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
         } else {
 #pragma unroll
             for (int r = 0; r < R; r++)
@@ -466,8 +553,9 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 // b, b + grid, ...; wave w takes hidden units 32*blk + w*HU .. + HU, HU/2 at
 // a time (item = 2 gate rows + the 2 matching up rows).
 // ---------------------------------------------------------------------------
-template <int FMT, int SU, int NW>
+template <int FMT, int SU, int NW, bool RX = false>
 __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
+    static_assert(!RX || FMT == F_Q8_0, "register activation: Q8_0 weights");
     extern __shared__ __align__(16) char smem[];
     constexpr int NT = NW * 64, HU = 32 / NW, IPB = HU / 2;  // items per wave per block
     static_assert(HU % 2 == 0, "two hidden units per item");
@@ -502,11 +590,14 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     MV_TS(0);
     MV_TSB(0);
     Stage<false, NT> stg;
-    stg.issue(a);
+    RegX8<RX ? SU : 1> rx;
+    if constexpr (RX) rx.issue(a, lane);
+    else stg.issue(a);
     FLARE_STAGE_BARRIER();
     load(ta, 0);  // unconditional, so the prologue waits for the activation loads only
     MV_TS(1);
-    stg.finish(a, smem);
+    if constexpr (RX) rx.finish(a, lane);
+    else stg.finish(a, smem);
     MV_TS(2);
 
     float acc[R];
@@ -518,7 +609,10 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int s = 0; s < SU; s++) acc[r] += pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+            for (int s = 0; s < SU; s++) {
+                if constexpr (RX) acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                else acc[r] += pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+            }
         if (u == 0) MV_TS(3);
         if (rr == NR - 1) {
 #pragma unroll
