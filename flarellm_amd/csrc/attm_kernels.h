@@ -701,7 +701,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         // (all loads of a batch independent), online rescale between batches:
         // out = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M)
         ATTN_TSL(6);
-        constexpr int MB = OPT == 1 ? 32 : 16;
+        // batch size from the live split count (8 / 16 / 24 / 32): every load
+        // of a batch is a live partial, and up to 24-32 splits take one trip
         const float *pb = a.part + (size_t)kvh * a.nsplit * P;
         float M[OPT], L[OPT], O[OPT];
 #pragma unroll
@@ -710,36 +711,43 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             L[k] = 0.0f;
             O[k] = 0.0f;
         }
-        for (int j0 = 0; j0 < nact; j0 += MB) {
+        auto merge = [&](auto mbc) {
+            constexpr int MB = decltype(mbc)::value;
+            for (int j0 = 0; j0 < nact; j0 += MB) {
 #pragma unroll
-            for (int k = 0; k < OPT; k++) {
-                const int i = min(tid + k * NTH, G * D - 1), g = i / D;
-                float mv[MB], lv[MB], ov[MB];
+                for (int k = 0; k < OPT; k++) {
+                    const int i = min(tid + k * NTH, G * D - 1), g = i / D;
+                    float mv[MB], lv[MB], ov[MB];
 #pragma unroll
-                for (int k2 = 0; k2 < MB; k2++) {
-                    const float *pj = pb + (size_t)min(j0 + k2, nact - 1) * P;
-                    mv[k2] = ld_agent(pj + G * D + 2 * g);
-                    lv[k2] = ld_agent(pj + G * D + 2 * g + 1);
-                    ov[k2] = ld_agent(pj + i);
-                }
-                float Mb = M[k];
-#pragma unroll
-                for (int k2 = 0; k2 < MB; k2++)
-                    if (j0 + k2 < nact) Mb = fmaxf(Mb, mv[k2]);
-                const float rr = (M[k] == -INFINITY) ? 0.0f : __expf(M[k] - Mb);
-                L[k] *= rr;
-                O[k] *= rr;
-#pragma unroll
-                for (int k2 = 0; k2 < MB; k2++) {
-                    if (j0 + k2 < nact) {
-                        const float w = (mv[k2] == -INFINITY) ? 0.0f : __expf(mv[k2] - Mb);
-                        L[k] += lv[k2] * w;
-                        O[k] += ov[k2] * w;
+                    for (int k2 = 0; k2 < MB; k2++) {
+                        const float *pj = pb + (size_t)min(j0 + k2, nact - 1) * P;
+                        mv[k2] = ld_agent(pj + G * D + 2 * g);
+                        lv[k2] = ld_agent(pj + G * D + 2 * g + 1);
+                        ov[k2] = ld_agent(pj + i);
                     }
+                    float Mb = M[k];
+#pragma unroll
+                    for (int k2 = 0; k2 < MB; k2++)
+                        if (j0 + k2 < nact) Mb = fmaxf(Mb, mv[k2]);
+                    const float rr = (M[k] == -INFINITY) ? 0.0f : __expf(M[k] - Mb);
+                    L[k] *= rr;
+                    O[k] *= rr;
+#pragma unroll
+                    for (int k2 = 0; k2 < MB; k2++) {
+                        if (j0 + k2 < nact) {
+                            const float w = (mv[k2] == -INFINITY) ? 0.0f : __expf(mv[k2] - Mb);
+                            L[k] += lv[k2] * w;
+                            O[k] += ov[k2] * w;
+                        }
+                    }
+                    M[k] = Mb;
                 }
-                M[k] = Mb;
             }
-        }
+        };
+        if (nact <= 8) merge(std::integral_constant<int, 8>{});
+        else if (nact <= 16) merge(std::integral_constant<int, 16>{});
+        else if (OPT > 1 || nact <= 24) merge(std::integral_constant<int, OPT == 1 ? 24 : 16>{});
+        else merge(std::integral_constant<int, 32>{});
         ATTN_TSL(7);
 #pragma unroll
         for (int k = 0; k < OPT; k++) O[k] *= 1.0f / L[k];
