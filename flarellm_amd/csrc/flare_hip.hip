@@ -463,7 +463,7 @@ static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const 
                        float *out, unsigned long long *slot, const QkvEpi *qe = nullptr) {
     if (pro == PRO_LOADQ && w.cols > 4 * 16 * kMvsThreads)
         return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
-    const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, false);
+    const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, false, epi == EPI_QKV);
     MvsArgs a = mvs_args(ctx, w, pro, epi, x, nw, eps, q, s, sums, out, slot);
     if (epi == EPI_QKV) {
         if (!qe) return fail(ctx, FL_E_INVALID, "EPI_QKV without its arguments");

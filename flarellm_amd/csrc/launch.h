@@ -51,19 +51,25 @@ struct MvsPlan {
 
 // (R, SU) per format and step count: tiles of 2-8 pieces, chosen so the
 // kernel stays within ~160 VGPRs (>= 3 waves per SIMD)
-inline void mvs_shape(int fmt, bool f32in, int S, int &r, int &su) {
+// pairs: the epilogue needs row pairs (fused QKV + RoPE)
+inline void mvs_shape(int fmt, bool f32in, int S, bool pairs, int &r, int &su) {
     // f32 input (logits), measured on MI355X: Q8_0 2 rows x 2 KiB, Q6_K 2 rows x 1 KiB
     if (fmt == F_Q8_0 && f32in) { r = 2; su = S >= 2 ? 2 : 1; return; }
     if (fmt == F_Q6K && f32in) { r = 2; su = 1; return; }
     if (S <= 1) { r = 4; su = 1; return; }
-    if (fmt == F_Q4K || fmt == F_Q6K) { r = 2; su = 2; return; }
+    // Q4_K with Q8 input, measured on MI355X (Llama-3-8B): QKV 2 rows x 1 KiB,
+    // wo / down 1 row x 2 KiB
+    if (fmt == F_Q4K) { r = pairs ? 2 : 1; su = pairs ? 1 : 2; return; }
+    if (fmt == F_Q6K) { r = 2; su = 2; return; }
     if (S == 2 || S == 3) { r = 4; su = 2; return; }
-    r = 2; su = 4;
+    // long Q8_0 rows (Llama-3.2-1B down, 8 KiB): 1 row x 4 KiB measured best
+    r = pairs ? 2 : 1;
+    su = 4;
 }
 
-inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in) {
+inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = false) {
     MvsPlan p;
-    mvs_shape(fmt, f32in, mvs_steps(fmt, cols), p.r, p.su);
+    mvs_shape(fmt, f32in, mvs_steps(fmt, cols), pairs, p.r, p.su);
     // tuning overrides for the Q8-input kernels (experiments): FLARE_MVS_R /
     // FLARE_MVS_SU / FLARE_MVS_GRID
     // (FLARE_MVF_R / FLARE_MVF_SU for the f32-input kernels)
