@@ -404,6 +404,25 @@ struct RegX8 {
     }
 };
 
+// PRO_LOADQ variant: the activation arrives quantized (the attention output,
+// the SiLU*up hidden vector); each lane loads its own 16 codes and block scale
+// per step straight into registers.
+template <int SX>
+struct RegX8L {
+    v4i_t q[SX];
+    float sc[SX];
+    __device__ __forceinline__ void issue(const MvsArgs &a, int lane) {
+        const int K = a.W.cols;
+#pragma unroll
+        for (int s = 0; s < SX; s++) {
+            const int off = min(s * 1024 + 16 * lane, K - 16);
+            q[s] = *(const v4i_t *)(a.gq + off);
+            sc[s] = a.gs[off >> 5];
+        }
+    }
+    __device__ __forceinline__ void finish(const MvsArgs &, int) {}
+};
+
 // matvec_q8_0_preq_into per-block term with the activation codes in registers
 __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W, const v4i_t &xq, float xs, int step,
                                             int lane) {
@@ -418,8 +437,9 @@ __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W,
 // ---------------------------------------------------------------------------
 constexpr int kMvsThreads = 256;
 
-// RX: register-resident activation (Q8_0, norm prologue, S <= SU; RegX8)
-template <int FMT, bool F32IN, int R, int SU, bool RX = false>
+// RX: register-resident activation (Q8_0, S <= SU): 1 = norm prologue
+// (RegX8), 2 = pre-quantized input (RegX8L)
+template <int FMT, bool F32IN, int R, int SU, int RX = 0>
 __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     static_assert(!RX || (FMT == F_Q8_0 && !F32IN), "register activation: Q8_0 weights, Q8 input");
     extern __shared__ __align__(16) char smem[];
@@ -444,7 +464,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     MV_TS(0);
     MV_TSB(0);
     Stage<F32IN, kMvsThreads> stg;
-    RegX8<RX ? SU : 1> rx;
+    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);             // 1. activation loads
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
@@ -553,7 +573,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 // b, b + grid, ...; wave w takes hidden units 32*blk + w*HU .. + HU, HU/2 at
 // a time (item = 2 gate rows + the 2 matching up rows).
 // ---------------------------------------------------------------------------
-template <int FMT, int SU, int NW, bool RX = false>
+template <int FMT, int SU, int NW, int RX = 0>
 __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     static_assert(!RX || FMT == F_Q8_0, "register activation: Q8_0 weights");
     extern __shared__ __align__(16) char smem[];
@@ -590,7 +610,7 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     MV_TS(0);
     MV_TSB(0);
     Stage<false, NT> stg;
-    RegX8<RX ? SU : 1> rx;
+    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);
     FLARE_STAGE_BARRIER();
