@@ -153,7 +153,10 @@ __device__ __forceinline__ uint32_t key_index(unsigned long long k) {
 }
 
 template <int FMT>
-__global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x) {
+// Also writes the RoPE (cos, sin) row of the step's position (RopeTable,
+// model.rs:7190-7212) to rope_cur, read by the QKV epilogues of every layer.
+__global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x, const float *rope,
+                                                   long long sin_off, int half, float *rope_cur) {
     __shared__ int tok_s, step_s;
     if (threadIdx.x == 0) {
         const int s = st->step;
@@ -182,6 +185,10 @@ __global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *
             v = ((const float *)E.q)[(size_t)row * H + i];
         }
         x[i] = v;
+    }
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        rope_cur[i] = rope[(size_t)step_s * half + i];
+        rope_cur[half + i] = rope[sin_off + (size_t)step_s * half + i];
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -254,6 +261,7 @@ struct fl_ctx {
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
     float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
     long long *bench_trace = nullptr;  // attention phase timestamps (FLARE_ATTN_TRACE builds)
+    float *rope_cur = nullptr;         // RoPE (cos, sin) of the step in flight [D]
     int8_t *aq = nullptr, *hq = nullptr;
     float *as = nullptr, *hs = nullptr;
     int *asum = nullptr, *hsum = nullptr;
@@ -634,12 +642,12 @@ static void model_release(fl_ctx *c) {
     c->kscale = c->vscale = nullptr; c->kparam = c->vparam = nullptr; c->kring = c->vring = nullptr;
     c->kvstage = nullptr; c->kvstage_rows = 0;
     void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits, c->bench_out,
-                    c->bench_trace,
+                    c->bench_trace, c->rope_cur,
                     c->aq, c->hq, c->as, c->hs, c->asum, c->hsum, c->st, c->tokens};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
-    c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
+    c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->rope_cur = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
     void *vp[] = {c->vx, c->vx2, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
                   c->vtok, c->vpos, c->vslots};
@@ -969,6 +977,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->logits, (size_t)c.vocab_size * 4);
     ALLOC(ctx, ctx->bench_out, std::max({(size_t)c.vocab_size, H, qd + 2 * kvd, 2 * F}) * 4);
     ALLOC(ctx, ctx->bench_trace, (64 + 3072) * 8);
+    ALLOC(ctx, ctx->rope_cur, (size_t)c.head_dim * 4);
     ALLOC(ctx, ctx->st, sizeof(DevState));
     ALLOC(ctx, ctx->tokens, S * 4);
     HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
@@ -1202,8 +1211,7 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
     AttnArgs a{};
     kv_layer_args(ctx, l, a);
     QkvEpi e{};
-    e.rope = ctx->rope;
-    e.sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
+    e.rope_cur = ctx->rope_cur;
     e.posp = &ctx->st->pos;
     e.kc = (void *)a.kc;
     e.vc = (void *)a.vc;
@@ -1224,11 +1232,12 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     const int hd = c.head_dim, G = c.num_heads / c.num_kv_heads;
     const float eps = c.rms_norm_eps;
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
+    const long long sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
     switch (ctx->embed.format) {
-    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
-    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
-    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
-    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x); break;
+    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
     }
     HIPCHK(ctx, hipGetLastError());
     for (int l = 0; l < c.num_layers; l++) {
@@ -1824,7 +1833,7 @@ const char *fl_bench_kernel_name(fl_ctx *ctx, int which) {
     case 2: return "k_mvs_gu";
     case 3: return "k_mvs";
     case 4: return "k_mvs";
-    case 5: return "k_attn";
+    case 5: return ctx->kv_format == FL_KV_F32 ? "k_attn" : "k_attm";
     }
     return "";
 }

@@ -15,8 +15,7 @@ enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_ARGMAX = 2, EPI_QKV = 3 };
 // row 2i+1 = original row i + D/2), so each rotate-half pair of
 // apply_rope_with_table (model.rs:7283-7296) lands in one tile.
 struct QkvEpi {
-    const float *rope;  // cos table [max_pos][D/2]; sin table at rope + sin_off
-    long long sin_off;
+    const float *rope_cur;  // RoPE cos [D/2] then sin [D/2] of the step's position (k_embed writes them)
     const int *posp;    // token position (device)
     void *kc, *vc;      // this layer's head-major cache [kv_head][slot][D]
     long long head_stride;  // elements between kv heads (max_seq * D)
@@ -302,10 +301,10 @@ __device__ __forceinline__ float lane_row(const float *acc, int gl) {
 
 // RoPE (cos, sin) of the pair that lane p < R/2 stores for rows n = row0 + 2p
 // (q and k rows only).
-__device__ __forceinline__ void qkv_rope_cs(const QkvEpi &e, int n, int pos, float &c, float &sn) {
+__device__ __forceinline__ void qkv_rope_cs(const QkvEpi &e, int n, float &c, float &sn) {
     const int half = e.hd >> 1, i = (n % e.hd) >> 1;
-    c = e.rope[(size_t)pos * half + i];
-    sn = e.rope[e.sin_off + (size_t)pos * half + i];
+    c = e.rope_cur[i];
+    sn = e.rope_cur[half + i];
 }
 
 // EPI_QKV store of one rotate-half pair (rows n, n+1 in the pair-interleaved
@@ -371,7 +370,7 @@ __device__ __forceinline__ void store_qkv(const float *acc, int row0, int rows, 
         if (gl == p && row0 + 2 * p < rows) {
             const int n = row0 + 2 * p;
             float c = pc, sn = ps;
-            if (!pre_ok && n < e.nq + e.nk) qkv_rope_cs(e, n, pos, c, sn);
+            if (!pre_ok && n < e.nq + e.nk) qkv_rope_cs(e, n, c, sn);
             store_qkv_pair(acc[2 * p], acc[2 * p + 1], n, e, pos, q, c, sn);
         }
 }

@@ -488,8 +488,8 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         if (a.epi == EPI_QKV) {
             const int half = a.qkv.hd >> 1;
             const int n = min(row0f + 2 * min(lane, R / 2 - 1), W.rows - 1);
-            p0 = a.qkv.rope + (size_t)qpos * half + ((n % a.qkv.hd) >> 1);
-            p1 = p0 + a.qkv.sin_off;
+            p0 = a.qkv.rope_cur + ((n % a.qkv.hd) >> 1);  // no dependence on the position load
+            p1 = p0 + half;
         }
         pre0 = *p0;
         pre1 = *p1;
