@@ -152,10 +152,13 @@ __device__ __forceinline__ uint32_t key_index(unsigned long long k) {
     return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull);
 }
 
-template <int FMT>
 // Also writes the RoPE (cos, sin) row of the step's position (RopeTable,
 // model.rs:7190-7212) to rope_cur, read by the QKV epilogues of every layer.
-__global__ __launch_bounds__(kThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x, const float *rope,
+// One workgroup of kEmbedThreads (few elements per thread: the dequant loads
+// of each element are a dependent chain).
+constexpr int kEmbedThreads = 1024;
+template <int FMT>
+__global__ __launch_bounds__(kEmbedThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x, const float *rope,
                                                    long long sin_off, int half, float *rope_cur) {
     __shared__ int tok_s, step_s;
     if (threadIdx.x == 0) {
@@ -1234,10 +1237,10 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
     const long long sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
     switch (ctx->embed.format) {
-    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
     }
     HIPCHK(ctx, hipGetLastError());
     for (int l = 0; l < c.num_layers; l++) {
