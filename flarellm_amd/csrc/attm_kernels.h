@@ -231,7 +231,29 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     const int kvh = blockIdx.y, s = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
     ATTN_TS(0);
-    const int pos = *a.posp + zq, T = pos + 1;
+    using Tile0 = typename std::conditional<KIVI, AttmKiviQ<D>, AttmTile<KT, D>>::type;
+    Tile0 tile;
+    // fp16 / Q8 caches of at most nsplit * chmin slots (spec_first): every
+    // chunk is chmin slots, so the wave's first block is known before the
+    // position is, and its K / V loads go out first.  The query loads precede
+    // the position load (a vector load, so waiting for it does not hold up
+    // the kernel arguments).
+    const int t0s = s * a.chmin;
+    // (Q8: always; the unconditional early load also keeps the Q8 kernel's
+    // registers below the spill threshold, measured at 128k slots)
+    const bool spec = std::is_same<KT, KvQ8>::value || (!KIVI && a.spec_first);
+    if (spec) tile.load(a, kvh, min(t0s + wave * kAttmBlock, a.S - kAttmBlock), a.S - 1, lane);
+    v4f_t qv[DT][2];
+    {
+        const int g = min(r >> 1, G - 1);
+        const v4f_t *qp = (const v4f_t *)(a.q + (size_t)(kvh * G + g) * D + 8 * kg);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            qv[dt][0] = qp[8 * dt];
+            qv[dt][1] = qp[8 * dt + 1];
+        }
+    }
+    const int pos = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + zq, T = pos + 1;
     // up to a.single tokens: one split (no cross-workgroup merge);
     // beyond: chunks of at least chmin slots over the nsplit workgroups
     int CH = T <= a.single ? T : max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
@@ -245,24 +267,24 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     NewRow<KT> nrow;
     const bool has_new = a.knew != nullptr;
 
-    // the first block's K / V loads go out before the query setup
     const int nblk = (t1 - t0 + kAttmBlock - 1) / kAttmBlock;
     // KIVI: blocks [0, nqb) of the chunk come from the 2-bit prefix (qlen
     // and t0 are multiples of 32), the rest from the fp16 ring
     const int qlen = kivi_qlen(T);
     const int nqb = KIVI ? min(nblk, max(0, (qlen - t0) / kAttmBlock)) : 0;
-    using Tile0 = typename std::conditional<KIVI, AttmKiviQ<D>, AttmTile<KT, D>>::type;
-    Tile0 tile;
-    if (wave < (KIVI ? nqb : nblk)) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
+    if constexpr (KIVI) {
+        if (wave < nqb) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
+    } else {
+        if ((!spec || t0 != t0s) && wave < nblk) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
+    }
 
     // A operand of S: row m = 2g + (hi / lo) of head g (rows >= 2G zero)
     v8h_t aq[DT];
     {
         const int m = r, g = min(m >> 1, G - 1);
-        const v4f_t *qp = (const v4f_t *)(a.q + (size_t)(kvh * G + g) * D + 8 * kg);
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            const v4f_t q0 = qp[8 * dt], q1 = qp[8 * dt + 1];
+            const v4f_t q0 = qv[dt][0], q1 = qv[dt][1];
             float x[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
             if ((m >> 1) >= G) {
 #pragma unroll
