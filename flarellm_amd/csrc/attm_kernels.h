@@ -233,16 +233,15 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     ATTN_TS(0);
     using Tile0 = typename std::conditional<KIVI, AttmKiviQ<D>, AttmTile<KT, D>>::type;
     Tile0 tile;
-    // fp16 / Q8 caches of at most nsplit * chmin slots (spec_first): every
-    // chunk is chmin slots, so the wave's first block is known before the
-    // position is, and its K / V loads go out first.  The query loads precede
-    // the position load (a vector load, so waiting for it does not hold up
-    // the kernel arguments).
+    // Q8: the wave's first block is loaded before the position is known,
+    // assuming chmin-slot chunks (exact while T <= nsplit * chmin, reloaded
+    // otherwise); the unconditional early load also keeps this kernel's
+    // registers below the spill threshold (measured at 128k slots).  The query
+    // loads precede the position load (a vector load, so waiting for it does
+    // not hold up the kernel arguments).
     const int t0s = s * a.chmin;
-    // (Q8: always; the unconditional early load also keeps the Q8 kernel's
-    // registers below the spill threshold, measured at 128k slots)
-    const bool spec = std::is_same<KT, KvQ8>::value || (!KIVI && a.spec_first);
-    if (spec) tile.load(a, kvh, min(t0s + wave * kAttmBlock, a.S - kAttmBlock), a.S - 1, lane);
+    constexpr bool spec = std::is_same<KT, KvQ8>::value;
+    if constexpr (spec) tile.load(a, kvh, min(t0s + wave * kAttmBlock, a.S - kAttmBlock), a.S - 1, lane);
     v4f_t qv[DT][2];
     {
         const int g = min(r >> 1, G - 1);

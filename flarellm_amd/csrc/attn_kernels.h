@@ -25,7 +25,6 @@ struct AttnArgs {
     int chmin;           // minimum tokens per split (a multiple of attn_tpp(D))
     int single;          // MFMA kernel: contexts up to this many tokens run as one split
     int waves;           // MFMA kernel: waves per workgroup (4 or 8; other values mean 8)
-    int spec_first;      // MFMA kernel: S <= nsplit * chmin, first block loaded before the position
     float *part;         // [nkv][nsplit][G][D+2] split partials
     int *counters;       // [nkv] arrival counters (zero between launches)
     float *out;          // [nh*D]

@@ -1192,7 +1192,6 @@ static AttnArgs layer_attn_args(fl_ctx *ctx, int l) {
     a.chmin = ctx->chmin;
     a.single = ctx->single;
     a.waves = ctx->attn_waves;
-    a.spec_first = a.S <= ctx->nsplit * ctx->chmin;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = nullptr;  // the wo matvec reads the Q8_0 copy only
@@ -1437,7 +1436,6 @@ int fl_gqa_from_cache(fl_ctx *ctx, int layer, const float *q, int seq_len, float
     a.chmin = ctx->chmin;
     a.single = ctx->single;
     a.waves = ctx->attn_waves;
-    a.spec_first = a.S <= ctx->nsplit * ctx->chmin;
     a.part = ctx->d_part;
     a.counters = ctx->d_counters;
     a.out = ctx->attn;
@@ -1463,7 +1461,6 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
         a.chmin = ctx->chmin;
         a.single = ctx->single;
         a.waves = ctx->attn_waves;
-        a.spec_first = a.S <= ctx->nsplit * ctx->chmin;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = ctx->attn;
@@ -1621,7 +1618,6 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         a.chmin = ctx->chmin;
         a.single = ctx->single;
         a.waves = ctx->attn_waves;
-        a.spec_first = a.S <= ctx->nsplit * ctx->chmin;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
         a.out = nullptr;
