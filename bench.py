@@ -157,7 +157,7 @@ def bench_attention_c4(args) -> int:
         "config": {"workload": WORKLOADS["c4"]["desc"], "model": "Llama-3-8B heads", "global_batch": 1,
                    "seq_len": max(ctxs), "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": d["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": d["frac"], "traffic": None, "kernel": f"k_attn {dom}", "bytes_per_launch": d["bytes"],
+                     "frac": d["frac"], "traffic": None, "kernel": f"k_attm {dom}", "bytes_per_launch": d["bytes"],
                      "avg_launch_us": d["us"]},
         "cpu_baseline": None,
         "cases": cases,
@@ -263,6 +263,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=40)
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="override the workload's prompt length (profiling runs of the weight-streaming kernels, "
+                         "whose bytes do not depend on the context; the reported line names the length used)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -283,7 +286,7 @@ def main() -> int:
         return bench_verify_c5(args)
     wl = WORKLOADS[args.config]
     spec = S.CONFIGS[wl["spec"]]
-    n_prompt = wl["prompt"]
+    n_prompt = wl["prompt"] if args.prompt is None else max(1, args.prompt)
     need = n_prompt + args.warmup + args.steps
     if need > spec.max_seq:
         spec = S.replace(spec, max_seq=need)
