@@ -57,9 +57,9 @@ inline void mvs_shape(int fmt, bool f32in, int S, bool pairs, int &r, int &su) {
     if (fmt == F_Q8_0 && f32in) { r = 2; su = S >= 2 ? 2 : 1; return; }
     if (fmt == F_Q6K && f32in) { r = 2; su = 1; return; }
     if (S <= 1) { r = 4; su = 1; return; }
-    // Q4_K with Q8 input, measured on MI355X (Llama-3-8B): QKV 2 rows x 1 KiB,
+    // Q4_K with Q8 input, measured on MI355X (Llama-3-8B): QKV 2 rows x 2 KiB,
     // wo / down 1 row x 2 KiB
-    if (fmt == F_Q4K) { r = pairs ? 2 : 1; su = pairs ? 1 : 2; return; }
+    if (fmt == F_Q4K) { r = pairs ? 2 : 1; su = 2; return; }
     if (fmt == F_Q6K) { r = 2; su = 2; return; }
     if (S == 2 || S == 3) { r = 4; su = 2; return; }
     // long Q8_0 rows (Llama-3.2-1B down, 8 KiB): 1 row x 4 KiB measured best
@@ -73,12 +73,14 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = fa
     // tuning overrides for the Q8-input kernels (experiments): FLARE_MVS_R /
     // FLARE_MVS_SU / FLARE_MVS_GRID
     // (FLARE_MVF_R / FLARE_MVF_SU for the f32-input kernels)
-    const char *er = getenv(f32in ? "FLARE_MVF_R" : "FLARE_MVS_R");
+    const char *er = getenv(f32in ? "FLARE_MVF_R" : pairs ? "FLARE_QKV_R" : "FLARE_MVS_R");
     if (er) p.r = atoi(er);
-    if (const char *e = getenv(f32in ? "FLARE_MVF_SU" : "FLARE_MVS_SU")) p.su = atoi(e);
+    if (const char *e = getenv(f32in ? "FLARE_MVF_SU" : pairs ? "FLARE_QKV_SU" : "FLARE_MVS_SU")) p.su = atoi(e);
     // fill the chip: halve the rows per group while fewer than 256
-    // workgroups (4 waves, one group each) would run
-    while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !er) p.r /= 2;
+    // workgroups (4 waves, one group each) would run; not for the fused QKV,
+    // whose waves each normalise the activation (4 rows x 2 KiB measured
+    // best for Llama-3.2-1B's 3072 rows: 5.7 vs 6.5 us)
+    while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !er && !pairs) p.r /= 2;
     const int ngrp = (rows + p.r - 1) / std::max(1, p.r);
     p.grid = std::max(1, std::min((ngrp + 3) / 4, 1024));
     if (const char *e = getenv("FLARE_MVS_GRID")) p.grid = std::max(1, std::min(p.grid, atoi(e)));
@@ -87,15 +89,15 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = fa
     return p;
 }
 
-// gate/up: 32 hidden units per workgroup block, 4 rows per item; 8 waves
-// per workgroup when the blocks fit one per CU, else 4 (so every block is
-// resident at once)
+// gate/up: 32 hidden units per workgroup block, 4 rows per item, 8 waves
+// per workgroup
 inline MvsPlan mvs_gu_plan(int fmt, int F, int cols) {
     MvsPlan p;
     const int nblk = F / 32;
-    // waves per workgroup and steps per unit, measured on MI355X: Q4_K (C3
-    // gate/up, 448 blocks) 8 waves x 1 KiB; Q8_0 (C2, 256 blocks) 4 waves x 2 KiB
-    p.r = fmt == F_Q4K ? 8 : 4;
+    // waves per workgroup and steps per unit, measured on MI355X: Q4_K
+    // (Llama-3-8B gate/up, 448 blocks) 8 waves x 1 KiB; Q8_0 (Llama-3.2-1B,
+    // 256 blocks) 8 waves x 2 KiB
+    p.r = 8;
     p.su = (fmt == F_Q8_0 && mvs_steps(fmt, cols) >= 2) ? 2 : 1;
     // tuning overrides (experiments): FLARE_GU_NW / FLARE_GU_SU
     if (const char *e = getenv("FLARE_GU_NW")) p.r = atoi(e);
