@@ -34,11 +34,6 @@ constexpr int kAttmBlock = 32;
 constexpr int kAttmMaxSplit = 64;
 constexpr int kAttmSingle = 1024;  // contexts up to this many tokens run as one split
 
-// Offset of (slot t, channel d) in one kv head's transposed V store.
-__host__ __device__ inline size_t vt_off(int t, int d, int D) {
-    return ((size_t)(t >> 5) * D + d) * 32 + (t & 31);
-}
-
 __device__ __forceinline__ v4f32_t mfma16(const v8h_t &a, const v8h_t &b, const v4f32_t &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

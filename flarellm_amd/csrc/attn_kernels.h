@@ -50,6 +50,11 @@ struct AttnArgs {
     int v_tblk;  // F16 / Q8 model caches: V stored in 32-slot transposed blocks [slot/32][D][32]
 };
 
+// Offset of (slot t, channel d) in one kv head's transposed V store.
+__host__ __device__ inline size_t vt_off(int t, int d, int D) {
+    return ((size_t)(t >> 5) * D + d) * 32 + (t & 31);
+}
+
 // KIVI 2-bit cache constants: groups of 32 (K per channel over 32 tokens, V
 // per token over 32 channels); the newest tokens stay in an fp16 ring.
 constexpr int kKiviGroup = 32;

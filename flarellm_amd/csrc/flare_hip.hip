@@ -1594,24 +1594,23 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         int ks;
         // attention block (model.rs:2016-2311), M tokens at positions pos0..pos0+M-1;
         // the previous layer's down projection is added to x here
-        if (l == 0) {
-            HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.attn_norm, eps, ctx->vxq, ctx->vxs,
-                                         ctx->vxsum));
-        } else {
-            // the previous layer's down projection: partials summed once per
-            // element, then the norm reads x only
-            HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));
-            HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.attn_norm, eps, ctx->vxq, ctx->vxs,
-                                         ctx->vxsum));
-        }
+        // the previous layer's down projection is added to x here (layer 0:
+        // norm only), one workgroup per token
+        HIPCHK(ctx, launch_v_resnorm(pro, st, l ? ctx->vpart : nullptr, ks_down, M, H, xa, L.attn_norm, eps, ctx->vxq,
+                                     ctx->vxs, ctx->vxsum));
         rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
         if (rc) return rc;
-        HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, qd, kvd, D, ctx->rope,
-                                      (long long)c.max_seq_len * (D / 2), ctx->vpos, ctx->vq, ctx->vk, ctx->vv));
         AttnArgs a{};
         kv_layer_args(ctx, l, a);
-        HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D,
-                                    dev_pos ? ctx->vpos : nullptr));
+        // F16 / F32 caches: RoPE'd K and V go straight into the cache slots
+        const bool plain = ctx->kv_format == FL_KV_F16 || ctx->kv_format == FL_KV_F32;
+        const KvDst kd{const_cast<void *>(a.kc), const_cast<void *>(a.vc), a.head_stride, a.v_tblk};
+        HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, qd, kvd, D, ctx->rope,
+                                      (long long)c.max_seq_len * (D / 2), ctx->vpos, ctx->vq, ctx->vk, ctx->vv,
+                                      ctx->kv_format, kd));
+        if (!plain)
+            HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D,
+                                        dev_pos ? ctx->vpos : nullptr));
         a.q = ctx->vq;
         a.posp = ctx->vpos;
         a.nsplit = ctx->nsplit;
@@ -1634,8 +1633,7 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         rc = verify_gemm(ctx, L.wo, M, ctx->vaq, ctx->vas, ctx->vasum, ks);
         if (rc) return rc;
         // FFN block (model.rs:2376-2543): wo residual + FFN norm in one kernel
-        HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks, M, H, xa));
-        HIPCHK(ctx, launch_v_resnorm(pro, st, nullptr, 0, M, H, xa, nullptr, L.ffn_norm, eps, ctx->vxq, ctx->vxs,
+        HIPCHK(ctx, launch_v_resnorm(pro, st, ctx->vpart, ks, M, H, xa, L.ffn_norm, eps, ctx->vxq, ctx->vxs,
                                      ctx->vxsum));
         rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
         if (rc) return rc;

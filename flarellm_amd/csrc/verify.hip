@@ -36,22 +36,30 @@ hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *to
     return hipGetLastError();
 }
 
-hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, const float *xin,
-                            float *xout, const float *w, float eps, int8_t *q, float *s, int *sum) {
-    const dim3 grid((H + 255) / 256, M);
+hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, float *x,
+                            const float *w, float eps, int8_t *q, float *s, int *sum) {
+    if (H % 32 || M < 1) return hipErrorInvalidValue;
     if (pro == PRO_NORMQ0)
-        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ0>, grid, dim3(256), 0, st, part, ksplit, M, H, xin, xout, w, eps, q, s, sum);
+        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ0>, dim3(M), dim3(kResnormThreads), 0, st, part, ksplit, M, H, x, w,
+                           eps, q, s, sum);
     else
-        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ1>, grid, dim3(256), 0, st, part, ksplit, M, H, xin, xout, w, eps, q, s, sum);
+        hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ1>, dim3(M), dim3(kResnormThreads), 0, st, part, ksplit, M, H, x, w,
+                           eps, q, s, sum);
     return hipGetLastError();
 }
 
+// kvfmt KV_F16 / KV_F32: K / V go straight into the cache slots (kv); else
+// to the f32 staging rows Kst / Vst
 hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
                              const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
-                             float *Vst) {
+                             float *Vst, int kvfmt, const KvDst &kv) {
     const dim3 grid((rows / 2 + 255) / 256, M);
-    hipLaunchKernelGGL(k_v_qkv_post, grid, dim3(256), 0, st, part, ksplit, M, rows, nq, nk, D, rope, sin_off, pos0p, Q,
-                       Kst, Vst);
+#define QP(KVW) hipLaunchKernelGGL(k_v_qkv_post<KVW>, grid, dim3(256), 0, st, part, ksplit, M, rows, nq, nk, D, rope, \
+                                   sin_off, pos0p, Q, Kst, Vst, kv)
+    if (kvfmt == KV_F16) QP(1);
+    else if (kvfmt == KV_F32) QP(2);
+    else QP(0);
+#undef QP
     return hipGetLastError();
 }
 

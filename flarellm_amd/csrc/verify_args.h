@@ -21,4 +21,12 @@ struct VgArgs {
     float *part;      // [ksplit][M][rows] fp32 partial sums
 };
 
+// Plain (F32 / F16) cache of one layer, for K / V written straight from the
+// QKV partials.
+struct KvDst {
+    void *kc, *vc;
+    long long head_stride;  // elements between kv heads
+    int v_tblk;             // V in 32-slot transposed blocks
+};
+
 }  // namespace fl

@@ -187,16 +187,30 @@ __global__ __launch_bounds__(256) void k_v_embed(WDesc E, const int *tokens, flo
 }
 
 // QKV partials -> per token: RoPE (apply_rope_with_table, model.rs:7283-7296)
-// on the pair-interleaved q / k rows at position pos0 + t; q to Q[t], K / V
-// rows (f32) to the staging rows written into the cache afterwards.
+// on the pair-interleaved q / k rows at position pos0 + t; q to Q[t].  K / V:
+// KVW 0 = f32 staging rows (quantized into the cache afterwards), 1 / 2 =
+// stored into the F16 / F32 cache slot pos0 + t (cpu_kv_write's layout,
+// model.rs:9810-9846).
+template <int KVW>
 __global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int ksplit, int M, int rows, int nq, int nk,
                                                     int D, const float *rope, long long sin_off, const int *pos0p,
-                                                    float *Q, float *Kst, float *Vst) {
+                                                    float *Q, float *Kst, float *Vst, KvDst kv) {
     const int t = blockIdx.y;
     const int pair = blockIdx.x * blockDim.x + threadIdx.x;  // rows 2*pair, 2*pair+1
     if (2 * pair >= rows) return;
     const int n = 2 * pair, half = D >> 1, pos = *pos0p + t;
     const float x0 = vsum_part(part, ksplit, M, rows, t, n), x1 = vsum_part(part, ksplit, M, rows, t, n + 1);
+    auto put = [&](bool isv, int e, float v) {  // element e of this token's K or V row
+        if constexpr (KVW == 0) {
+            (isv ? Vst : Kst)[(size_t)t * nk + e] = v;
+        } else {
+            const int kvh = e / D, ch = e % D;
+            const size_t o = (size_t)kvh * kv.head_stride +
+                             ((isv && kv.v_tblk) ? vt_off(pos, ch, D) : (size_t)pos * D + ch);
+            if constexpr (KVW == 1) ((__half *)(isv ? kv.vc : kv.kc))[o] = __float2half(v);
+            else ((float *)(isv ? kv.vc : kv.kc))[o] = v;
+        }
+    };
     if (n < nq + nk) {
         const int j = n % D, i = j >> 1;
         const float c = rope[(size_t)pos * half + i], sn = rope[sin_off + (size_t)pos * half + i];
@@ -207,13 +221,13 @@ __global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int kspli
             Q[(size_t)t * nq + h * D + i + half] = y1;
         } else {
             const int k0 = (n - nq) - j;
-            Kst[(size_t)t * nk + k0 + i] = y0;
-            Kst[(size_t)t * nk + k0 + i + half] = y1;
+            put(false, k0 + i, y0);
+            put(false, k0 + i + half, y1);
         }
     } else {
         const int vi = n - nq - nk;
-        Vst[(size_t)t * nk + vi] = x0;
-        Vst[(size_t)t * nk + vi + 1] = x1;
+        put(true, vi, x0);
+        put(true, vi + 1, x1);
     }
 }
 
@@ -223,33 +237,85 @@ __global__ __launch_bounds__(256) void k_v_store(const float *part, int ksplit, 
     if (i < rows) out[(size_t)t * rows + i] = vsum_part(part, ksplit, M, rows, t, i);
 }
 
-// Residual add + RMSNorm + Q8_0 quantization for M tokens (the decode
-// prologue's arithmetic, rmsnorm_quantize_q8_0 / rmsnorm_into + quantize,
-// model.rs:5581-5640 / 7456-7477).  Grid (slices of 256, M): every
-// workgroup of token t forms the whole updated row x_in + partials (for the
-// row's sum of squares), writes its 256-slice to x_out and quantizes it.
-// part == nullptr: no add (x_out unused).
+// Residual add + RMSNorm + Q8_0 quantization for M tokens, one workgroup per
+// token: x[t] += partials (the residual add, model.rs:2305-2311 / 2537-2543;
+// part == nullptr: none), then the decode prologue's arithmetic on the
+// updated row (rmsnorm_quantize_q8_0 / rmsnorm_into + quantize, model.rs:
+// 5581-5640 / 7456-7477).  Thread i holds elements 4i..4i+3 of every
+// 4096-element chunk, so 8 lanes form one 32-block.
+constexpr int kResnormThreads = 1024;
 template <int PRO>
-__global__ __launch_bounds__(256) void k_v_resnorm(const float *part, int ksplit, int M, int H, const float *xin,
-                                                   float *xout, const float *w, float eps, int8_t *q, float *s,
-                                                   int *sum) {
-    __shared__ float red[8];
-    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    const float *xi = xin + (size_t)t * H;
-    float ss = 0.0f, mine = 0.0f;
-    for (int j = threadIdx.x; j < H; j += 256) {
-        const float v = xi[j] + (part ? vsum_part(part, ksplit, M, H, t, j) : 0.0f);
-        ss += v * v;
-        if (j == i) mine = v;
+__global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part, int ksplit, int M, int H, float *x,
+                                                                const float *w, float eps, int8_t *q, float *s,
+                                                                int *sum) {
+    __shared__ float red[kResnormThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    float *xt = x + (size_t)t * H;
+    float ss = 0.0f;
+    for (int e = 4 * tid; e < H; e += 4 * kResnormThreads) {
+        float4 v = *(const float4 *)(xt + e);
+        if (part) {
+            float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int k = 0; k < ksplit; k++) {
+                const float4 pk = *(const float4 *)(part + ((size_t)k * M + t) * H + e);
+                p.x += pk.x;
+                p.y += pk.y;
+                p.z += pk.z;
+                p.w += pk.w;
+            }
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+            *(float4 *)(xt + e) = v;
+        }
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
-    ss = wg_sum(ss, red);
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kResnormThreads / 64; i++) ss += red[i];
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    if (i - (threadIdx.x & 31) >= H) return;  // whole 32-blocks past the row end
-    if (part && i < H) xout[(size_t)t * H + i] = mine;
-    const float wi = i < H ? w[i] : 0.0f;
-    const float v = (PRO == PRO_NORMQ0) ? mine * wi * inv : (mine * inv) * wi;
-    quant_block32_lanes(v, q + (size_t)t * H + (i & ~31), s + (size_t)t * (H >> 5) + (i >> 5),
-                        sum + (size_t)t * (H >> 5) + (i >> 5));
+    for (int e0 = 0; e0 < H; e0 += 4 * kResnormThreads) {  // uniform trip count (shuffles below)
+        const int e = e0 + 4 * tid;
+        const bool in = e < H;  // H % 32 == 0: a 32-block is wholly in or out
+        float4 v = in ? *(const float4 *)(xt + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 wv = in ? *(const float4 *)(w + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float y[4] = {v.x, v.y, v.z, v.w}, wi[4] = {wv.x, wv.y, wv.z, wv.w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            y[j] = (PRO == PRO_NORMQ0) ? y[j] * wi[j] * inv : (y[j] * inv) * wi[j];
+            amax = fmaxf(amax, fabsf(y[j]));
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const float d = amax / 127.0f;
+        const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+        int cs = 0;
+        char4 c;
+        int8_t qq[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            qq[j] = sat_i8(roundf(y[j] * id));
+            cs += qq[j];
+        }
+        c.x = qq[0];
+        c.y = qq[1];
+        c.z = qq[2];
+        c.w = qq[3];
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) cs += __shfl_xor(cs, o, 64);
+        if (in) {
+            *(char4 *)(q + (size_t)t * H + e) = c;
+            if ((tid & 7) == 0) {
+                s[(size_t)t * (H >> 5) + (e >> 5)] = d;
+                sum[(size_t)t * (H >> 5) + (e >> 5)] = cs;
+            }
+        }
+    }
 }
 
 // x[t] += partials (residual add, model.rs:2305-2311 / 2537-2543)
