@@ -1772,6 +1772,15 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
             rc = launch_attention(ctx, ctx->kv_format, c.head_dim, c.num_heads / c.num_kv_heads, a);
             break;
         }
+        case 6: case 7: case 8: case 9: {  // verify GEMMs (8 tokens): qkv, wo, gate/up, down
+            rc = verify_alloc(ctx);
+            if (rc) return rc;
+            const fl_weight *vw[4] = {&L.qkv, &L.wo, &L.gu, &L.down};
+            w = vw[which - 6];
+            int ks;
+            rc = verify_gemm(ctx, *w, 8, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+            break;
+        }
         default: return fail(ctx, FL_E_INVALID, "which=%d", which);
         }
         if (rc) return rc;
@@ -1835,6 +1844,7 @@ const char *fl_bench_kernel_name(fl_ctx *ctx, int which) {
     case 3: return "k_mvs";
     case 4: return "k_mvs";
     case 5: return ctx->kv_format == FL_KV_F32 ? "k_attn" : "k_attm";
+    case 6: case 7: case 8: case 9: return ctx->layer_fmt == FL_Q4K ? "k_vgemm_q4k" : "k_vgemm_q8_0";
     }
     return "";
 }

@@ -14,8 +14,13 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
         if (a.W.cols % 256) return hipErrorInvalidValue;
         const int nsb = a.W.cols >> 8;
         kn = (size_t)((nsb + a.ksplit - 1) / a.ksplit) * 256;
-        const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
-        hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);
+        if (a.M <= 8) {
+            // activations of 8 token rows, then 8 (scale, sum) pairs per block
+            hipLaunchKernelGGL(k_vgemm_q4k8, grid, dim3(256), 8 * kn + 8 * (kn / 32) * 8, st, a);
+        } else {
+            const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+            hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);
+        }
     } else {
         if (fmt != F_Q8_0) return hipErrorNotSupported;
         const int nb = a.W.cols >> 5;

@@ -18,16 +18,47 @@ namespace fl {
 
 // LDS staging of one K chunk: int8 activations of the M tokens, then
 // (scale, block sum as float) pairs.
-template <int FMT>
+// Every load of a round goes out before the first LDS store, so a round
+// costs one L2 round trip.
+// T8: (scale, sum) pairs block-major, 8 tokens per block ([b][8]); else
+// token-major ([t][nb]).
+template <int FMT, bool T8 = false>
 __device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t *lx, float2 *lsc) {
+    constexpr int U = 8;
     const int K = a.W.cols, nb = kn >> 5, b0 = k0 >> 5;
-    for (int i = threadIdx.x; i < a.M * (kn >> 3); i += blockDim.x) {
-        const int t = i / (kn >> 3), o = (i % (kn >> 3)) * 8;
-        *(i64x1_t *)(lx + t * kn + o) = *(const i64x1_t *)(a.xq + (size_t)t * K + k0 + o);
+    const int nx = a.M * (kn >> 3), ns = a.M * nb;
+    for (int base = threadIdx.x; base < nx; base += U * blockDim.x) {
+        i64x1_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * blockDim.x;
+            const int t = i / (kn >> 3), o = (i % (kn >> 3)) * 8;
+            if (i < nx) v[u] = *(const i64x1_t *)(a.xq + (size_t)t * K + k0 + o);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * blockDim.x;
+            const int t = i / (kn >> 3), o = (i % (kn >> 3)) * 8;
+            if (i < nx) *(i64x1_t *)(lx + t * kn + o) = v[u];
+        }
     }
-    for (int i = threadIdx.x; i < a.M * nb; i += blockDim.x) {
-        const int t = i / nb, b = i % nb;
-        lsc[t * nb + b] = make_float2(a.xs[(size_t)t * (K >> 5) + b0 + b], (float)a.xsum[(size_t)t * (K >> 5) + b0 + b]);
+    for (int base = threadIdx.x; base < ns; base += 4 * blockDim.x) {
+        float sv[4];
+        int mv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * blockDim.x;
+            const int t = i / nb, b = i % nb;
+            if (i < ns) {
+                sv[u] = a.xs[(size_t)t * (K >> 5) + b0 + b];
+                mv[u] = a.xsum[(size_t)t * (K >> 5) + b0 + b];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * blockDim.x;
+            if (i < ns) lsc[T8 ? (i % nb) * 8 + i / nb : i] = make_float2(sv[u], (float)mv[u]);
+        }
     }
     __syncthreads();
 }
@@ -105,9 +136,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     const int kn = (s1 - s0) * 256, nbc = kn >> 5;
     int8_t *lx = (int8_t *)smem;
     float2 *lsc = (float2 *)(smem + ((kVerifyMaxTokens * kn + 15) & ~15));
-    vg_stage<F_Q4K>(a, s0 * 256, kn, lx, lsc);
     const int tile = blockIdx.x * 4 + wave;
-    if (tile * 16 >= W.rows) return;
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
     const int row = min(n, W.rows - 1);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -121,6 +150,8 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     i64x1_t wn[4];
     v4i_t hn;
     load(s0, wn, hn);
+    vg_stage<F_Q4K>(a, s0 * 256, kn, lx, lsc);
+    if (tile * 16 >= W.rows) return;
     for (int sb = s0; sb < s1; sb++) {
         i64x1_t w[4];
         const v4i_t h = hn;
@@ -159,6 +190,93 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
         for (int i = 0; i < 4; i++) {
             const int t = 4 * kg + i;
             if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[i];
+        }
+    }
+}
+
+// Q4_K, M <= 8 tokens.  Sub-blocks j and j+4 are the low and high nibbles
+// of the same 32 qs bytes, so one pair of accumulating MFMAs forms both:
+// token slots 0-7 carry sub-block j's activations in k 0-15 of each MFMA
+// (zeros in k 16-31), slots 8-15 sub-block j+4's in k 16-31; the weight
+// lanes of k 0-15 hold the low nibbles, those of k 16-31 the high ones.  Lane
+// (n, kg) loads 16 qs bytes at 16*(kg&1): the first MFMA takes bytes 0-7, the
+// second 8-15.  Every output slot is then a live (token, sub-block) term, so
+// the per-block fp32 work per MFMA halves against k_vgemm_q4k.
+__global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const WDesc &W = a.W;
+    const int K = W.cols, nsb = K >> 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = (nsb + a.ksplit - 1) / a.ksplit;
+    const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
+    if (s0 >= s1) return;
+    const int kn = (s1 - s0) * 256;
+    int8_t *lx = (int8_t *)smem;
+    float2 *lsc = (float2 *)(smem + 8 * kn);
+    const int tile = blockIdx.x * 4 + wave;
+    const bool live = tile * 16 < W.rows;  // wave-uniform
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int h = kg & 1, hi = kg >> 1;     // weight lane: byte half, nibble (sub-block j + 4*hi)
+    const int tx = tA & 7, xhi = tA >> 3;   // activation lane: token tx of sub-block j + 4*xhi
+    const bool xon = xhi == hi && tx < a.M;
+    const int row = min(n, W.rows - 1);
+    const uint8_t *qs = W.q + (size_t)row * nsb * 128 + 16 * h;
+    const uint8_t *hd = W.h + (size_t)row * nsb * 16;
+    v4i_t wn[4], hn;
+    auto load = [&](int sb) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) wn[p] = *(const v4i_t *)(qs + (size_t)sb * 128 + 32 * p);
+        hn = *(const v4i_t *)(hd + (size_t)sb * 16);
+    };
+    if (live) load(s0);
+    vg_stage<F_Q4K, true>(a, s0 * 256, kn, lx, lsc);
+    if (!live) return;
+    const int sh = 4 * hi;
+    const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
+    const int8_t *xo = lx + tx * kn + 16 * h + 128 * xhi;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sb = s0; sb < s1; sb++) {
+        v4i_t w[4];
+        const v4i_t hh = hn;
+#pragma unroll
+        for (int p = 0; p < 4; p++) w[p] = wn[p];
+        if (sb + 1 < s1) load(sb + 1);
+        const int sl = sb - s0;
+        v4i32_t dd[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const v4i_t xv = xon ? *(const v4i_t *)(xo + sl * 256 + 32 * p) : v4i_t{0, 0, 0, 0};
+            const i64x1_t w1 = ((((i64x1_t)(uint32_t)w[p].y << 32) | (uint32_t)w[p].x) >> sh) & m4;
+            const i64x1_t w2 = ((((i64x1_t)(uint32_t)w[p].w << 32) | (uint32_t)w[p].z) >> sh) & m4;
+            const i64x1_t x1 = ((i64x1_t)(uint32_t)xv.y << 32) | (uint32_t)xv.x;
+            const i64x1_t x2 = ((i64x1_t)(uint32_t)xv.w << 32) | (uint32_t)xv.z;
+            dd[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x2, w2, vg_mfma(x1, w1), 0, 0, 0);
+        }
+        const uint32_t h0 = (uint32_t)hh.x;
+        const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            // unpack_q4k_scales (model.rs:8709-8719), flare packing, sub-block p + 4*hi
+            const uint32_t sa = byte_of((uint32_t)hh.y, p), sbb = byte_of((uint32_t)hh.z, p),
+                           scc = byte_of((uint32_t)hh.w, p);
+            const uint32_t sc = hi ? ((sa >> 6) | ((scc & 0xF) << 2)) : (sa & 63);
+            const uint32_t mn = hi ? ((sbb >> 6) | ((scc >> 4) << 2)) : (sbb & 63);
+            const float dsc = d * (float)sc, dmn = dmin * (float)mn;
+            const float4 *ls = (const float4 *)(lsc + (sl * 8 + p + 4 * hi) * 8 + 4 * h);
+            const float4 l0 = ls[0], l1 = ls[1];
+            const float xs[4] = {l0.x, l0.z, l1.x, l1.z}, xm[4] = {l0.y, l0.w, l1.y, l1.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] += xs[e] * (dsc * (float)dd[p][e] - dmn * xm[e]);
+        }
+    }
+    // lanes kg and kg+2 hold sub-blocks 0-3 and 4-7 of the same outputs
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] += __shfl_xor(acc[e], 32, 64);
+    if (n < W.rows && hi == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 4 * h + e;
+            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[e];
         }
     }
 }

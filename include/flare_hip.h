@@ -237,8 +237,9 @@ int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out);
 
 /* ---- measurement helpers ---------------------------------------------------- */
 /* Enqueue `iters` launches of one decode kernel for `which` (0=qkv, 1=wo,
- * 2=gate_up, 3=down, 4=output argmax, 5=attention at the current position)
- * on the context stream, launch i using layer (first_layer + i) % num_layers,
+ * 2=gate_up, 3=down, 4=output argmax, 5=attention at the current position;
+ * 6..9 = the verify GEMM of qkv / wo / gate_up / down for 8 tokens, over the
+ * verify activation buffers) on the context stream, launch i using layer (first_layer + i) % num_layers,
  * reading the model's live activation buffers.  Writes the algorithmic HBM
  * bytes of one launch (GGUF weight bytes; K+V bytes for attention) to
  * *bytes_per_launch.  No counterpart in the reference: measurement only. */
