@@ -1508,7 +1508,8 @@ static int verify_alloc(fl_ctx *ctx) {
 static int verify_ksplit(const fl_weight &w) {
     const int tiles = (w.rows + 15) / 16;
     const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
-    const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (2048 + tiles - 1) / tiles}));
+    static const int target = getenv("FLARE_VG_WAVES") ? atoi(getenv("FLARE_VG_WAVES")) : 2048;  // tuning
+    const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (target + tiles - 1) / tiles}));
     // every chunk non-empty: the reducers sum all ksplit partial sets
     const int chunk = (units + want - 1) / want;
     return (units + chunk - 1) / chunk;

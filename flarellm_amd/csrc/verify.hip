@@ -16,7 +16,10 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
         kn = (size_t)((nsb + a.ksplit - 1) / a.ksplit) * 256;
         if (a.M <= 8) {
             // activations of 8 token rows, then 8 (scale, sum) pairs per block
-            hipLaunchKernelGGL(k_vgemm_q4k8, grid, dim3(256), 8 * kn + 8 * (kn / 32) * 8, st, a);
+            // one super-block in flight per wave: 2 or 3 measured slower on
+            // MI355X (Llama-3-8B shapes; VGPRs 112 / 132 against 85)
+            const size_t lds = 8 * (kn + 32) + 8 * (kn / 32) * 8;
+            hipLaunchKernelGGL(k_vgemm_q4k8<1>, grid, dim3(256), lds, st, a);
         } else {
             const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
             hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);

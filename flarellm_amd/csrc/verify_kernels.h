@@ -23,7 +23,8 @@ namespace fl {
 // T8: (scale, sum) pairs block-major, 8 tokens per block ([b][8]); else
 // token-major ([t][nb]).
 template <int FMT, bool T8 = false>
-__device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t *lx, float2 *lsc) {
+__device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t *lx, float2 *lsc, int xs = 0) {
+    if (!xs) xs = kn;  // LDS row stride of the activations
     constexpr int U = 8;
     const int K = a.W.cols, nb = kn >> 5, b0 = k0 >> 5;
     const int nx = a.M * (kn >> 3), ns = a.M * nb;
@@ -39,7 +40,7 @@ __device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t
         for (int u = 0; u < U; u++) {
             const int i = base + u * blockDim.x;
             const int t = i / (kn >> 3), o = (i % (kn >> 3)) * 8;
-            if (i < nx) *(i64x1_t *)(lx + t * kn + o) = v[u];
+            if (i < nx) *(i64x1_t *)(lx + t * xs + o) = v[u];
         }
     }
     for (int base = threadIdx.x; base < ns; base += 4 * blockDim.x) {
@@ -202,6 +203,8 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
 // (n, kg) loads 16 qs bytes at 16*(kg&1): the first MFMA takes bytes 0-7, the
 // second 8-15.  Every output slot is then a live (token, sub-block) term, so
 // the per-block fp32 work per MFMA halves against k_vgemm_q4k.
+// PD super-blocks of weights in flight per wave.
+template <int PD>
 __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
@@ -211,8 +214,11 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
     if (s0 >= s1) return;
     const int kn = (s1 - s0) * 256;
+    // activation rows kn + 32 bytes apart: the 16-byte reads of the 8 token
+    // rows land on distinct LDS banks
+    const int xst = kn + 32;
     int8_t *lx = (int8_t *)smem;
-    float2 *lsc = (float2 *)(smem + 8 * kn);
+    float2 *lsc = (float2 *)(smem + 8 * xst);
     const int tile = blockIdx.x * 4 + wave;
     const bool live = tile * 16 < W.rows;  // wave-uniform
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
@@ -222,25 +228,32 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     const int row = min(n, W.rows - 1);
     const uint8_t *qs = W.q + (size_t)row * nsb * 128 + 16 * h;
     const uint8_t *hd = W.h + (size_t)row * nsb * 16;
-    v4i_t wn[4], hn;
-    auto load = [&](int sb) {
+    v4i_t wb[PD][4], hb[PD];
+    auto load = [&](int u, int sb) {
 #pragma unroll
-        for (int p = 0; p < 4; p++) wn[p] = *(const v4i_t *)(qs + (size_t)sb * 128 + 32 * p);
-        hn = *(const v4i_t *)(hd + (size_t)sb * 16);
+        for (int p = 0; p < 4; p++) wb[u][p] = *(const v4i_t *)(qs + (size_t)sb * 128 + 32 * p);
+        hb[u] = *(const v4i_t *)(hd + (size_t)sb * 16);
     };
-    if (live) load(s0);
-    vg_stage<F_Q4K, true>(a, s0 * 256, kn, lx, lsc);
+    if (live) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) load(u, min(s0 + u, s1 - 1));
+    }
+    vg_stage<F_Q4K, true>(a, s0 * 256, kn, lx, lsc, xst);
     if (!live) return;
     const int sh = 4 * hi;
     const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
-    const int8_t *xo = lx + tx * kn + 16 * h + 128 * xhi;
+    const int8_t *xo = lx + tx * xst + 16 * h + 128 * xhi;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sb = s0; sb < s1; sb++) {
-        v4i_t w[4];
-        const v4i_t hh = hn;
+    for (int sb0 = s0; sb0 < s1; sb0 += PD)
 #pragma unroll
-        for (int p = 0; p < 4; p++) w[p] = wn[p];
-        if (sb + 1 < s1) load(sb + 1);
+    for (int u = 0; u < PD; u++) {
+        const int sb = sb0 + u;
+        if (sb >= s1) break;
+        v4i_t w[4];
+        const v4i_t hh = hb[u];
+#pragma unroll
+        for (int p = 0; p < 4; p++) w[p] = wb[u][p];
+        if (sb + PD < s1) load(u, sb + PD);
         const int sl = sb - s0;
         v4i32_t dd[4];
 #pragma unroll
@@ -254,14 +267,15 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
         }
         const uint32_t h0 = (uint32_t)hh.x;
         const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+        // unpack_q4k_scales (model.rs:8709-8719), flare packing: the 6-bit
+        // scale / min of sub-block p + 4*hi in byte p, all four at once
+        const uint32_t sa = (uint32_t)hh.y, sbb = (uint32_t)hh.z, scc = (uint32_t)hh.w;
+        const uint32_t scw = hi ? (((sa >> 6) & 0x03030303u) | ((scc & 0x0F0F0F0Fu) << 2)) : (sa & 0x3F3F3F3Fu);
+        const uint32_t mnw =
+            hi ? (((sbb >> 6) & 0x03030303u) | (((scc >> 4) & 0x0F0F0F0Fu) << 2)) : (sbb & 0x3F3F3F3Fu);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            // unpack_q4k_scales (model.rs:8709-8719), flare packing, sub-block p + 4*hi
-            const uint32_t sa = byte_of((uint32_t)hh.y, p), sbb = byte_of((uint32_t)hh.z, p),
-                           scc = byte_of((uint32_t)hh.w, p);
-            const uint32_t sc = hi ? ((sa >> 6) | ((scc & 0xF) << 2)) : (sa & 63);
-            const uint32_t mn = hi ? ((sbb >> 6) | ((scc >> 4) << 2)) : (sbb & 63);
-            const float dsc = d * (float)sc, dmn = dmin * (float)mn;
+            const float dsc = d * (float)byte_of(scw, p), dmn = dmin * (float)byte_of(mnw, p);
             const float4 *ls = (const float4 *)(lsc + (sl * 8 + p + 4 * hi) * 8 + 4 * h);
             const float4 l0 = ls[0], l1 = ls[1];
             const float xs[4] = {l0.x, l0.z, l1.x, l1.z}, xm[4] = {l0.y, l0.w, l1.y, l1.w};
