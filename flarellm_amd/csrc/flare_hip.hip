@@ -1615,7 +1615,10 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         a.q = ctx->vq;
         a.posp = ctx->vpos;
         a.nsplit = ctx->nsplit;
-        a.chmin = ctx->chmin;
+        // M queries: chunks M times the decode minimum, so the launch keeps
+        // about the decode step's workgroup count (Llama-3-8B, 8 queries at
+        // 4k on MI355X: 33 vs 40 us per layer; one split per query: 47 us)
+        a.chmin = ctx->chmin * M;
         a.single = ctx->single;
         a.waves = ctx->attn_waves;
         a.part = ctx->d_part;
