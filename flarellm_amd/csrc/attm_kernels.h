@@ -212,13 +212,15 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 
     AttnArgs a = a0;
     const int zq = (int)blockIdx.z;
+    const bool qpair = a.qpair != 0;
+    const int z0 = qpair ? 2 * zq : zq;  // first query of this workgroup
     if (zq) {
-        a.q += (size_t)zq * a.qstride;
-        if (a.out) a.out += (size_t)zq * a.ostride;
+        a.q += (size_t)z0 * a.qstride;
+        if (a.out) a.out += (size_t)z0 * a.ostride;
         if (a.oq) {
-            a.oq += (size_t)zq * a.ostride;
-            a.os += (size_t)zq * (a.ostride / 32);
-            a.osum += (size_t)zq * (a.ostride / 32);
+            a.oq += (size_t)z0 * a.ostride;
+            a.os += (size_t)z0 * (a.ostride / 32);
+            a.osum += (size_t)z0 * (a.ostride / 32);
         }
         a.part += (size_t)zq * a.nkv * a.nsplit * G * (D + 2);
         a.counters += (size_t)zq * a.nkv;
@@ -240,14 +242,28 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     v4f_t qv[DT][2];
     {
         const int g = min(r >> 1, G - 1);
-        const v4f_t *qp = (const v4f_t *)(a.q + (size_t)(kvh * G + g) * D + 8 * kg);
+        // query pairs: rows g >= G/2 are the second query's heads
+        constexpr int GH = G / 2 > 0 ? G / 2 : 1;
+        const size_t qo = !qpair ? (size_t)(kvh * G + g) * D
+                                 : (g >= GH ? (size_t)a.qstride : 0) + (size_t)(kvh * GH + g % GH) * D;
+        const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
             qv[dt][0] = qp[8 * dt];
             qv[dt][1] = qp[8 * dt + 1];
         }
     }
-    const int pos = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + zq, T = pos + 1;
+    const int pos = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + (qpair ? z0 + 1 : zq),
+              T = pos + 1;
+    // query pairs: the first query's heads (rows < G/2) stop before slot pos
+    const int lastA0 = (qpair && 2 * kg < G / 2) ? pos : INT_MAX;
+    const int lastA1 = (qpair && 2 * kg + 1 < G / 2) ? pos : INT_MAX;
+    // element i of this kv head's G*D outputs -> offset from a.out / a.oq
+    auto oix = [&](int i) -> size_t {
+        if (!qpair) return (size_t)kvh * G * D + i;
+        constexpr int HD = (G / 2) * D;
+        return (i >= HD ? (size_t)a.ostride + (i - HD) : (size_t)i) + (size_t)kvh * HD;
+    };
     // up to a.single tokens: one split (no cross-workgroup merge);
     // beyond: chunks of at least chmin slots over the nsplit workgroups
     int CH = T <= a.single ? T : max(a.chmin, (T + a.nsplit - 1) / a.nsplit);
@@ -465,8 +481,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             }
             const int t = tb + 16 * h + r;
             const bool ok = t < t1;
-            sc[h][0] = ok ? (acc[0] + acc[1] + kbh[0]) * scale : -INFINITY;
-            sc[h][1] = ok ? (acc[2] + acc[3] + kbh[1]) * scale : -INFINITY;
+            sc[h][0] = ok && t != lastA0 ? (acc[0] + acc[1] + kbh[0]) * scale : -INFINITY;
+            sc[h][1] = ok && t != lastA1 ? (acc[2] + acc[3] + kbh[1]) * scale : -INFINITY;
         }
         if (bi == wave) ATTN_TS(2);
         // ---- online softmax per head (rows of 16 lanes hold one head pair) --
@@ -686,7 +702,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             if (i < G * D) {
                 const float v = res[k] * (1.0f / Lx[i / D]);
                 mo[i] = v;
-                if (a.out) a.out[(size_t)kvh * G * D + i] = v;
+                if (a.out) a.out[oix(i)] = v;
             }
         }
     } else {
@@ -774,7 +790,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             if (i < G * D) {
                 const float v = O[k];
                 mo[i] = v;
-                if (a.out) a.out[(size_t)kvh * G * D + i] = v;
+                if (a.out) a.out[oix(i)] = v;
             }
         }
         if (tid == 0) __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -786,8 +802,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         // Q8_0 copy of this kv head's G*D outputs (quantize_input_q8_0_into), 32 lanes per block
         const int nb = G * D / 32;
         for (int b = tid >> 5; b < nb; b += NTH / 32) {
-            const int gb = kvh * nb + b;
-            quant_block32_lanes(mo[b * 32 + (tid & 31)], a.oq + gb * 32, a.os + gb, a.osum + gb);
+            const size_t e0 = oix(b * 32);
+            quant_block32_lanes(mo[b * 32 + (tid & 31)], a.oq + e0, a.os + e0 / 32, a.osum + e0 / 32);
         }
     }
     if (nact > 1) ATTN_TSL(9);

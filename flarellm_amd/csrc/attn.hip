@@ -36,6 +36,14 @@ static hipError_t launch_attm_t(int D, int G, hipStream_t st, const AttnArgs &a,
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
     if (nq < 1) return hipErrorInvalidValue;
     if (nq > 1 && a.knew) return hipErrorInvalidValue;  // new-token stores are single-query
+    if (a.qpair) {
+        // query pairs: fp16 / Q8 MFMA kernel, even query count, 2G <= 8
+        if (nq % 2 || !(G == 1 || G == 2 || G == 4) || !((kvfmt == KV_F16 && a.v_tblk) || kvfmt == KV_Q8))
+            return hipErrorInvalidValue;
+        if (a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32) return hipErrorInvalidValue;
+        if (kvfmt == KV_F16) return launch_attm_t<__half>(D, 2 * G, st, a, nq / 2);
+        return launch_attm_t<KvQ8>(D, 2 * G, st, a, nq / 2);
+    }
     // model caches in fp16 / Q8 (V in transposed blocks): the MFMA kernel
     if ((kvfmt == KV_F16 && a.v_tblk) || kvfmt == KV_Q8 || kvfmt == KV_KIVI) {
         if ((kvfmt != KV_KIVI && !a.v_tblk) || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32)

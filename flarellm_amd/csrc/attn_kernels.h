@@ -48,6 +48,10 @@ struct AttnArgs {
     // partials and counters have one set per query.
     int qstride, ostride;
     int v_tblk;  // F16 / Q8 model caches: V stored in 32-slot transposed blocks [slot/32][D][32]
+    // MFMA kernel, several queries: grid z = query pairs; the model's G/2
+    // query heads of queries 2z and 2z+1 (kernel G = 2 x the model's) share
+    // each K/V block, query 2z masking slot *posp + 2z + 1
+    int qpair;
 };
 
 // Offset of (slot t, channel d) in one kv head's transposed V store.

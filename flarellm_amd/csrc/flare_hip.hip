@@ -1615,10 +1615,14 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         a.q = ctx->vq;
         a.posp = ctx->vpos;
         a.nsplit = ctx->nsplit;
-        // M queries: chunks M times the decode minimum, so the launch keeps
-        // about the decode step's workgroup count (Llama-3-8B, 8 queries at
+        // M queries (M/2 pairs): chunks M (M/2) times the decode minimum, so
+        // the launch keeps about the decode step's workgroup count (Llama-3-8B, 8 queries at
         // 4k on MI355X: 33 vs 40 us per layer; one split per query: 47 us)
-        a.chmin = ctx->chmin * M;
+        // query pairs share each K/V block (fp16 / Q8, G <= 4, even M)
+        static const bool no_pair = getenv("FLARE_NO_QPAIR") != nullptr;  // measurement switch
+        a.qpair = !no_pair && M % 2 == 0 && (G == 1 || G == 2 || G == 4) &&
+                  (ctx->kv_format == FL_KV_F16 || ctx->kv_format == FL_KV_Q8);
+        a.chmin = ctx->chmin * (a.qpair ? M / 2 : M);
         a.single = ctx->single;
         a.waves = ctx->attn_waves;
         a.part = ctx->d_part;
