@@ -1617,7 +1617,8 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         a.nsplit = ctx->nsplit;
         // M queries (M/2 pairs): chunks M (M/2) times the decode minimum, so
         // the launch keeps about the decode step's workgroup count (Llama-3-8B, 8 queries at
-        // 4k on MI355X: 33 vs 40 us per layer; one split per query: 47 us)
+        // 4k on MI355X, unpaired: 33 vs 40 us per layer, one split per query 47 us;
+        // paired: M/2 measured best against 1, 2, 6 and 8)
         // query pairs share each K/V block (fp16 / Q8, G <= 4, even M)
         static const bool no_pair = getenv("FLARE_NO_QPAIR") != nullptr;  // measurement switch
         a.qpair = !no_pair && M % 2 == 0 && (G == 1 || G == 2 || G == 4) &&

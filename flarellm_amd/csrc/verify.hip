@@ -46,7 +46,7 @@ hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *to
 
 hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, float *x,
                             const float *w, float eps, int8_t *q, float *s, int *sum) {
-    if (H % 32 || M < 1) return hipErrorInvalidValue;
+    if (H % 32 || H > kResnormMaxH || M < 1) return hipErrorInvalidValue;
     if (pro == PRO_NORMQ0)
         hipLaunchKernelGGL(k_v_resnorm<PRO_NORMQ0>, dim3(M), dim3(kResnormThreads), 0, st, part, ksplit, M, H, x, w,
                            eps, q, s, sum);

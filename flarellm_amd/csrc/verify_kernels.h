@@ -374,8 +374,11 @@ __global__ __launch_bounds__(256) void k_v_store(const float *part, int ksplit, 
 // part == nullptr: none), then the decode prologue's arithmetic on the
 // updated row (rmsnorm_quantize_q8_0 / rmsnorm_into + quantize, model.rs:
 // 5581-5640 / 7456-7477).  Thread i holds elements 4i..4i+3 of every
-// 4096-element chunk, so 8 lanes form one 32-block.
+// 4096-element chunk in registers (H <= kResnormMaxH), so 8 lanes form one
+// 32-block; the norm weights load before the reduction.
 constexpr int kResnormThreads = 1024;
+constexpr int kResnormChunks = 4;
+constexpr int kResnormMaxH = 4 * kResnormThreads * kResnormChunks;
 template <int PRO>
 __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part, int ksplit, int M, int H, float *x,
                                                                 const float *w, float eps, int8_t *q, float *s,
@@ -383,25 +386,32 @@ __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part
     __shared__ float red[kResnormThreads / 64];
     const int t = blockIdx.x, tid = threadIdx.x;
     float *xt = x + (size_t)t * H;
+    float4 v[kResnormChunks], wv[kResnormChunks];
     float ss = 0.0f;
-    for (int e = 4 * tid; e < H; e += 4 * kResnormThreads) {
-        float4 v = *(const float4 *)(xt + e);
-        if (part) {
-            float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int k = 0; k < ksplit; k++) {
-                const float4 pk = *(const float4 *)(part + ((size_t)k * M + t) * H + e);
-                p.x += pk.x;
-                p.y += pk.y;
-                p.z += pk.z;
-                p.w += pk.w;
+#pragma unroll
+    for (int c = 0; c < kResnormChunks; c++) {
+        const int e = 4 * (tid + c * kResnormThreads);
+        v[c] = wv[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (e < H) {
+            v[c] = *(const float4 *)(xt + e);
+            wv[c] = *(const float4 *)(w + e);
+            if (part) {
+                float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int k = 0; k < ksplit; k++) {
+                    const float4 pk = *(const float4 *)(part + ((size_t)k * M + t) * H + e);
+                    p.x += pk.x;
+                    p.y += pk.y;
+                    p.z += pk.z;
+                    p.w += pk.w;
+                }
+                v[c].x += p.x;
+                v[c].y += p.y;
+                v[c].z += p.z;
+                v[c].w += p.w;
+                *(float4 *)(xt + e) = v[c];
             }
-            v.x += p.x;
-            v.y += p.y;
-            v.z += p.z;
-            v.w += p.w;
-            *(float4 *)(xt + e) = v;
         }
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
     }
     ss = wave_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -410,12 +420,12 @@ __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part
 #pragma unroll
     for (int i = 0; i < kResnormThreads / 64; i++) ss += red[i];
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int e0 = 0; e0 < H; e0 += 4 * kResnormThreads) {  // uniform trip count (shuffles below)
-        const int e = e0 + 4 * tid;
+#pragma unroll
+    for (int c = 0; c < kResnormChunks; c++) {
+        const int e = 4 * (tid + c * kResnormThreads);
+        if (c * 4 * kResnormThreads >= H) break;  // uniform: shuffles below
         const bool in = e < H;  // H % 32 == 0: a 32-block is wholly in or out
-        float4 v = in ? *(const float4 *)(xt + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float4 wv = in ? *(const float4 *)(w + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float y[4] = {v.x, v.y, v.z, v.w}, wi[4] = {wv.x, wv.y, wv.z, wv.w};
+        float y[4] = {v[c].x, v[c].y, v[c].z, v[c].w}, wi[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
         float amax = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -427,21 +437,21 @@ __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part
         const float d = amax / 127.0f;
         const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
         int cs = 0;
-        char4 c;
         int8_t qq[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             qq[j] = sat_i8(roundf(y[j] * id));
             cs += qq[j];
         }
-        c.x = qq[0];
-        c.y = qq[1];
-        c.z = qq[2];
-        c.w = qq[3];
+        char4 cq;
+        cq.x = qq[0];
+        cq.y = qq[1];
+        cq.z = qq[2];
+        cq.w = qq[3];
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) cs += __shfl_xor(cs, o, 64);
         if (in) {
-            *(char4 *)(q + (size_t)t * H + e) = c;
+            *(char4 *)(q + (size_t)t * H + e) = cq;
             if ((tid & 7) == 0) {
                 s[(size_t)t * (H >> 5) + (e >> 5)] = d;
                 sum[(size_t)t * (H >> 5) + (e >> 5)] = cs;
