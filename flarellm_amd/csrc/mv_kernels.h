@@ -288,14 +288,14 @@ __device__ __forceinline__ void store_rows(const float *acc, int row0, int rows,
     }
 }
 
-// Lane r's row of a finished group (every lane holds all R sums): a chain of
-// selects rather than a dynamically indexed private array.
+// Lane r's row of a finished group (every lane holds all R sums), formed by
+// adding masked terms: a select chain here was turned back into a private
+// array indexed by the lane (scratch stores on every group).
 template <int R>
 __device__ __forceinline__ float lane_row(const float *acc, int gl) {
-    float v = acc[0];
+    float v = 0.0f;
 #pragma unroll
-    for (int r = 1; r < R; r++)
-        if (gl == r) v = acc[r];
+    for (int r = 0; r < R; r++) v += gl == r ? acc[r] : 0.0f;
     return v;
 }
 
@@ -365,14 +365,21 @@ template <int R>
 __device__ __forceinline__ void store_qkv(const float *acc, int row0, int rows, int gl, const QkvEpi &e, int pos,
                                           float *q, bool pre_ok, float pc, float ps) {
     static_assert(R % 2 == 0, "EPI_QKV needs row pairs");
+    // lane p < R/2 stores pair p: select its two rows first (constant
+    // indices only), then one store path
+    float x0 = acc[0], x1 = acc[1];
 #pragma unroll
-    for (int p = 0; p < R / 2; p++)
-        if (gl == p && row0 + 2 * p < rows) {
-            const int n = row0 + 2 * p;
-            float c = pc, sn = ps;
-            if (!pre_ok && n < e.nq + e.nk) qkv_rope_cs(e, n, c, sn);
-            store_qkv_pair(acc[2 * p], acc[2 * p + 1], n, e, pos, q, c, sn);
+    for (int p = 1; p < R / 2; p++)
+        if (gl == p) {
+            x0 = acc[2 * p];
+            x1 = acc[2 * p + 1];
         }
+    if (gl < R / 2 && row0 + 2 * gl < rows) {
+        const int n = row0 + 2 * gl;
+        float c = pc, sn = ps;
+        if (!pre_ok && n < e.nq + e.nk) qkv_rope_cs(e, n, c, sn);
+        store_qkv_pair(x0, x1, n, e, pos, q, c, sn);
+    }
 }
 
 }  // namespace fl
