@@ -277,9 +277,10 @@ struct fl_ctx {
     // speculative verify buffers (allocated on first fl_verify)
     bool have_verify = false;
     float *vx = nullptr, *vx2 = nullptr, *vq = nullptr, *vk = nullptr, *vv = nullptr, *vpart = nullptr;
-    int8_t *vxq = nullptr, *vaq = nullptr;
-    float *vxs = nullptr, *vas = nullptr;
-    int *vxsum = nullptr, *vasum = nullptr;
+    int8_t *vxq = nullptr, *vaq = nullptr, *vhq = nullptr;  // vhq: Q8_0 of the hidden vector (fused SiLU)
+    float *vxs = nullptr, *vas = nullptr, *vhs = nullptr;
+    int *vxsum = nullptr, *vasum = nullptr, *vhsum = nullptr;
+    int *vcnt = nullptr;  // arrival counters of the fused verify GEMM epilogues
     int *vtok = nullptr, *vpos = nullptr;
     unsigned long long *vslots = nullptr;
     size_t vpart_floats = 0;
@@ -653,11 +654,12 @@ static void model_release(fl_ctx *c) {
     c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->rope_cur = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
     void *vp[] = {c->vx, c->vx2, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
-                  c->vtok, c->vpos, c->vslots};
+                  c->vtok, c->vpos, c->vslots, c->vhq, c->vhs, c->vhsum, c->vcnt};
     for (void *p : vp)
         if (p) (void)hipFree(p);
     c->vx = c->vx2 = c->vq = c->vk = c->vv = c->vpart = nullptr; c->vxq = c->vaq = nullptr; c->vxs = c->vas = nullptr;
     c->vxsum = c->vasum = nullptr; c->vtok = c->vpos = nullptr; c->vslots = nullptr; c->vpart_floats = 0;
+    c->vhq = nullptr; c->vhs = nullptr; c->vhsum = c->vcnt = nullptr;
     c->have_verify = false;
     c->have_cfg = c->have_weights = false;
 }
@@ -1475,6 +1477,7 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
 // ---- speculative verify -------------------------------------------------------
 
 constexpr int kVerifyMaxKsplit = 16;
+constexpr int kVerifyCounters = 4096;  // workgroup columns of a fused verify GEMM
 
 static int verify_alloc(fl_ctx *ctx) {
     if (ctx->have_verify) return 0;
@@ -1499,6 +1502,11 @@ static int verify_alloc(fl_ctx *ctx) {
     ALLOC(ctx, ctx->vtok, M * 4);
     ALLOC(ctx, ctx->vpos, 4);
     ALLOC(ctx, ctx->vslots, M * 8);
+    ALLOC(ctx, ctx->vhq, M * F);
+    ALLOC(ctx, ctx->vhs, M * (F / 32) * 4);
+    ALLOC(ctx, ctx->vhsum, M * (F / 32) * 4);
+    ALLOC(ctx, ctx->vcnt, kVerifyCounters * 4);
+    HIPCHK(ctx, hipMemset(ctx->vcnt, 0, kVerifyCounters * 4));  // the kernels leave them at zero
     ctx->have_verify = true;
     return 0;
 }
@@ -1516,8 +1524,9 @@ static int verify_ksplit(const fl_weight &w) {
 }
 
 static int verify_gemm(fl_ctx *ctx, const fl_weight &w, int M, const int8_t *xq, const float *xs, const int *xsum,
-                       int &ksplit) {
+                       int &ksplit, const VgArgs *post = nullptr) {
     VgArgs a{};
+    if (post) a = *post;  // fused epilogue fields
     a.W = w.desc();
     a.xq = xq;
     a.xs = xs;
@@ -1589,6 +1598,10 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
     hipStream_t st = ctx->stream;
     float *xa = ctx->vx;
     HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, xa));
+    // Q4_K layers, up to 8 tokens: the QKV post and SiLU run inside the GEMMs
+    static const bool no_fuse = getenv("FLARE_NO_VFUSE") != nullptr;  // measurement switch
+    const bool fuse = !no_fuse && ctx->layer_fmt == FL_Q4K && M <= 8 &&
+                      std::max(qd + 2 * kvd, 2 * F) / 64 <= kVerifyCounters;
     int ks_down = 0;
     for (int l = 0; l < c.num_layers; l++) {
         Layer &L = ctx->layers[l];
@@ -1599,16 +1612,36 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         // norm only), one workgroup per token
         HIPCHK(ctx, launch_v_resnorm(pro, st, l ? ctx->vpart : nullptr, ks_down, M, H, xa, L.attn_norm, eps, ctx->vxq,
                                      ctx->vxs, ctx->vxsum));
-        rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
-        if (rc) return rc;
         AttnArgs a{};
         kv_layer_args(ctx, l, a);
-        // F16 / F32 caches: RoPE'd K and V go straight into the cache slots
+        // RoPE'd q; K and V straight into F16 / F32 cache slots, else staged
         const bool plain = ctx->kv_format == FL_KV_F16 || ctx->kv_format == FL_KV_F32;
-        const KvDst kd{const_cast<void *>(a.kc), const_cast<void *>(a.vc), a.head_stride, a.v_tblk};
-        HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, qd, kvd, D, ctx->rope,
-                                      (long long)c.max_seq_len * (D / 2), ctx->vpos, ctx->vq, ctx->vk, ctx->vv,
-                                      ctx->kv_format, kd));
+        VgArgs pq{};
+        pq.qp.nq = qd;
+        pq.qp.nk = kvd;
+        pq.qp.D = D;
+        pq.qp.rope = ctx->rope;
+        pq.qp.sin_off = (long long)c.max_seq_len * (D / 2);
+        pq.qp.pos0p = ctx->vpos;
+        pq.qp.Q = ctx->vq;
+        pq.qp.Kst = ctx->vk;
+        pq.qp.Vst = ctx->vv;
+        pq.qp.kc = const_cast<void *>(a.kc);
+        pq.qp.vc = const_cast<void *>(a.vc);
+        pq.qp.head_stride = a.head_stride;
+        pq.qp.v_tblk = a.v_tblk;
+        pq.qp.kvw = !plain ? 0 : ctx->kv_format == FL_KV_F16 ? 1 : 2;
+        if (fuse && L.qkv.rows % 64 == 0) {
+            // the QKV post runs in the GEMM's last-arriving K split
+            pq.post = 2;
+            pq.counters = ctx->vcnt;
+            rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks, &pq);
+            if (rc) return rc;
+        } else {
+            rc = verify_gemm(ctx, L.qkv, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+            if (rc) return rc;
+            HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, pq.qp));
+        }
         if (!plain)
             HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D,
                                         dev_pos ? ctx->vpos : nullptr));
@@ -1644,10 +1677,22 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         // FFN block (model.rs:2376-2543): wo residual + FFN norm in one kernel
         HIPCHK(ctx, launch_v_resnorm(pro, st, ctx->vpart, ks, M, H, xa, L.ffn_norm, eps, ctx->vxq, ctx->vxs,
                                      ctx->vxsum));
-        rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+        if (fuse && L.gu.rows == 2 * F && F % 32 == 0) {
+            // SiLU(gate)*up + Q8_0 in the GEMM's last-arriving K split
+            VgArgs pg{};
+            pg.post = 1;
+            pg.counters = ctx->vcnt;
+            pg.hq = ctx->vhq;
+            pg.hs = ctx->vhs;
+            pg.hsum = ctx->vhsum;
+            pg.F = F;
+            rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks, &pg);
+        } else {
+            rc = verify_gemm(ctx, L.gu, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks);
+            if (!rc) HIPCHK(ctx, launch_v_silu_quant(st, ctx->vpart, ks, M, F, ctx->vhq, ctx->vhs, ctx->vhsum));
+        }
         if (rc) return rc;
-        HIPCHK(ctx, launch_v_silu_quant(st, ctx->vpart, ks, M, F, ctx->vxq, ctx->vxs, ctx->vxsum));
-        rc = verify_gemm(ctx, L.down, M, ctx->vxq, ctx->vxs, ctx->vxsum, ks_down);
+        rc = verify_gemm(ctx, L.down, M, ctx->vhq, ctx->vhs, ctx->vhsum, ks_down);
         if (rc) return rc;
     }
     HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));

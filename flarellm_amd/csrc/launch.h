@@ -145,9 +145,8 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a);
 hipError_t launch_v_embed(int fmt, hipStream_t st, const WDesc &E, const int *tokens, int M, float *x);
 hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int ksplit, int M, int H, float *x,
                             const float *w, float eps, int8_t *q, float *s, int *sum);
-hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
-                             const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
-                             float *Vst, int kvfmt, const KvDst &kv);
+hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows,
+                             const VgArgs::QkvPost &P);
 hipError_t launch_v_store(hipStream_t st, const float *part, int ksplit, int M, int rows, float *out);
 hipError_t launch_v_residual(hipStream_t st, const float *part, int ksplit, int M, int H, float *x);
 hipError_t launch_v_silu_quant(hipStream_t st, const float *part, int ksplit, int M, int F, int8_t *q, float *s,

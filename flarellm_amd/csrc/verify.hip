@@ -14,6 +14,11 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
         if (a.W.cols % 256) return hipErrorInvalidValue;
         const int nsb = a.W.cols >> 8;
         kn = (size_t)((nsb + a.ksplit - 1) / a.ksplit) * 256;
+        if (a.post) {
+            // fused epilogues: 8-token kernel, whole 64-row columns
+            if (a.M > 8 || a.W.rows % 64 || !a.counters) return hipErrorInvalidValue;
+            if (a.post == 1 && (a.F % 32 || a.W.rows != 2 * a.F || !a.hq)) return hipErrorInvalidValue;
+        }
         if (a.M <= 8) {
             // activations of 8 token rows, then 8 (scale, sum) pairs per block
             // one super-block in flight per wave: 2 or 3 measured slower on
@@ -25,7 +30,7 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
             hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);
         }
     } else {
-        if (fmt != F_Q8_0) return hipErrorNotSupported;
+        if (fmt != F_Q8_0 || a.post) return hipErrorNotSupported;
         const int nb = a.W.cols >> 5;
         kn = (size_t)((nb + a.ksplit - 1) / a.ksplit) * 32;
         const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
@@ -56,18 +61,14 @@ hipError_t launch_v_resnorm(int pro, hipStream_t st, const float *part, int kspl
     return hipGetLastError();
 }
 
-// kvfmt KV_F16 / KV_F32: K / V go straight into the cache slots (kv); else
-// to the f32 staging rows Kst / Vst
-hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows, int nq, int nk, int D,
-                             const float *rope, long long sin_off, const int *pos0p, float *Q, float *Kst,
-                             float *Vst, int kvfmt, const KvDst &kv) {
+// P.kvw 1 / 2: K / V go straight into the F16 / F32 cache slots; 0: to the
+// f32 staging rows
+hipError_t launch_v_qkv_post(hipStream_t st, const float *part, int ksplit, int M, int rows,
+                             const VgArgs::QkvPost &P) {
     const dim3 grid((rows / 2 + 255) / 256, M);
-#define QP(KVW) hipLaunchKernelGGL(k_v_qkv_post<KVW>, grid, dim3(256), 0, st, part, ksplit, M, rows, nq, nk, D, rope, \
-                                   sin_off, pos0p, Q, Kst, Vst, kv)
-    if (kvfmt == KV_F16) QP(1);
-    else if (kvfmt == KV_F32) QP(2);
-    else QP(0);
-#undef QP
+    if (P.kvw == 1) hipLaunchKernelGGL(k_v_qkv_post<1>, grid, dim3(256), 0, st, part, ksplit, M, rows, P);
+    else if (P.kvw == 2) hipLaunchKernelGGL(k_v_qkv_post<2>, grid, dim3(256), 0, st, part, ksplit, M, rows, P);
+    else hipLaunchKernelGGL(k_v_qkv_post<0>, grid, dim3(256), 0, st, part, ksplit, M, rows, P);
     return hipGetLastError();
 }
 

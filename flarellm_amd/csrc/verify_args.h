@@ -19,14 +19,27 @@ struct VgArgs {
     int M;
     int ksplit;       // K chunks (grid y); chunk = ceil(units / ksplit) units
     float *part;      // [ksplit][M][rows] fp32 partial sums
-};
-
-// Plain (F32 / F16) cache of one layer, for K / V written straight from the
-// QKV partials.
-struct KvDst {
-    void *kc, *vc;
-    long long head_stride;  // elements between kv heads
-    int v_tblk;             // V in 32-slot transposed blocks
+    // k_vgemm_q4k8 only (rows % 64 == 0): the last-arriving K split of each
+    // workgroup column sums the partials of its 64 rows and applies
+    // post 1 = SiLU(gate)*up + Q8_0 (gate/up weight; a column holds 32 gate
+    // and the matching 32 up rows), post 2 = the QKV post (qp); 0 = none
+    int post;
+    int *counters;    // [gridDim.x] arrival counters, zero between launches
+    int8_t *hq;       // post 1: Q8_0 of h, [M][F] codes, [M][F/32] scales and sums
+    float *hs;
+    int *hsum;
+    int F;
+    struct QkvPost {
+        int nq, nk, D;
+        const float *rope;
+        long long sin_off;
+        const int *pos0p;
+        float *Q, *Kst, *Vst;
+        void *kc, *vc;          // KVW 1 / 2: the layer's F16 / F32 cache
+        long long head_stride;
+        int v_tblk;
+        int kvw;                // 0 staging rows, 1 F16 cache, 2 F32 cache
+    } qp;
 };
 
 }  // namespace fl

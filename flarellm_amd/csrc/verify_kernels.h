@@ -195,6 +195,9 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     }
 }
 
+template <int KVW>
+__device__ __forceinline__ void qkv_post_pair(const VgArgs::QkvPost &P, int t, int n, float x0, float x1);
+
 // Q4_K, M <= 8 tokens.  Sub-blocks j and j+4 are the low and high nibbles
 // of the same 32 qs bytes, so one pair of accumulating MFMAs forms both:
 // token slots 0-7 carry sub-block j's activations in k 0-15 of each MFMA
@@ -219,8 +222,11 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     const int xst = kn + 32;
     int8_t *lx = (int8_t *)smem;
     float2 *lsc = (float2 *)(smem + 8 * xst);
-    const int tile = blockIdx.x * 4 + wave;
-    const bool live = tile * 16 < W.rows;  // wave-uniform
+    // post 1: waves 0-1 take gate rows 32x .. 32x+31, waves 2-3 the up rows F
+    // further on
+    const int tile = a.post == 1 ? (wave < 2 ? 2 * (int)blockIdx.x + wave : a.F / 16 + 2 * (int)blockIdx.x + wave - 2)
+                                 : (int)blockIdx.x * 4 + wave;
+    const bool live = tile * 16 < W.rows;  // wave-uniform (always, with post)
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
     const int h = kg & 1, hi = kg >> 1;     // weight lane: byte half, nibble (sub-block j + 4*hi)
     const int tx = tA & 7, xhi = tA >> 3;   // activation lane: token tx of sub-block j + 4*xhi
@@ -290,7 +296,49 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 4 * h + e;
-            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[e];
+            float *dst = a.part + ((size_t)blockIdx.y * a.M + t) * W.rows + n;
+            if (t < a.M) {
+                if (a.post) st_agent(dst, acc[e]);  // read by another workgroup
+                else *dst = acc[e];
+            }
+        }
+    }
+    if (!a.post) return;
+    // ---- the last-arriving K split of this column finishes its rows -------
+    __shared__ int is_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = old == a.ksplit - 1;
+        if (is_last) __hip_atomic_store(&a.counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    const int t = threadIdx.x >> 5, u = threadIdx.x & 31;  // token, unit (post 1) / row pair (post 2)
+    const int tc = min(t, a.M - 1);
+    auto psum = [&](int row) {
+        float v = 0.0f;
+        for (int k = 0; k < a.ksplit; k++) v += ld_agent(a.part + ((size_t)k * a.M + tc) * W.rows + row);
+        return v;
+    };
+    if (a.post == 1) {
+        // silu_mul_into (model.rs:9783-9796), then quantize_input_q8_0_into:
+        // one 32-block of h per token
+        const int j = 32 * (int)blockIdx.x + u;
+        const float g = psum(j), up = psum(a.F + j);
+        const float hv = (g / (1.0f + expf(-g))) * up;
+        if (t < a.M) {  // uniform per 32-lane group
+            const size_t b = (size_t)t * (a.F >> 5) + blockIdx.x;
+            quant_block32_lanes(hv, a.hq + (size_t)t * a.F + 32 * blockIdx.x, a.hs + b, a.hsum + b);
+        }
+    } else {
+        const int n2 = 64 * (int)blockIdx.x + 2 * u;
+        const float x0 = psum(n2), x1 = psum(n2 + 1);
+        if (t < a.M) {
+            if (a.qp.kvw == 1) qkv_post_pair<1>(a.qp, t, n2, x0, x1);
+            else if (a.qp.kvw == 2) qkv_post_pair<2>(a.qp, t, n2, x0, x1);
+            else qkv_post_pair<0>(a.qp, t, n2, x0, x1);
         }
     }
 }
@@ -318,39 +366,34 @@ __global__ __launch_bounds__(256) void k_v_embed(WDesc E, const int *tokens, flo
     }
 }
 
-// QKV partials -> per token: RoPE (apply_rope_with_table, model.rs:7283-7296)
-// on the pair-interleaved q / k rows at position pos0 + t; q to Q[t].  K / V:
-// KVW 0 = f32 staging rows (quantized into the cache afterwards), 1 / 2 =
-// stored into the F16 / F32 cache slot pos0 + t (cpu_kv_write's layout,
-// model.rs:9810-9846).
+// QKV post of one rotate-half pair (rows n, n+1) of token t: RoPE
+// (apply_rope_with_table, model.rs:7283-7296) on the pair-interleaved q / k
+// rows at position pos0 + t; q to Q[t].  K / V: KVW 0 = f32 staging rows
+// (quantized into the cache afterwards), 1 / 2 = stored into the F16 / F32
+// cache slot pos0 + t (cpu_kv_write's layout, model.rs:9810-9846).
 template <int KVW>
-__global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int ksplit, int M, int rows, int nq, int nk,
-                                                    int D, const float *rope, long long sin_off, const int *pos0p,
-                                                    float *Q, float *Kst, float *Vst, KvDst kv) {
-    const int t = blockIdx.y;
-    const int pair = blockIdx.x * blockDim.x + threadIdx.x;  // rows 2*pair, 2*pair+1
-    if (2 * pair >= rows) return;
-    const int n = 2 * pair, half = D >> 1, pos = *pos0p + t;
-    const float x0 = vsum_part(part, ksplit, M, rows, t, n), x1 = vsum_part(part, ksplit, M, rows, t, n + 1);
+__device__ __forceinline__ void qkv_post_pair(const VgArgs::QkvPost &P, int t, int n, float x0, float x1) {
+    const int D = P.D, half = D >> 1, pos = *P.pos0p + t;
+    const int nq = P.nq, nk = P.nk;
     auto put = [&](bool isv, int e, float v) {  // element e of this token's K or V row
         if constexpr (KVW == 0) {
-            (isv ? Vst : Kst)[(size_t)t * nk + e] = v;
+            (isv ? P.Vst : P.Kst)[(size_t)t * nk + e] = v;
         } else {
             const int kvh = e / D, ch = e % D;
-            const size_t o = (size_t)kvh * kv.head_stride +
-                             ((isv && kv.v_tblk) ? vt_off(pos, ch, D) : (size_t)pos * D + ch);
-            if constexpr (KVW == 1) ((__half *)(isv ? kv.vc : kv.kc))[o] = __float2half(v);
-            else ((float *)(isv ? kv.vc : kv.kc))[o] = v;
+            const size_t o = (size_t)kvh * P.head_stride +
+                             ((isv && P.v_tblk) ? vt_off(pos, ch, D) : (size_t)pos * D + ch);
+            if constexpr (KVW == 1) ((__half *)(isv ? P.vc : P.kc))[o] = __float2half(v);
+            else ((float *)(isv ? P.vc : P.kc))[o] = v;
         }
     };
     if (n < nq + nk) {
         const int j = n % D, i = j >> 1;
-        const float c = rope[(size_t)pos * half + i], sn = rope[sin_off + (size_t)pos * half + i];
+        const float c = P.rope[(size_t)pos * half + i], sn = P.rope[P.sin_off + (size_t)pos * half + i];
         const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
         if (n < nq) {
             const int h = n / D;
-            Q[(size_t)t * nq + h * D + i] = y0;
-            Q[(size_t)t * nq + h * D + i + half] = y1;
+            P.Q[(size_t)t * nq + h * D + i] = y0;
+            P.Q[(size_t)t * nq + h * D + i + half] = y1;
         } else {
             const int k0 = (n - nq) - j;
             put(false, k0 + i, y0);
@@ -361,6 +404,17 @@ __global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int kspli
         put(true, vi, x0);
         put(true, vi + 1, x1);
     }
+}
+
+// QKV partials -> qkv_post_pair for every (token, row pair).
+template <int KVW>
+__global__ __launch_bounds__(256) void k_v_qkv_post(const float *part, int ksplit, int M, int rows,
+                                                    VgArgs::QkvPost P) {
+    const int t = blockIdx.y;
+    const int pair = blockIdx.x * blockDim.x + threadIdx.x;  // rows 2*pair, 2*pair+1
+    if (2 * pair >= rows) return;
+    const int n = 2 * pair;
+    qkv_post_pair<KVW>(P, t, n, vsum_part(part, ksplit, M, rows, t, n), vsum_part(part, ksplit, M, rows, t, n + 1));
 }
 
 // out[t] = partials (plain store, fl_op_batched_matvec_q8in)
