@@ -1518,8 +1518,10 @@ static int verify_ksplit(const fl_weight &w) {
     const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
     static const int target = getenv("FLARE_VG_WAVES") ? atoi(getenv("FLARE_VG_WAVES")) : 2048;  // tuning
     const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (target + tiles - 1) / tiles}));
-    // every chunk non-empty: the reducers sum all ksplit partial sets
-    const int chunk = (units + want - 1) / want;
+    // every chunk non-empty: the reducers sum all ksplit partial sets.  Q8_0
+    // chunks of whole 8-block rounds (the paired kernel's unit)
+    int chunk = (units + want - 1) / want;
+    if (w.format == FL_Q8_0) chunk = (chunk + 7) / 8 * 8;
     return (units + chunk - 1) / chunk;
 }
 

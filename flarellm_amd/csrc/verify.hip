@@ -33,8 +33,12 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
         if (fmt != F_Q8_0 || a.post) return hipErrorNotSupported;
         const int nb = a.W.cols >> 5;
         kn = (size_t)((nb + a.ksplit - 1) / a.ksplit) * 32;
-        const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
-        hipLaunchKernelGGL(k_vgemm_q8_0, grid, dim3(256), lds, st, a);
+        if (a.M <= 8) {
+            hipLaunchKernelGGL(k_vgemm_q8_08, grid, dim3(256), 8 * (kn + 32) + 8 * (kn / 32) * 8, st, a);
+        } else {
+            const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+            hipLaunchKernelGGL(k_vgemm_q8_0, grid, dim3(256), lds, st, a);
+        }
     }
     return hipGetLastError();
 }

@@ -195,6 +195,93 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     }
 }
 
+// Q8_0, M <= 8 tokens: blocks b and b+1 share one accumulating MFMA pair,
+// as the sub-block pairs of k_vgemm_q4k8 (token slots 0-7 carry block b's
+// activations in k 0-15, slots 8-15 block b+1's in k 16-31; weight lanes of
+// k 0-15 hold block b, those of k 16-31 block b+1).  Lane (n, kg) loads 16
+// bytes at 16*(kg&1) of its block; eight blocks per round.  Block term of
+// matvec_q8_0_preq_into (model.rs:8082-8099).
+__global__ __launch_bounds__(256) void k_vgemm_q8_08(VgArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const WDesc &W = a.W;
+    const int K = W.cols, nbk = K >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = (nbk + a.ksplit - 1) / a.ksplit;
+    const int b0 = blockIdx.y * chunk, b1 = min(nbk, b0 + chunk);
+    if (b0 >= b1) return;
+    const int kn = (b1 - b0) * 32, xst = kn + 32;
+    int8_t *lx = (int8_t *)smem;
+    float2 *lsc = (float2 *)(smem + 8 * xst);
+    const int tile = blockIdx.x * 4 + wave;
+    const bool live = tile * 16 < W.rows;  // wave-uniform
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int h = kg & 1, hi = kg >> 1;    // weight lane: byte half, block b + hi
+    const int tx = tA & 7, xhi = tA >> 3;  // activation lane: token tx of block b + xhi
+    const bool xon = xhi == hi && tx < a.M;
+    const int row = min(n, W.rows - 1);
+    const int8_t *wq = (const int8_t *)W.q + (size_t)row * K + 16 * h;
+    const uint16_t *ws = W.s + (size_t)row * nbk;
+    v4i_t wn[4];
+    uint16_t sn[4];
+    auto load = [&](int g0) {  // pair p: blocks g0+2p, g0+2p+1 (clamped into the chunk)
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int bb = min(g0 + 2 * p + hi, b1 - 1);
+            wn[p] = *(const v4i_t *)(wq + 32 * (size_t)bb);
+            sn[p] = ws[bb];
+        }
+    };
+    if (live) load(b0);
+    vg_stage<F_Q8_0, true>(a, b0 * 32, kn, lx, lsc, xst);
+    if (!live) return;
+    const int8_t *xo = lx + tx * xst + 16 * h + 32 * xhi;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int g0 = b0; g0 < b1; g0 += 8) {
+        v4i_t w[4];
+        uint16_t sc[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            w[p] = wn[p];
+            sc[p] = sn[p];
+        }
+        if (g0 + 8 < b1) load(g0 + 8);
+        v4i32_t dd[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int bl = g0 - b0 + 2 * p;
+            const bool xok = xon && g0 + 2 * p + xhi < b1;
+            const v4i_t xv = xok ? *(const v4i_t *)(xo + 32 * bl) : v4i_t{0, 0, 0, 0};
+            const i64x1_t w1 = ((i64x1_t)(uint32_t)w[p].y << 32) | (uint32_t)w[p].x;
+            const i64x1_t w2 = ((i64x1_t)(uint32_t)w[p].w << 32) | (uint32_t)w[p].z;
+            const i64x1_t x1 = ((i64x1_t)(uint32_t)xv.y << 32) | (uint32_t)xv.x;
+            const i64x1_t x2 = ((i64x1_t)(uint32_t)xv.w << 32) | (uint32_t)xv.z;
+            dd[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x2, w2, vg_mfma(x1, w1), 0, 0, 0);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int bb = g0 + 2 * p + hi;
+            if (bb < b1) {
+                const float wsc = h2f(sc[p]);
+                const float4 *ls = (const float4 *)(lsc + (bb - b0) * 8 + 4 * h);
+                const float4 l0 = ls[0], l1 = ls[1];
+                const float xs[4] = {l0.x, l0.z, l1.x, l1.z};
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] += (wsc * xs[e]) * (float)dd[p][e];
+            }
+        }
+    }
+    // lanes kg and kg+2 hold the even and odd blocks of the same outputs
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] += __shfl_xor(acc[e], 32, 64);
+    if (n < W.rows && hi == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 4 * h + e;
+            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[e];
+        }
+    }
+}
+
 template <int KVW>
 __device__ __forceinline__ void qkv_post_pair(const VgArgs::QkvPost &P, int t, int n, float x0, float x1);
 
