@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflare_hi
 
 FL_F32, FL_Q8_0, FL_Q4K, FL_Q6K = 0, 1, 2, 3
 FL_KV_F32, FL_KV_F16, FL_KV_Q8, FL_KV_KIVI2 = 0, 1, 2, 3
+FL_OPT_VERIFY_FUSE, FL_OPT_VERIFY_GRAPH, FL_OPT_EXACT = 1, 2, 3
 FORMAT_NAMES = {FL_F32: "F32", FL_Q8_0: "Q8_0", FL_Q4K: "Q4_K", FL_Q6K: "Q6_K"}
 
 
@@ -58,6 +59,7 @@ SIGNATURES = {
     "fl_last_error": (C.c_char_p, [vp]),
     "fl_ctx_stream": (vp, [vp]),
     "fl_sync": (i32, [vp]),
+    "fl_set_option": (i32, [vp, i32, i32]),
     "fl_weight_upload": (i32, [vp, C.POINTER(RawWeight), C.POINTER(vp)]),
     "fl_weight_free": (None, [vp, vp]),
     "fl_op_quantize_q8": (i32, [vp, vp, i32, vp, vp, vp]),

@@ -76,6 +76,10 @@ class HipBackend:
     def stream(self) -> int:
         return self.lib.fl_ctx_stream(self.ctx)
 
+    def set_option(self, option: int, value: int):
+        """fl_set_option: FL_OPT_VERIFY_FUSE / FL_OPT_VERIFY_GRAPH switches."""
+        check(self.lib.fl_set_option(self.ctx, option, int(value)), self.ctx)
+
     def sync(self):
         check(self.lib.fl_sync(self.ctx), self.ctx)
 

@@ -33,7 +33,7 @@ def _run(cmd: list[str]) -> None:
     subprocess.run(cmd, check=True)
 
 
-HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "attn.hip", "verify.hip", "mvo.hip"]
+HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "attn.hip", "verify.hip", "mvo.hip", "seq.hip"]
 
 
 def build(verbose: bool = True) -> str:

@@ -548,10 +548,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a0) {
             st_agent(mypart + G * D + 2 * tid, Mx[tid]);
             st_agent(mypart + G * D + 2 * tid + 1, Lx[tid]);
         }
-        __builtin_amdgcn_s_waitcnt(0);
+        // barrier + release / acquire counter: see the MFMA kernel's merge
         __syncthreads();
         if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(&a.counters[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int old = __hip_atomic_fetch_add(&a.counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             is_last = (old == nact - 1);
         }
         __syncthreads();

@@ -48,11 +48,11 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float *x, int nblk,
     quant_block32(v, q + b * 32, s + b, sums + b);
 }
 
-template <int PRO>
+template <int PRO, bool SEQ>
 __global__ __launch_bounds__(kThreads) void k_norm_quant(const float *x, const float *w, int n,
                                                          float eps, int8_t *q, float *s, int *sums) {
     __shared__ float red[8];
-    stage_q8<PRO>(x, w, eps, n, nullptr, nullptr, nullptr, q, s, sums, red);
+    stage_q8<PRO, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, q, s, sums, red);
 }
 
 __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const float *w, int n,
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void k_silu_mul(const float *g, const flo
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float gv = g[i];
-    out[i] = (gv / (1.0f + expf(-gv))) * u[i];
+    out[i] = (gv / (1.0f + fl_expf(-gv))) * u[i];
 }
 
 // Decode-step head: choose the token (prompt slot or previous argmax) and
@@ -284,7 +284,16 @@ struct fl_ctx {
     int *vtok = nullptr, *vpos = nullptr;
     unsigned long long *vslots = nullptr;
     size_t vpart_floats = 0;
+    // fl_set_option switches (measurement / testing)
+    bool verify_fuse = true, verify_graph = true;
+    // FL_OPT_EXACT: the decode step in the reference's floating-point order
+    bool exact = false;
+    float *seq_scores = nullptr;  // [num_heads][kv_slots] attention scores (exact mode)
+    float *seq_xn = nullptr;      // [hidden] final-normed vector (exact mode)
 };
+
+constexpr int kVerifyMaxKsplit = 16;
+constexpr int kVerifyCounters = 4096;  // workgroup columns of a fused verify GEMM
 
 static std::string g_err;
 static thread_local char g_errbuf[512];
@@ -477,6 +486,7 @@ static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const 
         return fail(ctx, FL_E_UNSUPPORTED, "quantized input of %d columns is too wide", w.cols);
     const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, false, epi == EPI_QKV);
     MvsArgs a = mvs_args(ctx, w, pro, epi, x, nw, eps, q, s, sums, out, slot);
+    a.seq = ctx->exact;
     if (epi == EPI_QKV) {
         if (!qe) return fail(ctx, FL_E_INVALID, "EPI_QKV without its arguments");
         if (w.rows != qe->nq + 2 * qe->nk || qe->nq % qe->hd || qe->nk % qe->hd)
@@ -530,6 +540,7 @@ static int launch_gateup(fl_ctx *ctx, const fl_weight &w, int pro, const float *
     if (pro == PRO_LOADQ && w.cols > 4 * 16 * 4 * 64)
         return fail(ctx, FL_E_UNSUPPORTED, "gate_up input of %d columns is too wide", w.cols);
     MvsArgs a = mvs_args(ctx, w, pro, EPI_STORE, x, nw, eps, q, s, sums, nullptr, nullptr);
+    a.seq = ctx->exact;
     a.F = F;
     a.hq = hq;
     a.hs = hs;
@@ -626,7 +637,20 @@ int fl_ctx_create(int device, fl_ctx **out) {
         return rc;
     }
     (void)hipMemset(c->d_counters, 0, 1024 * 4);
+    c->verify_fuse = getenv("FLARE_NO_VFUSE") == nullptr;  // initial value of FL_OPT_VERIFY_FUSE
     *out = c;
+    return 0;
+}
+
+int fl_set_option(fl_ctx *ctx, int option, int value) {
+    if (!ctx) return fail(nullptr, FL_E_INVALID, "null context");
+    switch (option) {
+    case FL_OPT_VERIFY_FUSE: ctx->verify_fuse = value != 0; break;
+    case FL_OPT_VERIFY_GRAPH: ctx->verify_graph = value != 0; break;
+    case FL_OPT_EXACT: ctx->exact = value != 0; break;
+    default: return fail(ctx, FL_E_INVALID, "unknown option %d", option);
+    }
+    drop_graphs(ctx);  // captured passes bake the old choice in
     return 0;
 }
 
@@ -646,13 +670,14 @@ static void model_release(fl_ctx *c) {
     c->kscale = c->vscale = nullptr; c->kparam = c->vparam = nullptr; c->kring = c->vring = nullptr;
     c->kvstage = nullptr; c->kvstage_rows = 0;
     void *ptrs[] = {c->out_norm, c->kcache, c->vcache, c->rope, c->x, c->qkv, c->attn, c->logits, c->bench_out,
-                    c->bench_trace, c->rope_cur,
+                    c->bench_trace, c->rope_cur, c->seq_scores, c->seq_xn,
                     c->aq, c->hq, c->as, c->hs, c->asum, c->hsum, c->st, c->tokens};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     c->out_norm = nullptr; c->kcache = c->vcache = nullptr; c->rope = nullptr; c->x = c->qkv = nullptr;
     c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->rope_cur = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
+    c->seq_scores = c->seq_xn = nullptr;
     void *vp[] = {c->vx, c->vx2, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
                   c->vtok, c->vpos, c->vslots, c->vhq, c->vhs, c->vhsum, c->vcnt};
     for (void *p : vp)
@@ -721,19 +746,18 @@ int fl_op_rmsnorm_quantize_q8(fl_ctx *ctx, const float *x, const float *w, int n
                               int8_t *q, float *scales, int32_t *sums) {
     if (!ctx || !x || !w || !q || !scales || !sums) return fail(ctx, FL_E_INVALID, "null argument");
     if (n <= 0 || n % 32) return fail(ctx, FL_E_INVALID, "n=%d must be a positive multiple of 32", n);
-    if (order == 0)
-        hipLaunchKernelGGL(k_norm_quant<PRO_NORMQ0>, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, q,
-                           scales, (int *)sums);
-    else
-        hipLaunchKernelGGL(k_norm_quant<PRO_NORMQ1>, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, q,
-                           scales, (int *)sums);
+    // FL_OPT_EXACT: the sum of squares in the reference's sequential order
+    auto kern = order == 0 ? (ctx->exact ? k_norm_quant<PRO_NORMQ0, true> : k_norm_quant<PRO_NORMQ0, false>)
+                           : (ctx->exact ? k_norm_quant<PRO_NORMQ1, true> : k_norm_quant<PRO_NORMQ1, false>);
+    hipLaunchKernelGGL(kern, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, q, scales, (int *)sums);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
 
 int fl_op_rmsnorm(fl_ctx *ctx, const float *x, const float *w, int n, float eps, float *out) {
     if (!ctx || !x || !w || !out || n <= 0) return fail(ctx, FL_E_INVALID, "bad argument");
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
+    if (ctx->exact) HIPCHK(ctx, launch_rmsnorm_seq(ctx->stream, x, w, n, eps, out));
+    else hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
     HIPCHK(ctx, hipGetLastError());
     return 0;
 }
@@ -973,6 +997,8 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->x, H * 4);
     ALLOC(ctx, ctx->qkv, (qd + 2 * kvd) * 4);
     ALLOC(ctx, ctx->attn, qd * 4);
+    ALLOC(ctx, ctx->seq_scores, (size_t)c.num_heads * ctx->kv_slots * 4);
+    ALLOC(ctx, ctx->seq_xn, H * 4);
     ALLOC(ctx, ctx->aq, qd);
     ALLOC(ctx, ctx->as, qd / 32 * 4);
     ALLOC(ctx, ctx->asum, qd / 32 * 4);
@@ -1151,7 +1177,11 @@ int fl_reset(fl_ctx *ctx) {
         HIPCHK(ctx, hipMemsetAsync(ctx->vring, 0, L * kKiviRing * kvd * 2, ctx->stream));
     }
     HIPCHK(ctx, hipMemsetAsync(ctx->st, 0, sizeof(DevState), ctx->stream));
+    // split-merge arrival counters: every launch leaves them at zero (the
+    // last arriver resets its counter); cleared here too, so a launch that
+    // did not complete cannot leave a stale count behind a reset
     HIPCHK(ctx, hipMemsetAsync(ctx->d_counters, 0, 1024 * 4, ctx->stream));
+    if (ctx->vcnt) HIPCHK(ctx, hipMemsetAsync(ctx->vcnt, 0, kVerifyCounters * 4, ctx->stream));
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
     return 0;
 }
@@ -1234,6 +1264,8 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
 
 static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     const fl_model_config &c = ctx->cfg;
+    if (ctx->exact && ctx->kv_format != FL_KV_F32 && ctx->kv_format != FL_KV_F16)
+        return fail(ctx, FL_E_UNSUPPORTED, "FL_OPT_EXACT needs an F32 or F16 KV cache (the reference's forms)");
     const int hd = c.head_dim, G = c.num_heads / c.num_kv_heads;
     const float eps = c.rms_norm_eps;
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
@@ -1251,9 +1283,30 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
         int rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
                              ctx->qkv, nullptr, &qe);
         if (rc) return rc;
-        AttnArgs a = layer_attn_args(ctx, l);
-        rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
-        if (rc) return rc;
+        if (ctx->exact) {
+            // reference-order attention, then quantize_input_q8_0_into of its output
+            AttnArgs a = layer_attn_args(ctx, l);
+            SeqAttnArgs sa{};
+            sa.q = ctx->qkv;
+            sa.kc = a.kc;
+            sa.vc = a.vc;
+            sa.head_stride = a.head_stride;
+            sa.D = hd;
+            sa.group = G;
+            sa.slots = ctx->kv_slots;
+            sa.posp = &ctx->st->pos;
+            sa.scores = ctx->seq_scores;
+            sa.out = ctx->attn;
+            HIPCHK(ctx, launch_attn_seq(ctx->kv_format == FL_KV_F16, ctx->stream, sa, c.num_heads));
+            const int nblk = c.num_heads * hd / 32;
+            hipLaunchKernelGGL(k_quantize, dim3((nblk + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream,
+                               ctx->attn, nblk, ctx->aq, ctx->as, ctx->asum);
+            HIPCHK(ctx, hipGetLastError());
+        } else {
+            AttnArgs a = layer_attn_args(ctx, l);
+            rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
+            if (rc) return rc;
+        }
         rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
                          nullptr);
         if (rc) return rc;
@@ -1272,6 +1325,12 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     if (q8out) {
         rc = launch_q8in(ctx, O, PRO_NORMQ1, want_logits ? EPI_STORE : EPI_ARGMAX, ctx->x, ctx->out_norm, eps,
                          nullptr, nullptr, nullptr, ctx->logits, &ctx->st->argmax);
+    } else if (ctx->exact) {
+        // rmsnorm_into, then matvec_argmax_f32 / matvec_into over the dequantized weight
+        HIPCHK(ctx, launch_rmsnorm_seq(ctx->stream, ctx->x, ctx->out_norm, c.hidden_dim, eps, ctx->seq_xn));
+        HIPCHK(ctx, launch_out_seq(O.format, ctx->stream, O.desc(), ctx->seq_xn, want_logits ? ctx->logits : nullptr,
+                                   &ctx->st->argmax));
+        rc = 0;
     } else {
         if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
         rc = launch_f32in(ctx, O, 1, want_logits ? EPI_STORE : EPI_ARGMAX, ctx->x, ctx->out_norm, eps, ctx->logits,
@@ -1476,8 +1535,6 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
 
 // ---- speculative verify -------------------------------------------------------
 
-constexpr int kVerifyMaxKsplit = 16;
-constexpr int kVerifyCounters = 4096;  // workgroup columns of a fused verify GEMM
 
 static int verify_alloc(fl_ctx *ctx) {
     if (ctx->have_verify) return 0;
@@ -1601,8 +1658,7 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
     float *xa = ctx->vx;
     HIPCHK(ctx, launch_v_embed(ctx->embed.format, st, ctx->embed.desc(), ctx->vtok, M, xa));
     // Q4_K layers, up to 8 tokens: the QKV post and SiLU run inside the GEMMs
-    static const bool no_fuse = getenv("FLARE_NO_VFUSE") != nullptr;  // measurement switch
-    const bool fuse = !no_fuse && ctx->layer_fmt == FL_Q4K && M <= 8 &&
+    const bool fuse = ctx->verify_fuse && ctx->layer_fmt == FL_Q4K && M <= 8 &&
                       std::max(qd + 2 * kvd, 2 * F) / 64 <= kVerifyCounters;
     int ks_down = 0;
     for (int l = 0; l < c.num_layers; l++) {
@@ -1749,7 +1805,7 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
     // F32 / F16 / Q8 caches: one captured graph per batch size (the positions
     // are read from the device); KIVI plans its group work from the host.
     // FLARE_NO_VERIFY_GRAPH (read per call): enqueue the kernels directly
-    const bool graph = use_graph() && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr;
+    const bool graph = use_graph() && ctx->verify_graph && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr;
     if (graph && ctx->kv_format != FL_KV_KIVI2) {
         auto it = ctx->vgraphs.find(M);
         if (it == ctx->vgraphs.end()) {

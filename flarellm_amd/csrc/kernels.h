@@ -110,6 +110,68 @@ __device__ __forceinline__ float wg_sum(float v, float *red) {
     return t;
 }
 
+// ------------------------------------------------------------------------
+// expf with the arithmetic of the x86-64 reference.  Rust's f32::exp lowers to
+// the C library's expf; glibc (sysdeps/ieee754/flt-32/e_expf.c, the published
+// ARM optimized-routines algorithm) computes it in double precision as
+//   z = x * 32/ln2, k = round(z) (shift trick), r = z - k,
+//   exp(x) = 2^(k/32) * (1 + C2 r + C1 r^2 + C0 r^3),
+// with 2^(i/32) from a 32-entry table, and on FMA-capable hosts evaluates r
+// and the polynomial with fused multiply-adds.  Every operation here is an
+// IEEE double operation with the same rounding, so the result is bit-identical
+// to the host's expf: checked for all 2^32 float inputs on the CPU, and on
+// the GPU against the host library by the tests.
+// kExp2Tab[i] = bits(2^(i/32) rounded to double) - (i << 47).
+// ------------------------------------------------------------------------
+__device__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__device__ __forceinline__ float fl_expf(float x) {
+    if (x != x) return x + x;                   // NaN
+    if (x == -INFINITY) return 0.0f;
+    if (x > 0x1.62e42ep6f) return INFINITY;     // above log(2^128)
+    if (x < -0x1.9fe368p6f) return 0.0f;        // below log(2^-150)
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    const double s = __longlong_as_double((long long)t);
+    const double p = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// Sum of squares in the reference's order: a sequential f32 fold over the
+// vector (x.iter().map(|v| v * v).sum(), model.rs:5615 / 7466).  Every lane
+// runs the same chain on uniform loads and holds the result.
+__device__ __forceinline__ float seq_sumsq(const float *x, int n) {
+    float ss = 0.0f;
+    for (int j = 0; j < n; j += 4) {
+        const v4f_t v = *(const v4f_t *)(x + j);
+        ss += v.x * v.x;
+        ss += v.y * v.y;
+        ss += v.z * v.z;
+        ss += v.w * v.w;
+    }
+    return ss;
+}
+
 __device__ __forceinline__ int8_t sat_i8(float v) {
     v = fminf(fmaxf(v, -128.0f), 127.0f);
     return (int8_t)(int)v;
@@ -170,15 +232,21 @@ __device__ __forceinline__ void quant_block32_lanes(float v, int8_t *q, float *s
 // ------------------------------------------------------------------------
 enum Pro { PRO_LOADQ = 0, PRO_NORMQ0 = 1, PRO_NORMQ1 = 2 };
 
+// SEQ: the sum of squares in the reference's sequential order (seq_sumsq).
+template <bool SEQ = false>
 __device__ __forceinline__ float wg_inv_rms(const float *x, int n, float eps, float *red) {
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
-    ss = wg_sum(ss, red);
+    if (SEQ) {
+        ss = seq_sumsq(x, n);
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+        ss = wg_sum(ss, red);
+    }
     const float rms = sqrtf(ss / (float)n + eps);
     return 1.0f / rms;
 }
 
-template <int PRO>
+template <int PRO, bool SEQ = false>
 __device__ __forceinline__ void stage_q8(const float *x, const float *w, float eps, int n,
                                          const int8_t *gq, const float *gs, const int *gsum,
                                          int8_t *lq, float *ls, int *lsum, float *red) {
@@ -194,7 +262,7 @@ __device__ __forceinline__ void stage_q8(const float *x, const float *w, float e
     } else {
         // one element per lane; the 32 lanes of a half-wave form one block
         // (blockDim and n are multiples of 32), quantized by the lane quantizer
-        const float inv = wg_inv_rms(x, n, eps, red);
+        const float inv = wg_inv_rms<SEQ>(x, n, eps, red);
         for (int i = threadIdx.x; i < n; i += blockDim.x) {
             const float v = (PRO == PRO_NORMQ0) ? x[i] * w[i] * inv : (x[i] * inv) * w[i];
             quant_block32_lanes(v, lq + (i & ~31), ls + (i >> 5), lsum + (i >> 5));

@@ -136,6 +136,23 @@ hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &
 hipError_t launch_kv_write(int kvfmt, hipStream_t st, const AttnArgs &a, const float *krows, const float *vrows,
                            int p0, int n, int D, const int *p0p = nullptr);
 
+// Reference-order kernels (seq.hip): sequential attention of the new token
+// over slots 0..*posp of an F32 / F16 head-major cache, rmsnorm_into, and the
+// f32-input output projection with first-max argmax.
+struct SeqAttnArgs {
+    const float *q;
+    const void *kc, *vc;     // layer cache planes [kv head][slot][D] (F16: V in 32-slot transposed blocks)
+    long long head_stride;   // elements between kv heads
+    int D, group, slots;     // head_dim, query heads per kv head, slots per kv head
+    const int *posp;         // token position (device)
+    float *scores;           // [num_heads][slots] scratch
+    float *out;              // [num_heads][D]
+};
+hipError_t launch_attn_seq(bool f16, hipStream_t st, const SeqAttnArgs &a, int num_heads);
+hipError_t launch_rmsnorm_seq(hipStream_t st, const float *x, const float *w, int n, float eps, float *out);
+hipError_t launch_out_seq(int fmt, hipStream_t st, const WDesc &W, const float *xn, float *logits,
+                          unsigned long long *slot);
+
 // MFMA output projection with f32 input for up to 8 tokens (mvo.hip)
 struct MvoArgs;
 hipError_t launch_mvo(int fmt, hipStream_t st, const MvoArgs &a);

@@ -64,7 +64,8 @@ struct QkvEpi {
 // NT = threads of the workgroup; E = elements per thread of the norm input
 // (n == NT*E with E in {8, 16}); other n take the generic loop of stage_q8.
 // ---------------------------------------------------------------------------
-template <int NT>
+// SEQ: the sum of squares in the reference's sequential order.
+template <int NT, bool SEQ = false>
 struct StageQ8 {
     v4i_t qv[4];  // PRO_LOADQ: int8 quants (16 B each), scales, sums
     float sv[2];
@@ -123,8 +124,8 @@ struct StageQ8 {
         }
         const int E = n / NT;
         if (!(n == NT * E && (E == 8 || E == 16))) {
-            if (pro == PRO_NORMQ0) stage_q8<PRO_NORMQ0>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
-            else stage_q8<PRO_NORMQ1>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
+            if (pro == PRO_NORMQ0) stage_q8<PRO_NORMQ0, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
+            else stage_q8<PRO_NORMQ1, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
             return;
         }
         float xs[16], ws[16];
@@ -139,7 +140,8 @@ struct StageQ8 {
         for (int j = 0; j < 16; j++)
             if (j < E) ss += xs[j] * xs[j];
         ST_TS(8);
-        ss = wg_sum(ss, red);
+        if (SEQ) ss = seq_sumsq(x, n);
+        else ss = wg_sum(ss, red);
         ST_TS(9);
         const float rms = sqrtf(ss / (float)n + eps);
         const float inv = 1.0f / rms;

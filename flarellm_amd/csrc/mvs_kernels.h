@@ -280,6 +280,7 @@ struct MvsArgs {
     int *hsum;
     float *hout;
     long long *trace;
+    int seq;  // host-side: launch the reference-order (SEQ) instantiation
 };
 
 // f32 input: x[K] | gx[K/16] | red[64]; Q8 input: q[K] | scales, sums [K/32] | red
@@ -288,11 +289,11 @@ __host__ __device__ inline size_t mvs_lds_bytes(bool f32in, int K) {
 }
 
 // prologue staging shared by both kernels: x (Q8 or f32) into LDS
-template <bool F32IN, int NT>
+template <bool F32IN, int NT, bool SEQ = false>
 struct Stage;
-template <int NT>
-struct Stage<false, NT> {
-    StageQ8<NT> s;
+template <int NT, bool SEQ>
+struct Stage<false, NT, SEQ> {
+    StageQ8<NT, SEQ> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw, a.gq, a.gs, a.gsum); }
     __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
         const int K = a.W.cols;
@@ -303,8 +304,8 @@ struct Stage<false, NT> {
         s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red, a.trace);
     }
 };
-template <int NT>
-struct Stage<true, NT> {
+template <int NT, bool SEQ>
+struct Stage<true, NT, SEQ> {
     StageF32<NT> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw); }
     __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
@@ -348,7 +349,7 @@ __device__ __forceinline__ float pc_dot(const Pc<FMT> &P, const WDesc &W, const 
 // (rmsnorm_quantize_q8_0_scalar model.rs:5610-5640 / rmsnorm_scalar_into +
 // quantize_input_q8_0_into 7456-7477, 5534-5571)
 // ---------------------------------------------------------------------------
-template <int SX>
+template <int SX, bool SEQ = false>
 struct RegX8 {
     v4f_t xv[SX][4], wv[SX][4];
     v4i_t q[SX];
@@ -377,7 +378,8 @@ struct RegX8 {
                     for (int k = 0; k < 4; k++) ss += xv[s][j][k] * xv[s][j][k];
             }
         }
-        ss = wave_sum(ss);
+        if (SEQ) ss = seq_sumsq(a.x, K);  // the reference's sequential order
+        else ss = wave_sum(ss);
         const float rms = sqrtf(ss / (float)K + a.eps);
         const float inv = 1.0f / rms;
 #pragma unroll
@@ -433,15 +435,67 @@ __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W,
 }
 
 // ---------------------------------------------------------------------------
+// Reference-order row sums (SEQ kernels).  The reference adds the per-block
+// terms of a row one at a time in block order (model.rs:8082-8099 for Q8_0,
+// 8997-9014 for Q4_K).  Within one 1 KiB step, lane l holds the term of the
+// piece at byte 16*l: Q8_0 block 32*step + l/2 on the even lane (the odd
+// lane's copy is zero); Q4_K super-block l/8, sub-block c = (l/2)%4 (even
+// lane, low nibbles) or c+4 (odd lane), i.e. the reference's order lo(0),
+// hi(0), lo(1), hi(1), ...  A unit's terms pass through a wave-private LDS
+// area and lane r adds row r's terms in that order to its running sum.  The
+// tiles, loads, integer dots and per-block float terms are the ones the
+// tree-order kernels use.
+// ---------------------------------------------------------------------------
+template <int FMT, int R, int SU>
+struct SeqFold {
+    float run = 0.0f;  // lane r: running sum of row r
+    __device__ __forceinline__ void add(const float (&t)[R][SU], float *fs, int rr, int span, int lane) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int s = 0; s < SU; s++) fs[(r * SU + s) * 64 + lane] = t[r][s];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (rr == 0) run = 0.0f;
+        if (lane < R) {
+            for (int s = 0; s < SU; s++) {
+                const int nl = min(64, max(0, (span - (rr * SU + s) * 1024 + 15) >> 4));
+                const float *p = fs + (lane * SU + s) * 64;
+                if (FMT == F_Q8_0) {
+                    for (int l = 0; l < nl; l += 2) run += p[l];
+                } else {
+                    for (int l = 0; l < nl; l++) run += p[l];
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // row r's sum, read from lane r (every lane gets it)
+    __device__ __forceinline__ float row(int r) const {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(run), r));
+    }
+};
+
+__host__ __device__ inline size_t align16(size_t b) { return (b + 15) & ~(size_t)15; }
+// LDS of the SEQ fold areas: waves x R x SU x 64 floats
+__host__ __device__ inline size_t seq_lds_bytes(int waves, int r, int su) { return (size_t)waves * r * su * 64 * 4; }
+
+// ---------------------------------------------------------------------------
 // k_mvs: generic persistent streaming matvec
 // ---------------------------------------------------------------------------
 constexpr int kMvsThreads = 256;
 
 // RX: register-resident activation (Q8_0, S <= SU): 1 = norm prologue
 // (RegX8), 2 = pre-quantized input (RegX8L)
-template <int FMT, bool F32IN, int R, int SU, int RX = 0>
+// SEQ: row sums and the norm's sum of squares in the reference's sequential
+// order (SeqFold, seq_sumsq); LDS grows by seq_lds_bytes(4, R, SU)
+template <int FMT, bool F32IN, int R, int SU, int RX = 0, bool SEQ = false>
 __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     static_assert(!RX || (FMT == F_Q8_0 && !F32IN), "register activation: Q8_0 weights, Q8 input");
+    static_assert(!SEQ || !F32IN, "reference-order sums: Q8 input");
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
     const int K = W.cols;
@@ -463,8 +517,8 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     };
     MV_TS(0);
     MV_TSB(0);
-    Stage<F32IN, kMvsThreads> stg;
-    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1>>::type rx;
+    Stage<F32IN, kMvsThreads, SEQ> stg;
+    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1, SEQ>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);             // 1. activation loads
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
@@ -503,9 +557,21 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     unsigned long long best = 0;
+    SeqFold<FMT, R, SU> fold;
+    float *fs = (float *)(smem + align16(mvs_lds_bytes(F32IN, K))) + wave * (R * SU * 64);
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
         const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
-        if constexpr (F32IN) {
+        if constexpr (SEQ) {
+            float t[R][SU];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int s = 0; s < SU; s++) {
+                    if constexpr (RX) t[r][s] = pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                    else t[r][s] = pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+                }
+            fold.add(t, fs, rr, mvs_span(FMT, K), lane);
+        } else if constexpr (F32IN) {
             // one step at a time: the lane's activation floats are loaded
             // once and shared by the R rows (not hoisted for the whole tile)
 #pragma unroll
@@ -531,7 +597,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         if (u == 0) MV_TS(3);
         if (rr == NR - 1) {
 #pragma unroll
-            for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+            for (int r = 0; r < R; r++) acc[r] = SEQ ? fold.row(r) : wave_sum(acc[r]);
             const int row0 = rg * R;
             if (a.epi == EPI_ARGMAX) {
                 best = umax64(best, rows_best<R>(acc, row0, W.rows));
@@ -573,7 +639,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 // b, b + grid, ...; wave w takes hidden units 32*blk + w*HU .. + HU, HU/2 at
 // a time (item = 2 gate rows + the 2 matching up rows).
 // ---------------------------------------------------------------------------
-template <int FMT, int SU, int NW, int RX = 0>
+template <int FMT, int SU, int NW, int RX = 0, bool SEQ = false>
 __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     static_assert(!RX || FMT == F_Q8_0, "register activation: Q8_0 weights");
     extern __shared__ __align__(16) char smem[];
@@ -609,8 +675,8 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     };
     MV_TS(0);
     MV_TSB(0);
-    Stage<false, NT> stg;
-    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1>>::type rx;
+    Stage<false, NT, SEQ> stg;
+    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1, SEQ>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);
     FLARE_STAGE_BARRIER();
@@ -623,24 +689,38 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    SeqFold<FMT, R, SU> fold;
+    float *fs = (float *)(smem + align16(mvs_lds_bytes(false, K) + 32 * 4)) + wave * (R * SU * 64);
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
         int blk, item, rr;
         rows_of(u, blk, item, rr);
+        if constexpr (SEQ) {
+            float t[R][SU];
 #pragma unroll
-        for (int r = 0; r < R; r++)
+            for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int s = 0; s < SU; s++) {
-                if constexpr (RX) acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
-                else acc[r] += pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
-            }
+                for (int s = 0; s < SU; s++) {
+                    if constexpr (RX) t[r][s] = pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                    else t[r][s] = pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+                }
+            fold.add(t, fs, rr, mvs_span(FMT, K), lane);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int s = 0; s < SU; s++) {
+                    if constexpr (RX) acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                    else acc[r] += pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
+                }
+        }
         if (u == 0) MV_TS(3);
         if (rr == NR - 1) {
 #pragma unroll
-            for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+            for (int r = 0; r < R; r++) acc[r] = SEQ ? fold.row(r) : wave_sum(acc[r]);
             if (lane < 2) {
                 // silu_mul_into: g / (1 + exp(-g)) * u
                 const float g = lane ? acc[1] : acc[0], up = lane ? acc[3] : acc[2];
-                hb[wave * HU + item * 2 + lane] = (g / (1.0f + expf(-g))) * up;
+                hb[wave * HU + item * 2 + lane] = (g / (1.0f + fl_expf(-g))) * up;
             }
 #pragma unroll
             for (int r = 0; r < R; r++) acc[r] = 0.0f;

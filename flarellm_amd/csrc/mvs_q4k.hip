@@ -11,13 +11,41 @@ namespace fl {
         return hipSuccess;                                                                            \
     }
 
+// Reference-order (SEQ) instantiations of the plans mvs_plan picks.
+#define SX(RR, SS)                                                                                      \
+    if (p.r == RR && p.su == SS) {                                                                      \
+        const size_t lds = align16(p.lds) + seq_lds_bytes(kMvsThreads / 64, RR, SS);                   \
+        hipLaunchKernelGGL((k_mvs<F_Q4K, false, RR, SS, 0, true>),                                     \
+                           dim3(resident_grid(k_mvs<F_Q4K, false, RR, SS, 0, true>, kMvsThreads, lds, p.grid)), \
+                           dim3(kMvsThreads), lds, st, a);                                              \
+        return hipSuccess;                                                                              \
+    }
+
 hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
+    if (a.seq) {
+        SX(4, 1) SX(2, 1) SX(1, 2)
+        return hipErrorNotSupported;
+    }
     C(F_Q4K, false, 4, 1) C(F_Q4K, false, 2, 1) C(F_Q4K, false, 2, 2) C(F_Q4K, false, 1, 2) C(F_Q4K, false, 1, 4)
     return hipErrorNotSupported;
 }
 #undef C
+#undef SX
 
 hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
+    if (a.seq) {
+#define GS(SS, NW)                                                                                    \
+    if (p.su == SS && p.r == NW) {                                                                    \
+        const size_t lds = align16(p.lds) + seq_lds_bytes(NW, 4, SS);                                 \
+        hipLaunchKernelGGL((k_mvs_gu<F_Q4K, SS, NW, 0, true>),                                       \
+                           dim3(resident_grid(k_mvs_gu<F_Q4K, SS, NW, 0, true>, NW * 64, lds, p.grid)), \
+                           dim3(NW * 64), lds, st, a);                                                \
+        return hipSuccess;                                                                            \
+    }
+        GS(1, 8) GS(2, 8)
+#undef GS
+        return hipErrorNotSupported;
+    }
 #define G(SS, NW)                                                                               \
     if (p.su == SS && p.r == NW) {                                                              \
         hipLaunchKernelGGL((k_mvs_gu<F_Q4K, SS, NW>),                                         \

@@ -23,8 +23,25 @@ static int use_regx(const MvsPlan &p, const MvsArgs &a) {
     return a.pro == PRO_LOADQ ? 2 : 0;
 }
 
+// Reference-order (SEQ) instantiations of the plans mvs_plan picks.
+#define SX(RR, SS, RXX)                                                                                  \
+    if (p.r == RR && p.su == SS && rx == RXX) {                                                          \
+        const size_t lds = align16(p.lds) + seq_lds_bytes(kMvsThreads / 64, RR, SS);                    \
+        hipLaunchKernelGGL((k_mvs<F_Q8_0, false, RR, SS, RXX, true>),                                   \
+                           dim3(resident_grid(k_mvs<F_Q8_0, false, RR, SS, RXX, true>, kMvsThreads, lds, p.grid)), \
+                           dim3(kMvsThreads), lds, st, a);                                               \
+        return hipSuccess;                                                                               \
+    }
+
 hipError_t launch_mvs_q8_0(bool f32in, const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
     const int rx = f32in ? 0 : use_regx(p, a);
+    if (a.seq) {
+        if (f32in) return hipErrorNotSupported;
+        SX(4, 1, 1) SX(4, 2, 1) SX(2, 1, 1) SX(2, 2, 1) SX(2, 4, 1)
+        SX(4, 1, 2) SX(4, 2, 2) SX(2, 1, 2) SX(2, 2, 2) SX(1, 4, 2) SX(1, 8, 2)
+        SX(4, 1, 0) SX(4, 2, 0) SX(2, 1, 0) SX(2, 2, 0) SX(1, 4, 0)
+        return hipErrorNotSupported;
+    }
     if (!f32in) {
         if (rx == 1) {
             CX(F_Q8_0, false, 4, 1, 1) CX(F_Q8_0, false, 4, 2, 1) CX(F_Q8_0, false, 2, 1, 1)
@@ -43,9 +60,23 @@ hipError_t launch_mvs_q8_0(bool f32in, const MvsPlan &p, hipStream_t st, const M
 }
 #undef C
 #undef CX
+#undef SX
 
 hipError_t launch_mvs_gu_q8_0(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
     const int rx = use_regx(p, a);
+    if (a.seq) {
+#define GS(SS, NW, RXX)                                                                               \
+    if (p.su == SS && p.r == NW && rx == RXX) {                                                       \
+        const size_t lds = align16(p.lds) + seq_lds_bytes(NW, 4, SS);                                 \
+        hipLaunchKernelGGL((k_mvs_gu<F_Q8_0, SS, NW, RXX, true>),                                    \
+                           dim3(resident_grid(k_mvs_gu<F_Q8_0, SS, NW, RXX, true>, NW * 64, lds, p.grid)), \
+                           dim3(NW * 64), lds, st, a);                                                \
+        return hipSuccess;                                                                            \
+    }
+        GS(1, 8, 1) GS(2, 8, 1) GS(1, 8, 0) GS(2, 8, 0)
+#undef GS
+        return hipErrorNotSupported;
+    }
 #define GX(SS, NW, RXX)                                                                              \
     if (p.su == SS && p.r == NW && (rx == RXX || !RXX)) {                                                      \
         hipLaunchKernelGGL((k_mvs_gu<F_Q8_0, SS, NW, RXX>),                                        \

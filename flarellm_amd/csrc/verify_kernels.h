@@ -393,10 +393,12 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     if (!a.post) return;
     // ---- the last-arriving K split of this column finishes its rows -------
     __shared__ int is_last;
-    __builtin_amdgcn_s_waitcnt(0);
+    // the barrier orders every thread's partial stores before thread 0's
+    // release; its acquire (then the barrier) orders the last split's loads
+    // after every other split's release
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         is_last = old == a.ksplit - 1;
         if (is_last) __hip_atomic_store(&a.counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -414,7 +416,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
         // one 32-block of h per token
         const int j = 32 * (int)blockIdx.x + u;
         const float g = psum(j), up = psum(a.F + j);
-        const float hv = (g / (1.0f + expf(-g))) * up;
+        const float hv = (g / (1.0f + fl_expf(-g))) * up;
         if (t < a.M) {  // uniform per 32-lane group
             const size_t b = (size_t)t * (a.F >> 5) + blockIdx.x;
             quant_block32_lanes(hv, a.hq + (size_t)t * a.F + 32 * blockIdx.x, a.hs + b, a.hsum + b);
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(256) void k_v_silu_quant(const float *part, int ksp
     const int rows = 2 * F;
     const int ic = min(i, F - 1);
     const float g = vsum_part(part, ksplit, M, rows, t, ic), u = vsum_part(part, ksplit, M, rows, t, F + ic);
-    const float h = (g / (1.0f + expf(-g))) * u;
+    const float h = (g / (1.0f + fl_expf(-g))) * u;
     // 32 lanes per block (F % 32 == 0, so a block never straddles the end)
     if (i - (threadIdx.x & 31) < F)
         quant_block32_lanes(h, q + (size_t)t * F + (i & ~31), s + (size_t)t * (F >> 5) + (i >> 5),

@@ -105,6 +105,27 @@ int fl_sync(fl_ctx *ctx);
 /* ComputeBackend::name (model.rs:615). */
 const char *fl_backend_name(void);
 
+/* Execution switches of a context (measurement and testing; no reference
+ * counterpart).  FL_OPT_VERIFY_FUSE (default 1): fl_verify runs the Q4_K QKV
+ * post-processing and SiLU*up inside the GEMMs' last-arriving K split (0: as
+ * separate kernels; both sum the K-split partials in the same order, so the
+ * results are identical).  FL_OPT_VERIFY_GRAPH (default 1): replay fl_verify
+ * as a captured HIP graph (0: enqueue kernel by kernel).  Drops captured
+ * graphs. */
+#define FL_OPT_VERIFY_FUSE 1
+#define FL_OPT_VERIFY_GRAPH 2
+/* FL_OPT_EXACT (default 0): the decode step (fl_decode_step, fl_generate)
+ * and the Q8-input op matvecs compute in the x86 reference's floating-point
+ * order -- row sums folded block by block, sequential sums of squares,
+ * sequential online-softmax attention, expf as the C library computes it,
+ * the f32 output dot in column order -- so logits equal the CPU reference's
+ * bit for bit.  The matvecs are the same streaming kernels with an in-order
+ * fold; attention and the f32 output projection run simple sequential
+ * kernels (slow).  F32 / F16 KV caches only.  Default: tree-order sums (fast;
+ * outputs within 1e-3 relative). */
+#define FL_OPT_EXACT 3
+int fl_set_option(fl_ctx *ctx, int option, int value);
+
 /* ---- weights -------------------------------------------------------------- */
 /* Upload one RawWeight for use with the fl_op_matvec* entry points (the
  * weight argument of ComputeBackend::batched_dequant_matmul, model.rs:468). */

@@ -10,6 +10,33 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Row-parallel threading (OpenMP).  Default 1 thread: the reference's
+ * quantized x86 path is single-threaded.  Rows, heads and tensor blocks are
+ * independent, and every row keeps its sequential order of operations, so the
+ * results do not depend on the thread count. */
+static int g_threads = 1;
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int or_get_threads(void) { return g_threads; }
+/* Summation order of the float reductions (row sums of the matvecs, sums of
+ * squares, f32 dots).  0 = the reference's sequential order (default).
+ * 1 = pairwise (recursive halving): an equally valid order, used only to
+ * measure how far two correct implementations that sum in different orders
+ * drift apart on a model -- the yardstick for the GPU's tree-order kernels.
+ * Not part of the restatement. */
+static int g_order = 0;
+void or_set_order(int order) { g_order = order ? 1 : 0; }
+
+static float pairwise(const float *t, size_t n) {
+    if (n <= 2) return n == 0 ? 0.0f : (n == 1 ? t[0] : t[0] + t[1]);
+    size_t h = n / 2;
+    return pairwise(t, h) + pairwise(t + h, n - h);
+}
+
+#define OR_PAR _Pragma("omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)")
 
 #define Q8_BLK 32
 #define Q8_BYTES 34
@@ -137,15 +164,21 @@ int or_dequant_tensor(const uint8_t *data, int format, size_t rows, size_t bpr, 
     size_t nb = rows * bpr;
     switch (format) {
     case OR_F32: memcpy(out, data, nb * sizeof(float)); return 0;
-    case OR_Q8_0:
+    case OR_Q8_0: {
+        OR_PAR
         for (size_t b = 0; b < nb; b++) or_dequant_q8_0_block(data + b * Q8_BYTES, out + b * 32);
         return 0;
-    case OR_Q4K:
+    }
+    case OR_Q4K: {
+        OR_PAR
         for (size_t b = 0; b < nb; b++) or_dequant_q4k_block(data + b * Q4K_BYTES, out + b * 256);
         return 0;
-    case OR_Q6K:
+    }
+    case OR_Q6K: {
+        OR_PAR
         for (size_t b = 0; b < nb; b++) or_dequant_q6k_block(data + b * Q6K_BYTES, out + b * 256);
         return 0;
+    }
     }
     return -1;
 }
@@ -164,12 +197,26 @@ void or_quantize_input_q8_0(const float *x, size_t n, float *scales, int8_t *q) 
     }
 }
 
+/* x.iter().map(|v| v * v).sum() (model.rs:5615, 7466): a sequential f32 fold
+ * (pairwise when g_order == 1). */
+static float sum_squares(const float *x, size_t n) {
+    if (g_order) {
+        float *t = (float *)malloc(n * sizeof(float));
+        for (size_t i = 0; i < n; i++) t[i] = x[i] * x[i];
+        float s = pairwise(t, n);
+        free(t);
+        return s;
+    }
+    float sum_sq = 0.0f;
+    for (size_t i = 0; i < n; i++) sum_sq += x[i] * x[i];
+    return sum_sq;
+}
+
 /* flare-core/src/model.rs:5610-5640 (rmsnorm_quantize_q8_0_scalar). Note the
  * product order (x*w)*inv_rms, unlike rmsnorm_scalar_into. */
 void or_rmsnorm_quantize_q8_0(const float *x, const float *w, size_t n, float eps,
                               float *scales, int8_t *q) {
-    float sum_sq = 0.0f;
-    for (size_t i = 0; i < n; i++) sum_sq += x[i] * x[i];
+    float sum_sq = sum_squares(x, n);
     float rms = sqrtf(sum_sq / (float)n + eps);
     float inv_rms = 1.0f / rms;
     size_t blocks = n / Q8_BLK;
@@ -190,8 +237,7 @@ void or_rmsnorm_quantize_q8_0(const float *x, const float *w, size_t n, float ep
 
 /* flare-core/src/model.rs:7469-7477 (rmsnorm_scalar_into): (x*inv_rms)*w. */
 void or_rmsnorm(const float *x, const float *w, size_t n, float eps, float *out) {
-    float sum_sq = 0.0f;
-    for (size_t i = 0; i < n; i++) sum_sq += x[i] * x[i];
+    float sum_sq = sum_squares(x, n);
     float rms = sqrtf(sum_sq / (float)n + eps);
     float inv_rms = 1.0f / rms;
     for (size_t i = 0; i < n; i++) out[i] = (x[i] * inv_rms) * w[i];
@@ -228,22 +274,45 @@ static float q8_row_dot(const uint8_t *row, const float *xs, const int8_t *xq, s
     return sum;
 }
 
+/* The same per-block terms, summed pairwise (g_order == 1). */
+static float q8_row_dot_pw(const uint8_t *row, const float *xs, const int8_t *xq, size_t bpr) {
+    float *t = (float *)malloc(bpr * sizeof(float));
+    for (size_t b = 0; b < bpr; b++) {
+        const uint8_t *blk = row + b * Q8_BYTES;
+        float combined = or_f16_to_f32(rd16(blk)) * xs[b];
+        t[b] = combined * (float)q8_block_idot(blk + 2, xq + b * Q8_BLK);
+    }
+    float s = pairwise(t, bpr);
+    free(t);
+    return s;
+}
+
 void or_matvec_q8_0_preq(const uint8_t *w, const float *xs, const int8_t *xq, size_t rows,
                          size_t bpr, float *out) {
-    for (size_t r = 0; r < rows; r++) out[r] = q8_row_dot(w + r * bpr * Q8_BYTES, xs, xq, bpr);
+    OR_PAR
+    for (size_t r = 0; r < rows; r++)
+        out[r] = g_order ? q8_row_dot_pw(w + r * bpr * Q8_BYTES, xs, xq, bpr)
+                         : q8_row_dot(w + r * bpr * Q8_BYTES, xs, xq, bpr);
+}
+
+/* Strict '>' over the row scores keeps the first maximum (model.rs:8550,
+ * 8652, 8682).  Scores are formed row-parallel, then scanned in row order. */
+static void first_max(const float *scores, size_t rows, int64_t *idx, float *val) {
+    int64_t bi = 0;
+    float bv = -INFINITY;
+    for (size_t r = 0; r < rows; r++)
+        if (scores[r] > bv) { bv = scores[r]; bi = (int64_t)r; }
+    *idx = bi;
+    *val = bv;
 }
 
 /* flare-core/src/model.rs:8518-8556: strict '>' keeps the first maximum. */
 void or_matvec_argmax_q8_0_preq(const uint8_t *w, const float *xs, const int8_t *xq,
                                 size_t rows, size_t bpr, int64_t *idx, float *val) {
-    int64_t bi = 0;
-    float bv = -INFINITY;
-    for (size_t r = 0; r < rows; r++) {
-        float s = q8_row_dot(w + r * bpr * Q8_BYTES, xs, xq, bpr);
-        if (s > bv) { bv = s; bi = (int64_t)r; }
-    }
-    *idx = bi;
-    *val = bv;
+    float *sc = (float *)malloc(rows * sizeof(float));
+    or_matvec_q8_0_preq(w, xs, xq, rows, bpr, sc);
+    first_max(sc, rows, idx, val);
+    free(sc);
 }
 
 /* Integer parts of model.rs:8997-9014 for one superblock. */
@@ -300,51 +369,85 @@ static float q4k_row_dot(const uint8_t *row, const float *xs, const int8_t *xq, 
     return sum;
 }
 
+/* The same per-sub-block terms, summed pairwise (g_order == 1). */
+static float q4k_row_dot_pw(const uint8_t *row, const float *xs, const int8_t *xq, size_t bpr) {
+    float *t = (float *)malloc(bpr * 8 * sizeof(float));
+    size_t nt = 0;
+    for (size_t b = 0; b < bpr; b++) {
+        const uint8_t *blk = row + b * Q4K_BYTES;
+        float d = or_f16_to_f32(rd16(blk)), dmin = or_f16_to_f32(rd16(blk + 2));
+        uint8_t sc[8], mn[8];
+        or_unpack_q4k_scales(blk + 4, sc, mn);
+        size_t is_base = b * 8;
+        for (int sub = 0; sub < 4; sub++) {
+            int32_t dl, dh, sl, sh;
+            q4k_sub_idots(blk + 16, xq + b * 256, sub, &dl, &dh, &sl, &sh);
+            float s_lo = xs[is_base + sub], s_hi = xs[is_base + sub + 4];
+            float d_sc_lo = d * (float)sc[sub];
+            float dmin_mn_lo = dmin * (float)mn[sub];
+            float d_sc_hi = d * (float)sc[sub + 4];
+            float dmin_mn_hi = dmin * (float)mn[sub + 4];
+            t[nt++] = s_lo * (d_sc_lo * (float)dl - dmin_mn_lo * (float)sl);
+            t[nt++] = s_hi * (d_sc_hi * (float)dh - dmin_mn_hi * (float)sh);
+        }
+    }
+    float s = pairwise(t, nt);
+    free(t);
+    return s;
+}
+
 /* flare-core/src/model.rs:9672-9779, x86 branch 9768-9778. */
 void or_matvec_q4k_q8(const uint8_t *w, const float *xs, const int8_t *xq, size_t rows,
                       size_t cols, float *out) {
     size_t bpr = cols / Q4K_VALS;
-    for (size_t r = 0; r < rows; r++) out[r] = q4k_row_dot(w + r * bpr * Q4K_BYTES, xs, xq, bpr);
+    OR_PAR
+    for (size_t r = 0; r < rows; r++)
+        out[r] = g_order ? q4k_row_dot_pw(w + r * bpr * Q4K_BYTES, xs, xq, bpr)
+                         : q4k_row_dot(w + r * bpr * Q4K_BYTES, xs, xq, bpr);
 }
 
 /* flare-core/src/model.rs:8569-8659, x86 branch 8644-8658. */
 void or_matvec_argmax_q4k_q8_preq(const uint8_t *w, const float *xs, const int8_t *xq,
                                   size_t rows, size_t cols, int64_t *idx, float *val) {
-    size_t bpr = cols / Q4K_VALS;
-    int64_t bi = 0;
-    float bv = -INFINITY;
-    for (size_t r = 0; r < rows; r++) {
-        float s = q4k_row_dot(w + r * bpr * Q4K_BYTES, xs, xq, bpr);
-        if (s > bv) { bv = s; bi = (int64_t)r; }
+    float *sc = (float *)malloc(rows * sizeof(float));
+    or_matvec_q4k_q8(w, xs, xq, rows, cols, sc);
+    first_max(sc, rows, idx, val);
+    free(sc);
+}
+
+/* sum += row[j] * vec[j] in column order (model.rs:8679-8681); pairwise when
+ * g_order == 1. */
+static float f32_dot(const float *row, const float *vec, size_t n) {
+    if (g_order) {
+        float *t = (float *)malloc(n * sizeof(float));
+        for (size_t j = 0; j < n; j++) t[j] = row[j] * vec[j];
+        float s = pairwise(t, n);
+        free(t);
+        return s;
     }
-    *idx = bi;
-    *val = bv;
+    float s = 0.0f;
+    for (size_t j = 0; j < n; j++) s += row[j] * vec[j];
+    return s;
 }
 
 /* flare-core/src/model.rs:8668-8689 (matvec_argmax_f32): sequential f32. */
 void or_matvec_argmax_f32(const float *mat, const float *vec, size_t rows, size_t cols,
                           int64_t *idx, float *val) {
-    int64_t bi = 0;
-    float bv = -INFINITY;
+    float *sc = (float *)malloc(rows * sizeof(float));
+    OR_PAR
     for (size_t r = 0; r < rows; r++) {
-        const float *row = mat + r * cols;
-        float s = 0.0f;
-        for (size_t j = 0; j < cols; j++) s += row[j] * vec[j];
-        if (s > bv) { bv = s; bi = (int64_t)r; }
+        sc[r] = f32_dot(mat + r * cols, vec, cols);
     }
-    *idx = bi;
-    *val = bv;
+    first_max(sc, rows, idx, val);
+    free(sc);
 }
 
 /* Plain sequential f32 matvec (model.rs:5286-5292 matvec_scalar_row order);
  * the reference's AVX2 variant (5098-5149) reorders the sum, so outputs of the
  * non-greedy logits path are compared with a tolerance. */
 void or_matvec_f32(const float *mat, const float *vec, size_t rows, size_t cols, float *out) {
-    for (size_t r = 0; r < rows; r++) {
-        float s = 0.0f;
-        for (size_t j = 0; j < cols; j++) s += mat[r * cols + j] * vec[j];
-        out[r] = s;
-    }
+    OR_PAR
+    for (size_t r = 0; r < rows; r++) out[r] = f32_dot(mat + r * cols, vec, cols);
 }
 
 /* flare-core/src/model.rs:7190-7212 (RopeTable::new) and 7299-7313
@@ -391,6 +494,7 @@ void or_gqa_attention(const float *q, const float *k_cache, const float *v_cache
     size_t heads_per_kv = num_heads / num_kv_heads;
     size_t kv_stride = num_kv_heads * head_dim;
     float scale = 1.0f / sqrtf((float)head_dim);
+    OR_PAR
     for (size_t h = 0; h < num_heads; h++) {
         size_t kvh = h / heads_per_kv;
         const float *qh = q + h * head_dim;

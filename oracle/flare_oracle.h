@@ -57,6 +57,15 @@ void or_matvec_q8_0_preq(const uint8_t *w, const float *xs, const int8_t *xq, si
                          size_t bpr, float *out);
 void or_matvec_q4k_q8(const uint8_t *w, const float *xs, const int8_t *xq, size_t rows,
                       size_t cols, float *out);
+/* Threads for the row-parallel loops (matvecs, argmax scores, attention
+ * heads, dequantization).  Default 1 = the reference's single-threaded x86
+ * path; results are identical for every thread count. */
+void or_set_threads(int n);
+/* Summation order of the float reductions: 0 = the reference's sequential
+ * order (default), 1 = pairwise.  Order 1 is a measuring stick (how far two
+ * valid summation orders drift apart on a model), not the reference. */
+void or_set_order(int order);
+int or_get_threads(void);
 void or_matvec_argmax_q8_0_preq(const uint8_t *w, const float *xs, const int8_t *xq,
                                 size_t rows, size_t bpr, int64_t *idx, float *val);
 void or_matvec_argmax_q4k_q8_preq(const uint8_t *w, const float *xs, const int8_t *xq,

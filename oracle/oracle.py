@@ -44,6 +44,9 @@ def lib() -> C.CDLL:
             build()
         L = C.CDLL(LIB_PATH)
         sig = {
+            "or_set_threads": (None, [C.c_int]),
+            "or_get_threads": (C.c_int, []),
+            "or_set_order": (None, [C.c_int]),
             "or_f16_to_f32": (f32, [C.c_uint16]),
             "or_f32_to_f16_rne": (C.c_uint16, [f32]),
             "or_dequant_tensor": (C.c_int, [vp, C.c_int, sz, sz, vp]),
@@ -80,6 +83,21 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def set_threads(n: int | None = None) -> int:
+    """Thread count of the oracle's row-parallel loops (None: this host's
+    CPUs, at most 16).  Results do not depend on it."""
+    if n is None:
+        n = min(16, len(os.sched_getaffinity(0)))
+    lib().or_set_threads(int(n))
+    return int(lib().or_get_threads())
+
+
+def set_order(order: int) -> None:
+    """0: the reference's sequential sums (default); 1: pairwise sums (a
+    measuring stick for order-dependent drift, not the reference)."""
+    lib().or_set_order(int(order))
 
 
 def _p(a: np.ndarray) -> int:

@@ -17,6 +17,7 @@ def oracle():
     from oracle import oracle as O
 
     O.lib()
+    O.set_threads()  # row-parallel oracle; results do not depend on the thread count
     return O
 
 

@@ -86,6 +86,8 @@ FMTS = {"q8": FL_KV_Q8, "kivi": FL_KV_KIVI2, "f16": FL_KV_F16}
 SHAPES = [  # (head_dim, heads, kv_heads, T)
     (64, 4, 2, 1), (64, 4, 2, 33), (64, 9, 3, 129), (64, 4, 2, 161), (64, 32, 8, 200),
     (128, 8, 8, 160), (128, 32, 8, 193), (128, 32, 8, 1000), (128, 32, 8, 8192),
+    # C4 contexts at Llama-3-8B heads
+    (128, 32, 8, 32768), (128, 32, 8, 131072),
 ]
 
 
@@ -93,14 +95,15 @@ SHAPES = [  # (head_dim, heads, kv_heads, T)
 @pytest.mark.parametrize("hd,nh,nkv,T", SHAPES)
 def test_attention_from_quantized_cache(backend, oracle, fmt, hd, nh, nkv, T):
     print(f"[kv-attn] {fmt} hd={hd} nh={nh} nkv={nkv} T={T}", flush=True)
-    spec = S.tiny_spec(FL_Q8_0, heads=nh, kv_heads=nkv, head_dim=hd, max_seq=max(T, 32))
+    spec = S.tiny_spec(FL_Q8_0, heads=nh, kv_heads=nkv, head_dim=hd, max_seq=max(T, 32), layers=2 if T < 32768 else 1)
     backend.init_gpu_kv_cache(spec, FMTS[fmt])
     rng = np.random.default_rng(T * 7 + hd)
     K = rng.standard_normal((T, nkv, hd)).astype(np.float32)
     V = rng.standard_normal((T, nkv, hd)).astype(np.float32)
     q = rng.standard_normal(nh * hd).astype(np.float32)
-    _write(backend, 1, K, V)
-    got = backend.grouped_query_attention_from_gpu_cache(q, 1, T)
+    layer = spec.layers - 1
+    _write(backend, layer, K, V)
+    got = backend.grouped_query_attention_from_gpu_cache(q, layer, T)
     Kv, Vv = oracle.kv_view(_mode(oracle, FMTS[fmt]), K, V)
     want64, mag = _attention_f64(q, Kv, Vv, nh, with_abs=True)
     _close(got, want64, absb=np.maximum(_attn_abs_bound(mag, T), ATTN_FLOOR * np.abs(want64).max()))
@@ -108,12 +111,13 @@ def test_attention_from_quantized_cache(backend, oracle, fmt, hd, nh, nkv, T):
     _close(oracle.gqa_attention(q, Kv, Vv, nh, nkv, hd, T), want64, floor=ATTN_FLOOR)
 
 
-@pytest.mark.parametrize("fmt", ["q8", "kivi"])
-def test_attention_quantized_cache_properties_long(backend, oracle, fmt):
-    """32k context (C4 shape): softmax weights sum to one, so with V rows all
-    equal to a constant vector c the output is c; with uniform keys the output
-    is the mean of the (cache-form) V rows."""
-    T, hd, nh, nkv = 32768, 128, 32, 8
+@pytest.mark.parametrize("fmt", ["q8", "kivi", "f16"])
+@pytest.mark.parametrize("T", [32768, 131072])
+def test_attention_quantized_cache_properties_long(backend, oracle, fmt, T):
+    """C4 contexts: softmax weights sum to one, so with V rows all equal to a
+    constant vector c the output is c; with uniform keys the output is the
+    mean of the (cache-form) V rows."""
+    hd, nh, nkv = 128, 32, 8
     print(f"[kv-long] {fmt} T={T}", flush=True)
     spec = S.tiny_spec(FL_Q8_0, heads=nh, kv_heads=nkv, head_dim=hd, max_seq=T, layers=1)
     backend.init_gpu_kv_cache(spec, FMTS[fmt])
@@ -122,7 +126,7 @@ def test_attention_quantized_cache_properties_long(backend, oracle, fmt):
     # a V row the cache form stores exactly: Q8 -> multiples of 1/128 with
     # +-127/128 in every 32-block (step exactly 1/128); KIVI -> the four
     # levels -0.75, -0.25, 0.25, 0.75 with both ends in every 32-group
-    if fmt == "q8":
+    if fmt in ("q8", "f16"):  # multiples of 1/128 are exact binary16 too
         m = rng.integers(-127, 128, (1, nkv, hd)).astype(np.float32)
         m[..., ::32] = 127.0
         c = m / 128.0

@@ -663,3 +663,21 @@ def test_model_kv_quantized_modes_close_to_f32(oracle):
         a = last_logits(mode)
         rel = np.linalg.norm(a - b) / np.linalg.norm(b)
         assert np.isfinite(a).all() and 0 < rel < tol, (mode, rel)
+
+
+def test_thread_count_does_not_change_results(oracle):
+    """Row-parallel oracle loops: every row keeps its sequential order, so
+    1 thread and many threads give bit-identical outputs."""
+    from flarellm_amd import synth as S
+
+    spec = S.tiny_spec(S.FL_Q4K, embed_fmt=S.FL_Q6K, output_fmt=S.FL_Q6K)
+    model = S.make_model(spec, seed=21)
+    prompt = S.random_tokens(22, 6, spec.vocab)
+    outs = []
+    for n in (1, 4):
+        oracle.set_threads(n)
+        om = oracle.OracleModel(model)
+        outs.append((om.generate(prompt, 8), om.forward_logits(3, 13)))
+    oracle.set_threads()
+    assert outs[0][0].tolist() == outs[1][0].tolist()
+    assert np.array_equal(outs[0][1], outs[1][1])
