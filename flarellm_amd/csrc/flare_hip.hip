@@ -1568,17 +1568,18 @@ static int verify_alloc(fl_ctx *ctx) {
     return 0;
 }
 
-// K chunks of a verify GEMM: about 2048 waves (one 16-row tile x one chunk
-// each), at most kVerifyMaxKsplit.
-static int verify_ksplit(const fl_weight &w) {
+// K chunks of a verify GEMM for M tokens: about 2048 waves (one 16-row tile
+// x one chunk each), at most kVerifyMaxKsplit.  Returns the split count and
+// sets the chunk (units per split, every chunk non-empty: the reducers sum
+// all ksplit partial sets).  The paired Q8_0 kernel (M <= 8) walks rounds of
+// 8 blocks, so its chunks are whole rounds.
+static int verify_split(const fl_weight &w, int M, int &chunk) {
     const int tiles = (w.rows + 15) / 16;
     const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
     static const int target = getenv("FLARE_VG_WAVES") ? atoi(getenv("FLARE_VG_WAVES")) : 2048;  // tuning
     const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (target + tiles - 1) / tiles}));
-    // every chunk non-empty: the reducers sum all ksplit partial sets.  Q8_0
-    // chunks of whole 8-block rounds (the paired kernel's unit)
-    int chunk = (units + want - 1) / want;
-    if (w.format == FL_Q8_0) chunk = (chunk + 7) / 8 * 8;
+    chunk = (units + want - 1) / want;
+    if (w.format == FL_Q8_0 && M <= 8) chunk = std::min(units, (chunk + 7) / 8 * 8);
     return (units + chunk - 1) / chunk;
 }
 
@@ -1591,7 +1592,7 @@ static int verify_gemm(fl_ctx *ctx, const fl_weight &w, int M, const int8_t *xq,
     a.xs = xs;
     a.xsum = xsum;
     a.M = M;
-    a.ksplit = ksplit = verify_ksplit(w);
+    a.ksplit = ksplit = verify_split(w, M, a.chunk);
     a.part = ctx->vpart;
     if ((size_t)ksplit * M * w.rows > ctx->vpart_floats) return fail(ctx, FL_E_INVALID, "verify partials too small");
     const hipError_t e = launch_vgemm(w.format, ctx->stream, a);
@@ -1607,7 +1608,8 @@ int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, con
         return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kVerifyMaxTokens);
     if (w->format != FL_Q8_0 && w->format != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
     // partials of this op live in their own buffer (sized for this weight)
-    const int ks = verify_ksplit(*w);
+    int chunk = 0;
+    const int ks = verify_split(*w, n_tokens, chunk);
     const size_t need = (size_t)ks * n_tokens * w->rows;
     float *part = nullptr;
     ALLOC(ctx, part, need * 4);
@@ -1618,6 +1620,7 @@ int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, con
     a.xsum = sums;
     a.M = n_tokens;
     a.ksplit = ks;
+    a.chunk = chunk;
     a.part = part;
     hipError_t e = launch_vgemm(w->format, ctx->stream, a);
     if (e == hipSuccess) e = launch_v_store(ctx->stream, part, ks, n_tokens, w->rows, out);

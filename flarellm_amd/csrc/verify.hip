@@ -7,13 +7,13 @@ namespace fl {
 hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     const int tiles = (a.W.rows + 15) / 16;
     const dim3 grid((tiles + 3) / 4, a.ksplit);
-    if (a.M < 1 || a.M > kVerifyMaxTokens || a.ksplit < 1) return hipErrorInvalidValue;
+    if (a.M < 1 || a.M > kVerifyMaxTokens || a.ksplit < 1 || a.chunk < 1) return hipErrorInvalidValue;
     if (a.W.cols % 32) return hipErrorInvalidValue;
     size_t kn;
     if (fmt == F_Q4K) {
         if (a.W.cols % 256) return hipErrorInvalidValue;
         const int nsb = a.W.cols >> 8;
-        kn = (size_t)((nsb + a.ksplit - 1) / a.ksplit) * 256;
+        kn = (size_t)a.chunk * 256;
         if (a.post) {
             // fused epilogues: 8-token kernel, whole 64-row columns
             if (a.M > 8 || a.W.rows % 64 || !a.counters) return hipErrorInvalidValue;
@@ -32,7 +32,7 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     } else {
         if (fmt != F_Q8_0 || a.post) return hipErrorNotSupported;
         const int nb = a.W.cols >> 5;
-        kn = (size_t)((nb + a.ksplit - 1) / a.ksplit) * 32;
+        kn = (size_t)a.chunk * 32;
         if (a.M <= 8) {
             hipLaunchKernelGGL(k_vgemm_q8_08, grid, dim3(256), 8 * (kn + 32) + 8 * (kn / 32) * 8, st, a);
         } else {

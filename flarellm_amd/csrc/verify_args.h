@@ -17,7 +17,8 @@ struct VgArgs {
     const float *xs;  // [M][K/32] block scales
     const int *xsum;  // [M][K/32] block sums of the quants
     int M;
-    int ksplit;       // K chunks (grid y); chunk = ceil(units / ksplit) units
+    int ksplit;       // K chunks (grid y)
+    int chunk;        // units (Q8_0 blocks / Q4_K super-blocks) per K chunk; ksplit = ceil(units / chunk)
     float *part;      // [ksplit][M][rows] fp32 partial sums
     // k_vgemm_q4k8 only (rows % 64 == 0): the last-arriving K split of each
     // workgroup column sums the partials of its 64 rows and applies

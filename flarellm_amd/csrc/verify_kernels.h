@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
     const WDesc &W = a.W;
     const int K = W.cols, nbk = K >> 5;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = (nbk + a.ksplit - 1) / a.ksplit;
+    const int chunk = a.chunk;
     const int b0 = blockIdx.y * chunk, b1 = min(nbk, b0 + chunk);
     if (b0 >= b1) return;
     const int kn = (b1 - b0) * 32;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     const WDesc &W = a.W;
     const int K = W.cols, nsb = K >> 8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = (nsb + a.ksplit - 1) / a.ksplit;
+    const int chunk = a.chunk;
     const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
     if (s0 >= s1) return;
     const int kn = (s1 - s0) * 256, nbc = kn >> 5;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_08(VgArgs a) {
     const WDesc &W = a.W;
     const int K = W.cols, nbk = K >> 5;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = (nbk + a.ksplit - 1) / a.ksplit;
+    const int chunk = a.chunk;
     const int b0 = blockIdx.y * chunk, b1 = min(nbk, b0 + chunk);
     if (b0 >= b1) return;
     const int kn = (b1 - b0) * 32, xst = kn + 32;
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     const WDesc &W = a.W;
     const int K = W.cols, nsb = K >> 8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = (nsb + a.ksplit - 1) / a.ksplit;
+    const int chunk = a.chunk;
     const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
     if (s0 >= s1) return;
     const int kn = (s1 - s0) * 256;
