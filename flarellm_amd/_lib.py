@@ -69,6 +69,7 @@ SIGNATURES = {
     "fl_op_matvec_f32in": (i32, [vp, vp, vp, vp]),
     "fl_op_batched_matvec_q8in": (i32, [vp, vp, i32, vp, vp, vp, vp]),
     "fl_op_batched_matvec_f32in": (i32, [vp, vp, i32, vp, vp]),
+    "fl_op_batched_matvec_q8in_noalloc": (i32, [vp, vp, i32, vp, vp, vp, vp]),
     "fl_op_block_dots": (i32, [vp, vp, vp, vp]),
     "fl_op_dequant": (i32, [vp, vp, vp]),
     "fl_op_matvec_argmax": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),

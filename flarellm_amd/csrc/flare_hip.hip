@@ -288,12 +288,20 @@ struct fl_ctx {
     bool verify_fuse = true, verify_graph = true;
     // FL_OPT_EXACT: the decode step in the reference's floating-point order
     bool exact = false;
+    float *scratch = nullptr;     // device address of `scratch` on this context's GPU
     float *seq_scores = nullptr;  // [num_heads][kv_slots] attention scores (exact mode)
     float *seq_xn = nullptr;      // [hidden] final-normed vector (exact mode)
 };
 
 constexpr int kVerifyMaxKsplit = 16;
 constexpr int kVerifyCounters = 4096;  // workgroup columns of a fused verify GEMM
+
+// K-split partials of fl_op_batched_matvec_q8in_noalloc: a file-scope device
+// array (each GPU holds its own copy for the life of the process), 16 MiB.
+// Host code uses its device address from hipGetSymbolAddress (fl_ctx::scratch),
+// never the array's name.
+constexpr size_t kNoAllocScratchFloats = (size_t)4 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 static std::string g_err;
 static thread_local char g_errbuf[512];
@@ -637,6 +645,12 @@ int fl_ctx_create(int device, fl_ctx **out) {
         return rc;
     }
     (void)hipMemset(c->d_counters, 0, 1024 * 4);
+    // this device's copy of the no-alloc scratch array (device current)
+    e = hipGetSymbolAddress((void **)&c->scratch, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !c->scratch) {
+        fl_ctx_destroy(c);
+        return fail(nullptr, FL_E_HIP, "scratch array address: %s", hipGetErrorString(e));
+    }
     c->verify_fuse = getenv("FLARE_NO_VFUSE") == nullptr;  // initial value of FL_OPT_VERIFY_FUSE
     *out = c;
     return 0;
@@ -1628,6 +1642,37 @@ int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, con
     (void)hipFree(part);
     HIPCHK(ctx, e);
     HIPCHK(ctx, e2);
+    return 0;
+}
+
+int fl_op_batched_matvec_q8in_noalloc(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
+                                      const float *scales, const int32_t *sums, float *out) {
+    if (!ctx || !w || !q || !scales || !sums || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n_tokens < 1 || n_tokens > kVerifyMaxTokens)
+        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kVerifyMaxTokens);
+    if (w->format != FL_Q8_0 && w->format != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
+    if (!ctx->scratch) return fail(ctx, FL_E_STATE, "no scratch array on this device");
+    // same K split (and so the same kernels and summation order) as the
+    // allocating entry point; partials in the device's scratch array
+    int chunk = 0;
+    const int ks = verify_split(*w, n_tokens, chunk);
+    const size_t need = (size_t)ks * n_tokens * w->rows;
+    if (need > kNoAllocScratchFloats)
+        return fail(ctx, FL_E_INVALID,
+                    "batched matvec needs %zu floats of K-split partials (%d splits x %d tokens x %d rows); the "
+                    "no-alloc scratch holds %zu",
+                    need, ks, n_tokens, w->rows, kNoAllocScratchFloats);
+    VgArgs a{};
+    a.W = w->desc();
+    a.xq = q;
+    a.xs = scales;
+    a.xsum = sums;
+    a.M = n_tokens;
+    a.ksplit = ks;
+    a.chunk = chunk;
+    a.part = ctx->scratch;  // every partial is written before it is read: nothing to clear
+    HIPCHK(ctx, launch_vgemm(w->format, ctx->stream, a));
+    HIPCHK(ctx, launch_v_store(ctx->stream, ctx->scratch, ks, n_tokens, w->rows, out));
     return 0;
 }
 

@@ -155,6 +155,17 @@ int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const fl
  * per-block integer dots, formed on int8 MFMA).  Synchronises. */
 int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
                               const float *scales, const int32_t *sums, float *out);
+/* fl_op_batched_matvec_q8in without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels, K split and results as fl_op_batched_matvec_q8in; the K-split
+ * partials live in a file-scope device array of 4 Mi floats (16 MiB, one copy
+ * per GPU), so calls needing more (splits x n_tokens x rows) are rejected
+ * with FL_E_INVALID.  Enqueues on the context stream and returns (no
+ * synchronisation).  Every call on one GPU shares that array: calls that
+ * overlap in time on one GPU (other streams or contexts) race. */
+int fl_op_batched_matvec_q8in_noalloc(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
+                                      const float *scales, const int32_t *sums, float *out);
 /* Dequantized-weight x f32-input matvec for n_tokens (1..8) input rows at
  * once (the speculative-verify logits path: matvec_into / matvec_argmax_f32,
  * model.rs:7549 and 8668, per row): x [n][cols], out [n][rows], device
