@@ -70,6 +70,9 @@ SIGNATURES = {
     "fl_op_batched_matvec_q8in": (i32, [vp, vp, i32, vp, vp, vp, vp]),
     "fl_op_batched_matvec_f32in": (i32, [vp, vp, i32, vp, vp]),
     "fl_op_batched_matvec_q8in_noalloc": (i32, [vp, vp, i32, vp, vp, vp, vp]),
+    "fl_op_batched_dequant_matmul": (i32, [vp, vp, vp, i32, vp]),
+    "fl_op_prefill_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, vp]),
+    "fl_decode_step_embed": (i32, [vp, vp, i32, vp, C.POINTER(C.c_int32), C.POINTER(f32)]),
     "fl_op_block_dots": (i32, [vp, vp, vp, vp]),
     "fl_op_dequant": (i32, [vp, vp, vp]),
     "fl_op_matvec_argmax": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),

@@ -159,6 +159,30 @@ class HipBackend:
         self.sync()
         return out
 
+    def batched_dequant_matmul(self, w: Weight, x):
+        """ComputeBackend::batched_dequant_matmul (model.rs:468, 740-1036):
+        f32 rows x [batch, cols] quantized on the device, then the quantized
+        matvec of each row -> [batch, rows]."""
+        import torch
+
+        n = x.shape[0]
+        out = torch.empty((n, w.rows), dtype=torch.float32, device=x.device)
+        self._torch_sync()
+        check(self.lib.fl_op_batched_dequant_matmul(self.ctx, w.handle, _ptr(x), n, _ptr(out)), self.ctx)
+        return out
+
+    def prefill_attention_gpu(self, q, k, v, seq_len: int, num_heads: int, num_kv_heads: int, head_dim: int):
+        """ComputeBackend::prefill_attention_gpu (model.rs:336-368): causal
+        attention of seq_len tokens (token t over 0..t); q [seq_len, nh*hd],
+        k / v [seq_len, nkv*hd] -> [seq_len, nh*hd]."""
+        import torch
+
+        out = torch.empty((seq_len, num_heads * head_dim), dtype=torch.float32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_prefill_attention(self.ctx, _ptr(q), _ptr(k), _ptr(v), seq_len, num_heads,
+                                               num_kv_heads, head_dim, _ptr(out)), self.ctx)
+        return out
+
     def matvec_f32in(self, w: Weight, x):
         import torch
 
@@ -293,12 +317,21 @@ class HipBackend:
         check(self.lib.fl_decode_step(self.ctx, token, pos, None, C.byref(t), C.byref(v)), self.ctx)
         return t.value, v.value
 
-    def forward_single_token_gpu(self, token: int, pos: int) -> np.ndarray:
-        """forward_single_token_gpu (model.rs:555): full logits."""
+    def forward_single_token_gpu(self, token, pos: int) -> np.ndarray:
+        """forward_single_token_gpu (model.rs:555): full logits.  `token` is
+        the f32 embedding row (the reference's argument) or a token id whose
+        row the device dequantizes."""
         out = np.empty(self.spec.vocab, np.float32)
         t = C.c_int32()
         v = C.c_float()
-        check(self.lib.fl_decode_step(self.ctx, token, pos, out.ctypes.data, C.byref(t), C.byref(v)), self.ctx)
+        if isinstance(token, np.ndarray):
+            emb = np.ascontiguousarray(token, np.float32)
+            assert emb.size == self.spec.hidden
+            check(self.lib.fl_decode_step_embed(self.ctx, emb.ctypes.data, pos, out.ctypes.data, C.byref(t),
+                                                C.byref(v)), self.ctx)
+        else:
+            check(self.lib.fl_decode_step(self.ctx, int(token), pos, out.ctypes.data, C.byref(t), C.byref(v)),
+                  self.ctx)
         return out
 
     def generate(self, prompt, n_gen: int) -> np.ndarray:

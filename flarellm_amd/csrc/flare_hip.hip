@@ -158,6 +158,8 @@ __device__ __forceinline__ uint32_t key_index(unsigned long long k) {
 // of each element are a dependent chain).
 constexpr int kEmbedThreads = 1024;
 template <int FMT>
+// x == nullptr: the embedding row is already in the residual buffer (a caller
+// that passes the f32 embedding, forward_single_token_gpu model.rs:555).
 __global__ __launch_bounds__(kEmbedThreads) void k_embed(WDesc E, DevState *st, int *tokens, float *x, const float *rope,
                                                    long long sin_off, int half, float *rope_cur) {
     __shared__ int tok_s, step_s;
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(kEmbedThreads) void k_embed(WDesc E, DevState *st, 
     }
     __syncthreads();
     const int row = tok_s, H = E.cols;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    for (int i = threadIdx.x; x && i < H; i += blockDim.x) {
         float v;
         if (FMT == F_Q8_0) {
             v = (float)((const int8_t *)E.q)[(size_t)row * H + i] * h2f(E.s[(size_t)row * (H >> 5) + (i >> 5)]);
@@ -1276,7 +1278,8 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
     return e;
 }
 
-static int enqueue_step(fl_ctx *ctx, bool want_logits) {
+// x_given: the caller has put the step's f32 embedding row into ctx->x.
+static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
     const fl_model_config &c = ctx->cfg;
     if (ctx->exact && ctx->kv_format != FL_KV_F32 && ctx->kv_format != FL_KV_F16)
         return fail(ctx, FL_E_UNSUPPORTED, "FL_OPT_EXACT needs an F32 or F16 KV cache (the reference's forms)");
@@ -1285,10 +1288,10 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits) {
     const int norm_pro = ctx->layer_fmt == FL_Q8_0 ? PRO_NORMQ0 : PRO_NORMQ1;
     const long long sin_off = (long long)c.max_seq_len * (c.head_dim / 2);
     switch (ctx->embed.format) {
-    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
-    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q8_0: hipLaunchKernelGGL(k_embed<F_Q8_0>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, x_given ? nullptr : ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q6K: hipLaunchKernelGGL(k_embed<F_Q6K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, x_given ? nullptr : ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    case FL_Q4K: hipLaunchKernelGGL(k_embed<F_Q4K>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, x_given ? nullptr : ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
+    default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, x_given ? nullptr : ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
     }
     HIPCHK(ctx, hipGetLastError());
     for (int l = 0; l < c.num_layers; l++) {
@@ -1387,7 +1390,10 @@ static int ensure_graph(fl_ctx *ctx) {
     return 0;
 }
 
-int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int32_t *out_token, float *out_val) {
+// One decode step at `pos`: the token's embedding row (embedding == nullptr)
+// or the caller's f32 embedding row.
+static int decode_step(fl_ctx *ctx, uint32_t token, const float *embedding, int pos, float *out_logits,
+                       int32_t *out_token, float *out_val) {
     if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
     if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
     const fl_model_config &c = ctx->cfg;
@@ -1401,8 +1407,11 @@ int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int3
     hs.n_prompt = pos + 1;
     HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + pos, &tok, 4, hipMemcpyHostToDevice, ctx->stream));
     HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
-    if (out_logits) {
-        int rc = enqueue_step(ctx, true);
+    if (embedding)
+        HIPCHK(ctx, hipMemcpyAsync(ctx->x, embedding, (size_t)c.hidden_dim * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (out_logits || embedding) {
+        // enqueued directly: the captured step dequantizes the token's row
+        int rc = enqueue_step(ctx, out_logits != nullptr, embedding != nullptr);
         if (rc) return rc;
     } else {
         int rc = ensure_graph(ctx);
@@ -1432,6 +1441,16 @@ int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int3
         if (out_val) *out_val = v;
     }
     return 0;
+}
+
+int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int32_t *out_token, float *out_val) {
+    return decode_step(ctx, token, nullptr, pos, out_logits, out_token, out_val);
+}
+
+int fl_decode_step_embed(fl_ctx *ctx, const float *embedding, int pos, float *out_logits, int32_t *out_token,
+                         float *out_val) {
+    if (!embedding) return fail(ctx, FL_E_INVALID, "null embedding");
+    return decode_step(ctx, 0u, embedding, pos, out_logits, out_token, out_val);
 }
 
 int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen, uint32_t *out_tokens) {
@@ -1673,6 +1692,88 @@ int fl_op_batched_matvec_q8in_noalloc(fl_ctx *ctx, const fl_weight *w, int n_tok
     a.part = ctx->scratch;  // every partial is written before it is read: nothing to clear
     HIPCHK(ctx, launch_vgemm(w->format, ctx->stream, a));
     HIPCHK(ctx, launch_v_store(ctx->stream, ctx->scratch, ks, n_tokens, w->rows, out));
+    return 0;
+}
+
+int fl_op_batched_dequant_matmul(fl_ctx *ctx, const fl_weight *w, const float *input, int batch, float *out) {
+    if (!ctx || !w || !input || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (batch < 1) return fail(ctx, FL_E_INVALID, "batch %d", batch);
+    if (w->format != FL_Q8_0 && w->format != FL_Q4K)
+        return fail(ctx, FL_E_UNSUPPORTED, "batched_dequant_matmul for format %d (Q8_0 / Q4_K)", w->format);
+    // quantize_input_q8_0_into of every input row (rows are contiguous and
+    // cols % 32 == 0, so the blocks of all rows are one array)
+    const size_t cols = (size_t)w->cols, nblk = (size_t)batch * cols / 32;
+    int8_t *q = nullptr;
+    float *sc = nullptr;
+    int *sum = nullptr;
+    int rc = dev_alloc(ctx, (void **)&q, (size_t)batch * cols);
+    if (!rc) rc = dev_alloc(ctx, (void **)&sc, nblk * 4);
+    if (!rc) rc = dev_alloc(ctx, (void **)&sum, nblk * 4);
+    if (!rc) {
+        hipLaunchKernelGGL(k_quantize, dim3((unsigned)((nblk + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                           ctx->stream, input, (int)nblk, q, sc, sum);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) rc = fail(ctx, FL_E_HIP, "quantize: %s", hipGetErrorString(e));
+    }
+    // then the per-row quantized matvec, kVerifyMaxTokens rows per GEMM
+    for (int b0 = 0; !rc && b0 < batch; b0 += kVerifyMaxTokens) {
+        const int n = std::min(kVerifyMaxTokens, batch - b0);
+        rc = fl_op_batched_matvec_q8in(ctx, w, n, q + (size_t)b0 * cols, sc + (size_t)b0 * (cols / 32),
+                                       sum + (size_t)b0 * (cols / 32), out + (size_t)b0 * w->rows);
+    }
+    (void)hipStreamSynchronize(ctx->stream);
+    if (q) (void)hipFree(q);
+    if (sc) (void)hipFree(sc);
+    if (sum) (void)hipFree(sum);
+    return rc;
+}
+
+int fl_op_prefill_attention(fl_ctx *ctx, const float *q, const float *k, const float *v, int seq_len, int num_heads,
+                            int num_kv_heads, int head_dim, float *out) {
+    if (!ctx || !q || !k || !v || !out) return fail(ctx, FL_E_INVALID, "null argument");
+    if (seq_len < 1 || num_kv_heads <= 0 || num_heads % num_kv_heads || num_kv_heads > 1024)
+        return fail(ctx, FL_E_INVALID, "bad prefill attention shape");
+    const int G = num_heads / num_kv_heads;
+    if (!attn_supported(head_dim, G)) return fail(ctx, FL_E_UNSUPPORTED, "head_dim %d / group %d", head_dim, G);
+    // queries z0 .. z0+Z-1 per launch (grid z), each attending 0..z0+z of the
+    // token-major rows; one set of split partials and counters per query
+    const int Z = std::min(seq_len, std::max(1, 1024 / num_kv_heads));
+    int ns, chmin;
+    choose_splits(seq_len, num_kv_heads, head_dim, ns, chmin);
+    ns = std::min(ns, 8);
+    int rc = ensure_part(ctx, (size_t)Z * num_kv_heads * ns * G * (head_dim + 2));
+    if (rc) return rc;
+    const int qd = num_heads * head_dim;
+    std::vector<int> starts;
+    for (int z0 = 0; z0 < seq_len; z0 += Z) starts.push_back(z0);
+    int *dstart = nullptr;
+    rc = dev_alloc(ctx, (void **)&dstart, starts.size() * 4);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(dstart, starts.data(), starts.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+    for (size_t c = 0; e == hipSuccess && c < starts.size(); c++) {
+        const int z0 = starts[c], nq = std::min(Z, seq_len - z0);
+        AttnArgs a{};
+        a.q = q + (size_t)z0 * qd;
+        a.kc = k;
+        a.vc = v;
+        a.tok_stride = (long long)num_kv_heads * head_dim;  // [token][kv_head][head_dim]
+        a.head_stride = head_dim;
+        a.posp = dstart + c;
+        a.nkv = num_kv_heads;
+        a.nsplit = ns;
+        a.chmin = chmin;
+        a.single = kAttmSingle;
+        a.part = ctx->d_part;
+        a.counters = ctx->d_counters;
+        a.out = out + (size_t)z0 * qd;
+        a.qstride = qd;
+        a.ostride = qd;
+        e = launch_attn(FL_KV_F32, head_dim, G, ctx->stream, a, nq);
+    }
+    const hipError_t es = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(dstart);
+    HIPCHK(ctx, e);
+    HIPCHK(ctx, es);
     return 0;
 }
 

@@ -155,6 +155,20 @@ int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const fl
  * per-block integer dots, formed on int8 MFMA).  Synchronises. */
 int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
                               const float *scales, const int32_t *sums, float *out);
+/* ComputeBackend::batched_dequant_matmul(&RawWeight, input, batch)
+ * (model.rs:468; CPU semantics model.rs:740-1036): input [batch][cols] f32
+ * rows (device), each quantized on the device with quantize_input_q8_0_into,
+ * then the quantized matvec of every row: out [batch][rows] (device).  Q8_0 /
+ * Q4_K weights; any batch (16 rows per int8-MFMA GEMM).  Synchronises. */
+int fl_op_batched_dequant_matmul(fl_ctx *ctx, const fl_weight *w, const float *input, int batch,
+                                 float *out);
+/* ComputeBackend::prefill_attention_gpu (model.rs:336-368; softcap 0):
+ * causal attention of seq_len tokens, token t over keys / values 0..t, each
+ * as cpu_grouped_query_attention (model.rs:9849-9966).  q [seq_len][nh*hd],
+ * k, v [seq_len][nkv*hd], out [seq_len][nh*hd]: f32 device arrays.
+ * Synchronises. */
+int fl_op_prefill_attention(fl_ctx *ctx, const float *q, const float *k, const float *v, int seq_len,
+                            int num_heads, int num_kv_heads, int head_dim, float *out);
 /* fl_op_batched_matvec_q8in without any allocation: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
@@ -240,6 +254,11 @@ int fl_reset(fl_ctx *ctx);
  * slot), attending to pos+1 slots. */
 int fl_decode_step(fl_ctx *ctx, uint32_t token, int pos, float *out_logits, int32_t *out_token,
                    float *out_val);
+/* forward_single_token_gpu(token_embedding, pos, ...) (model.rs:555-557)
+ * exactly: the step's input is the caller's f32 embedding row (hidden_dim
+ * host floats) instead of a token id; otherwise as fl_decode_step. */
+int fl_decode_step_embed(fl_ctx *ctx, const float *embedding, int pos, float *out_logits,
+                         int32_t *out_token, float *out_val);
 /* Greedy generation (Generator::step loop, flare-core/src/generate.rs:186-206):
  * feeds the n_prompt tokens one per step from position 0, then writes n_gen
  * generated tokens to out_tokens.  Runs device-resident: one HIP graph replay
