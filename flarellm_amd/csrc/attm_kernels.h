@@ -719,17 +719,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             st_agent(mypart + G * D + 2 * tid + 1, Lx[tid]);
         }
         ATTN_TS(4);
-        // the barrier orders every thread's partial stores before thread 0's
-        // release; its acquire (then the barrier) orders the merge loads of
-        // the last workgroup after every other workgroup's release
-        __syncthreads();
         ATTN_TS(5);
-        if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(&a.counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            is_last = (old == nact - 1);
-        }
-        __syncthreads();
-        if (!is_last) return;
+        if (!split_arrive_last<false>(&a.counters[kvh], nact, &is_last)) return;
         // last workgroup of the kv head: each thread merges its OPT outputs
         // (one head each) over the nact partials, MB splits per round trip
         // (all loads of a batch independent), online rescale between batches:

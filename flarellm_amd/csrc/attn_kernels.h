@@ -548,14 +548,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a0) {
             st_agent(mypart + G * D + 2 * tid, Mx[tid]);
             st_agent(mypart + G * D + 2 * tid + 1, Lx[tid]);
         }
-        // barrier + release / acquire counter: see the MFMA kernel's merge
-        __syncthreads();
-        if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(&a.counters[kvh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            is_last = (old == nact - 1);
-        }
-        __syncthreads();
-        if (!is_last) return;
+        if (!split_arrive_last<false>(&a.counters[kvh], nact, &is_last)) return;
         ATTN_TSL(6);
         // last workgroup of the kv head: thread t merges outputs
         // [t*OPT, t*OPT+OPT) (one head g) from the split partials, 16 splits

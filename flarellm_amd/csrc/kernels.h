@@ -157,6 +157,59 @@ __device__ __forceinline__ float fl_expf(float x) {
     return (float)y;
 }
 
+// ------------------------------------------------------------------------
+// Arrival of a workgroup at a split-merge counter (split-K attention, fused
+// verify GEMM epilogues).  The workgroup has stored its partials with
+// agent-scope atomic stores; returns true (in every thread) in the workgroup
+// that arrives last, after which its agent-scope loads see every other
+// workgroup's partials.  RESET: the last arrival sets the counter back to 0.
+//   FLARE_SPLIT_SYNC 2 (default): each wave's agent-scope release fence (its
+//     stores complete and visible at agent scope) before the barrier, thread
+//     0 counts with an acq_rel RMW, the last workgroup's waves acquire at
+//     agent scope before loading.
+//   1: wait for the wave's own stores (s_waitcnt 0), barrier, relaxed RMW.
+//   0: barrier, thread 0's acq_rel RMW only.
+// (1 and 0 are measurement builds.)
+// ------------------------------------------------------------------------
+#ifndef FLARE_SPLIT_SYNC
+#define FLARE_SPLIT_SYNC 1
+#endif
+template <bool RESET>
+__device__ __forceinline__ bool split_arrive_last(int *counter, int n, int *flag) {
+#if FLARE_SPLIT_SYNC == 2
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == n - 1;
+        if (RESET && old == n - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const bool last = *flag != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return last;
+#elif FLARE_SPLIT_SYNC == 1
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == n - 1;
+        if (RESET && old == n - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *flag != 0;
+#else
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == n - 1;
+        if (RESET && old == n - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *flag != 0;
+#endif
+}
+
 // Sum of squares in the reference's order: a sequential f32 fold over the
 // vector (x.iter().map(|v| v * v).sum(), model.rs:5615 / 7466).  Every lane
 // runs the same chain on uniform loads and holds the result.

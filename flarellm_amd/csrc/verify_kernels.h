@@ -393,17 +393,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     if (!a.post) return;
     // ---- the last-arriving K split of this column finishes its rows -------
     __shared__ int is_last;
-    // the barrier orders every thread's partial stores before thread 0's
-    // release; its acquire (then the barrier) orders the last split's loads
-    // after every other split's release
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = old == a.ksplit - 1;
-        if (is_last) __hip_atomic_store(&a.counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!is_last) return;
+    if (!split_arrive_last<true>(&a.counters[blockIdx.x], a.ksplit, &is_last)) return;
     const int t = threadIdx.x >> 5, u = threadIdx.x & 31;  // token, unit (post 1) / row pair (post 2)
     const int tc = min(t, a.M - 1);
     auto psum = [&](int row) {
