@@ -8,7 +8,9 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflare_hip.so")
+# FLARE_LIB: load another build of the library (diagnostic builds, e.g. with
+# FLARE_BUILD_DEFS; measurement only)
+LIB_PATH = os.environ.get("FLARE_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflare_hip.so")
 
 FL_F32, FL_Q8_0, FL_Q4K, FL_Q6K = 0, 1, 2, 3
 FL_KV_F32, FL_KV_F16, FL_KV_Q8, FL_KV_KIVI2 = 0, 1, 2, 3
@@ -48,6 +50,30 @@ class ModelConfig(C.Structure):
 
 
 vp, i32, f32, sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+
+
+class SamplingParams(C.Structure):
+    """fl_sampling_params == flarellm SamplingParams (sampling.rs:19-54)
+    without the self-speculation fields."""
+
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_p", C.c_float),
+        ("top_k", C.c_int),
+        ("repeat_penalty", C.c_float),
+        ("min_p", C.c_float),
+        ("speculative", C.c_int),
+    ]
+
+
+class SpecStats(C.Structure):
+    """fl_spec_stats == SpeculativeStats (generate.rs:22-30)."""
+
+    _fields_ = [("attempts", C.c_uint64), ("drafted", C.c_uint64), ("accepted", C.c_uint64)]
+
+
+RNG_FN = C.CFUNCTYPE(C.c_float, C.c_void_p)
+TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_uint32, C.c_size_t, C.c_void_p)
 
 # name -> (restype, argtypes); every symbol here must be declared in
 # include/flare_hip.h (checked by tests/test_abi.py).
@@ -95,7 +121,26 @@ SIGNATURES = {
     "fl_generate": (i32, [vp, vp, i32, i32, vp]),
     "fl_decode_continue": (i32, [vp, i32]),
     "fl_verify": (i32, [vp, vp, i32, i32, vp, vp]),
+    "fl_prefill": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "fl_decode_run": (i32, [vp, C.c_uint32, i32, i32, vp]),
     "fl_read_tokens": (i32, [vp, i32, i32, vp]),
+    "fl_sampling_params_default": (None, [vp]),
+    "fl_op_sample": (i32, [vp, vp, i32, vp, vp, i32, f32, C.POINTER(C.c_int32)]),
+    "fl_decode_step_sample": (i32, [vp, C.c_uint32, i32, vp, vp, i32, f32, C.POINTER(C.c_int32)]),
+    "fl_ngram_create": (vp, []),
+    "fl_ngram_destroy": (None, [vp]),
+    "fl_ngram_record": (None, [vp, vp, sz]),
+    "fl_ngram_record_all": (None, [vp, vp, sz]),
+    "fl_ngram_lookup": (i32, [vp, vp, sz, vp]),
+    "fl_ngram_entries": (sz, [vp]),
+    "fl_generator_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "fl_generator_destroy": (None, [vp]),
+    "fl_generator_prefill": (i32, [vp, vp, i32, vp]),
+    "fl_generator_step": (i32, [vp, f32, C.POINTER(C.c_uint32)]),
+    "fl_generator_generate": (i32, [vp, vp, i32, i32, C.c_int64, vp, vp, vp, vp, vp, C.POINTER(i32)]),
+    "fl_generator_stats": (i32, [vp, vp]),
+    "fl_generator_position": (i32, [vp]),
+    "fl_generator_tokens": (i32, [vp, vp, i32]),
     "fl_bench_layer_kernel": (i32, [vp, i32, i32, i32, C.POINTER(C.c_double)]),
     "fl_bench_kernel_name": (C.c_char_p, [vp, i32]),
     "fl_synth_normal": (None, [C.c_uint64, C.c_uint64, sz, f32, f32, vp]),

@@ -351,6 +351,24 @@ class HipBackend:
                                  vals.ctypes.data), self.ctx)
         return out, vals
 
+    def forward_prefill(self, tokens, pos0: int = 0, logits: bool = True):
+        """Model::forward_prefill (model.rs:2578-3040): the prompt in batched
+        passes; returns (logits of the last token or None, greedy token,
+        its value)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.spec.vocab, np.float32) if logits else None
+        t = C.c_int32()
+        v = C.c_float()
+        check(self.lib.fl_prefill(self.ctx, tokens.ctypes.data, tokens.size, pos0,
+                                  out.ctypes.data if logits else None, C.byref(t), C.byref(v)), self.ctx)
+        return out, t.value, v.value
+
+    def decode_run(self, token: int, pos: int, n_steps: int) -> np.ndarray:
+        """n_steps device-resident greedy steps from `token` at `pos`."""
+        out = np.empty(n_steps, np.uint32)
+        check(self.lib.fl_decode_run(self.ctx, int(token), pos, n_steps, out.ctypes.data), self.ctx)
+        return out
+
     def decode_continue(self, n_steps: int):
         """Enqueue n_steps more device-resident greedy steps (asynchronous)."""
         check(self.lib.fl_decode_continue(self.ctx, n_steps), self.ctx)
@@ -369,4 +387,81 @@ class HipBackend:
         return self.lib.fl_bench_kernel_name(self.ctx, which).decode()
 
 
-__all__ = ["HipBackend", "Weight", "FlareError"]
+class Generator:
+    """flarellm Generator (flare-core/src/generate.rs:106-560) over a backend
+    holding a model: fl_generator_* in the library (n-gram drafts verified in
+    one fl_verify pass, sampling on the device)."""
+
+    def __init__(self, backend: "HipBackend", temperature=0.7, top_p=0.9, top_k=40, repeat_penalty=1.1,
+                 min_p=0.0, speculative=True):
+        self.b = backend
+        self.lib = backend.lib
+        self.params = _lib.SamplingParams(temperature, top_p, int(top_k), repeat_penalty, min_p, int(bool(speculative)))
+        h = C.c_void_p()
+        check(self.lib.fl_generator_create(backend.ctx, C.byref(self.params), C.byref(h)), backend.ctx)
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.fl_generator_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prefill(self, prompt, logits: bool = False):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(self.b.spec.vocab, np.float32) if logits else None
+        check(self.lib.fl_generator_prefill(self.h, prompt.ctypes.data, prompt.size,
+                                            out.ctypes.data if logits else None), self.b.ctx)
+        return out
+
+    def step(self, u: float = 0.5) -> int:
+        t = C.c_uint32()
+        check(self.lib.fl_generator_step(self.h, u, C.byref(t)), self.b.ctx)
+        return t.value
+
+    def generate(self, prompt, max_tokens: int, eos=None, rng=None, on_token=None) -> list:
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(max(max_tokens, 1), np.uint32)
+        n = C.c_int()
+        rng_cb = _lib.RNG_FN(lambda _u: float(rng())) if rng is not None else None
+        tok_cb = _lib.TOKEN_FN(lambda t, s, _u: 1 if on_token(int(t), int(s)) else 0) if on_token is not None else None
+        check(self.lib.fl_generator_generate(self.h, prompt.ctypes.data, prompt.size, max_tokens,
+                                             -1 if eos is None else int(eos),
+                                             C.cast(rng_cb, C.c_void_p) if rng_cb else None, None,
+                                             C.cast(tok_cb, C.c_void_p) if tok_cb else None, None,
+                                             out.ctypes.data, C.byref(n)), self.b.ctx)
+        return [int(x) for x in out[:n.value]]
+
+    def stats(self):
+        st = _lib.SpecStats()
+        check(self.lib.fl_generator_stats(self.h, C.byref(st)), self.b.ctx)
+        return st.attempts, st.drafted, st.accepted
+
+    @property
+    def position(self) -> int:
+        return self.lib.fl_generator_position(self.h)
+
+    def tokens(self) -> list:
+        n = self.lib.fl_generator_tokens(self.h, None, 0)
+        out = np.empty(max(n, 1), np.uint32)
+        self.lib.fl_generator_tokens(self.h, out.ctypes.data, n)
+        return [int(x) for x in out[:n]]
+
+
+def sample_logits(backend: "HipBackend", logits_dev, temperature=0.7, top_p=0.9, top_k=40, repeat_penalty=1.1,
+                  min_p=0.0, prev=(), u=0.5) -> int:
+    """fl_op_sample over a device logits row (a torch tensor)."""
+    params = _lib.SamplingParams(temperature, top_p, int(top_k), repeat_penalty, min_p, 0)
+    prev = np.ascontiguousarray(prev, np.uint32)
+    t = C.c_int32()
+    check(backend.lib.fl_op_sample(backend.ctx, logits_dev.data_ptr(), logits_dev.numel(), C.byref(params),
+                                   prev.ctypes.data if prev.size else None, prev.size, u, C.byref(t)), backend.ctx)
+    return t.value
+
+
+__all__ = ["HipBackend", "Generator", "Weight", "FlareError", "sample_logits"]

@@ -33,7 +33,9 @@ def _run(cmd: list[str]) -> None:
     subprocess.run(cmd, check=True)
 
 
-HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "attn.hip", "verify.hip", "mvo.hip", "seq.hip"]
+HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "attn.hip", "verify.hip", "mvo.hip", "seq.hip",
+               "sample.hip"]
+HOST_SOURCES = ["synth.cpp", "generate.cpp"]
 
 
 def build(verbose: bool = True) -> str:
@@ -48,9 +50,10 @@ def build(verbose: bool = True) -> str:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         jobs.append([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
-    syn_obj = os.path.join(BUILD, "synth.o")
-    jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "synth.cpp"), "-o", syn_obj])
-    objs.append(syn_obj)
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+        jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(workers) as ex:
         for f in [ex.submit(_run, j) for j in jobs]:

@@ -28,6 +28,7 @@
 #include "attm_kernels.h"
 #include "launch.h"
 #include "mvo_kernels.h"
+#include "sample_args.h"
 
 using namespace fl;
 
@@ -293,6 +294,13 @@ struct fl_ctx {
     float *scratch = nullptr;     // device address of `scratch` on this context's GPU
     float *seq_scores = nullptr;  // [num_heads][kv_slots] attention scores (exact mode)
     float *seq_xn = nullptr;      // [hidden] final-normed vector (exact mode)
+    // device sampler (allocated on first use, for rows of up to sample_cap)
+    int sample_cap = 0, sample_prev_cap = 0;
+    float *sp = nullptr;
+    int *scounts = nullptr, *sprev = nullptr, *sstate = nullptr, *svals = nullptr, *ssvals = nullptr;
+    unsigned *skeys = nullptr, *sskeys = nullptr;
+    void *ssort = nullptr;
+    size_t ssort_bytes = 0;
 };
 
 constexpr int kVerifyMaxKsplit = 16;
@@ -710,7 +718,9 @@ void fl_ctx_destroy(fl_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     model_release(ctx);
-    void *ptrs[] = {ctx->d_pos, ctx->d_rope_row, ctx->d_part, ctx->d_counters, ctx->d_slot};
+    void *ptrs[] = {ctx->d_pos, ctx->d_rope_row, ctx->d_part, ctx->d_counters, ctx->d_slot,
+                    ctx->sp, ctx->scounts, ctx->sprev, ctx->sstate, ctx->svals, ctx->ssvals, ctx->skeys,
+                    ctx->sskeys, ctx->ssort};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -1486,6 +1496,40 @@ int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen, ui
     return 0;
 }
 
+int fl_decode_run(fl_ctx *ctx, uint32_t token, int pos, int n_steps, uint32_t *out_tokens) {
+    if (!ctx || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    if (n_steps <= 0) return fail(ctx, FL_E_INVALID, "n_steps must be positive");
+    if (pos < 0 || pos + n_steps > c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "steps [%d, %d) outside the KV cache (max_seq_len %d)", pos, pos + n_steps,
+                    c.max_seq_len);
+    if ((int)token >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", token);
+    int rc = ensure_graph(ctx);
+    if (rc) return rc;
+    const int tok = (int)token;
+    DevState hs{};
+    hs.step = pos;
+    hs.pos = pos;
+    hs.n_prompt = pos + 1;  // step `pos` reads tokens[pos]; later steps take the previous argmax
+    HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + pos, &tok, 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
+    for (int s = 0; s < n_steps; s++) {
+        rc = launch_step(ctx);
+        if (rc) return rc;
+    }
+    std::vector<int> gen((size_t)std::max(n_steps - 1, 1));
+    DevState out{};
+    if (n_steps > 1)
+        HIPCHK(ctx, hipMemcpyAsync(gen.data(), ctx->tokens + pos + 1, (size_t)(n_steps - 1) * 4,
+                                   hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(&out, ctx->st, sizeof out, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    for (int i = 0; i < n_steps - 1; i++) out_tokens[i] = (uint32_t)gen[i];
+    out_tokens[n_steps - 1] = 0xFFFFFFFFu - (uint32_t)(out.argmax & 0xFFFFFFFFull);
+    return 0;
+}
+
 int fl_decode_continue(fl_ctx *ctx, int n_steps) {
     if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
     if (!ctx->graph_ready) return fail(ctx, FL_E_STATE, "fl_generate must run first");
@@ -1796,7 +1840,12 @@ int fl_op_batched_matvec_f32in(fl_ctx *ctx, const fl_weight *w, int n_tokens, co
 // The verify pass for M tokens at the device positions vpos.. (tokens in
 // vtok, vslots cleared); dev_pos: the cache writers read the position from the
 // device too (graph capture), pos0 is then only used for planning checks.
-static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
+// What a pass of enqueue_verify produces: the greedy key of every token
+// (speculative verify), nothing (prefill chunks before the last), or the key
+// / the logits of the last token only (the last prefill chunk).
+enum { VOUT_ALL = 0, VOUT_NONE = 1, VOUT_LAST_ARGMAX = 2, VOUT_LAST_LOGITS = 3 };
+
+static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mode = VOUT_ALL) {
     const fl_model_config &c = ctx->cfg;
     int rc;
     const int H = c.hidden_dim, D = c.head_dim, G = c.num_heads / c.num_kv_heads;
@@ -1903,10 +1952,21 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
         if (rc) return rc;
     }
     HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));
+    if (out_mode == VOUT_NONE) return 0;
     // output projection + fused argmax per token (forward_greedy, model.rs:1898-1932)
     const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
     const bool q8out = !ctx->tied && ((O.format == FL_Q8_0 && ctx->layer_fmt == FL_Q8_0) ||
                                       (O.format == FL_Q4K && ctx->layer_fmt == FL_Q4K));
+    if (out_mode == VOUT_LAST_ARGMAX || out_mode == VOUT_LAST_LOGITS) {
+        // the last token only (forward_prefill returns its logits, model.rs:2578-3040)
+        const float *xt = xa + (size_t)(M - 1) * H;
+        const int epi = out_mode == VOUT_LAST_LOGITS ? EPI_STORE : EPI_ARGMAX;
+        if (O.format == FL_Q4K && !q8out) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
+        if (q8out)
+            return launch_q8in(ctx, O, PRO_NORMQ1, epi, xt, ctx->out_norm, eps, nullptr, nullptr, nullptr, ctx->logits,
+                               ctx->vslots + (M - 1));
+        return launch_f32in(ctx, O, 1, epi, xt, ctx->out_norm, eps, ctx->logits, ctx->vslots + (M - 1));
+    }
     if (!q8out && O.format != FL_F32) {
         if (O.format == FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "Q4_K output with Q8_0 layers");
         // all M tokens in one MFMA launch (M <= 8 per launch)
@@ -1929,37 +1989,52 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos) {
     return 0;
 }
 
-int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
-    if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+// Decode a packed argmax key (value bits << 32 | ~index) into (index, value).
+static void unpack_key(unsigned long long k, int32_t *tok, float *val) {
+    if (tok) *tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+    if (val) {
+        uint32_t u = (uint32_t)(k >> 32);
+        u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+        std::memcpy(val, &u, 4);
+    }
+}
+
+// Checks shared by fl_verify and fl_prefill for a pass of M tokens at pos0.
+static int verify_check(fl_ctx *ctx, const uint32_t *tokens, int M, int pos0) {
     if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
     const fl_model_config &c = ctx->cfg;
-    const int M = n_tokens;
-    if (M < 1 || M > kVerifyMaxTokens) return fail(ctx, FL_E_INVALID, "verify batch of %d tokens (1..%d)", M, kVerifyMaxTokens);
     if (pos0 < 0 || pos0 + M > c.max_seq_len)
         return fail(ctx, FL_E_INVALID, "positions [%d, %d) outside the KV cache (max_seq_len %d)", pos0, pos0 + M,
                     c.max_seq_len);
-    if (M * c.num_kv_heads > 1024) return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
+    if (std::min(M, kVerifyMaxTokens) * c.num_kv_heads > 1024)
+        return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
     for (int i = 0; i < M; i++)
         if ((int)tokens[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", tokens[i]);
-    int rc = verify_alloc(ctx);
-    if (rc) return rc;
+    return verify_alloc(ctx);
+}
+
+// One pass of M (<= kVerifyMaxTokens) tokens at pos0; the token ids are
+// already in ctx->vtok.  `*pos_host` must stay valid until the stream
+// reaches the pass (the position is copied to the device asynchronously).
+static int run_verify_pass(fl_ctx *ctx, int M, const int *pos_host, int out_mode) {
+    const fl_model_config &c = ctx->cfg;
     hipStream_t st = ctx->stream;
     const int G = c.num_heads / c.num_kv_heads;
-    std::vector<int> tk(tokens, tokens + M);
-    HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data(), (size_t)M * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, &pos0, 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
-    rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, pos_host, 4, hipMemcpyHostToDevice, st));
+    if (out_mode != VOUT_NONE) HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
+    int rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
     if (rc) return rc;
-    // F32 / F16 / Q8 caches: one captured graph per batch size (the positions
-    // are read from the device); KIVI plans its group work from the host.
-    // FLARE_NO_VERIFY_GRAPH (read per call): enqueue the kernels directly
+    // F32 / F16 / Q8 caches: one captured graph per (batch size, output
+    // mode) (the positions are read from the device); KIVI plans its group
+    // work from the host.  FLARE_NO_VERIFY_GRAPH (read per call): enqueue the
+    // kernels directly
     const bool graph = use_graph() && ctx->verify_graph && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr;
     if (graph && ctx->kv_format != FL_KV_KIVI2) {
-        auto it = ctx->vgraphs.find(M);
+        const int key = M + 256 * out_mode;
+        auto it = ctx->vgraphs.find(key);
         if (it == ctx->vgraphs.end()) {
             HIPCHK(ctx, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-            rc = enqueue_verify(ctx, M, pos0, true);
+            rc = enqueue_verify(ctx, M, *pos_host, true, out_mode);
             hipGraph_t g = nullptr;
             const hipError_t e = hipStreamEndCapture(st, &g);
             if (rc) {
@@ -1971,26 +2046,201 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
             const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (ei != hipSuccess) return fail(ctx, FL_E_HIP, "verify graph instantiate: %s", hipGetErrorString(ei));
-            it = ctx->vgraphs.emplace(M, ge).first;
+            it = ctx->vgraphs.emplace(key, ge).first;
         }
         HIPCHK(ctx, hipGraphLaunch(it->second, st));
-    } else {
-        rc = enqueue_verify(ctx, M, pos0, false);
-        if (rc) return rc;
+        return 0;
     }
+    return enqueue_verify(ctx, M, *pos_host, false, out_mode);
+}
+
+int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens, float *out_vals) {
+    if (!ctx || !tokens || !out_tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    const int M = n_tokens;
+    if (M < 1 || M > kVerifyMaxTokens) return fail(ctx, FL_E_INVALID, "verify batch of %d tokens (1..%d)", M, kVerifyMaxTokens);
+    int rc = verify_check(ctx, tokens, M, pos0);
+    if (rc) return rc;
+    if (ctx->exact) {
+        // reference-order mode: the reference's own sequential verification
+        // (one forward_greedy per draft, generate.rs:244-312)
+        for (int t = 0; t < M; t++) {
+            rc = decode_step(ctx, tokens[t], nullptr, pos0 + t, nullptr, &out_tokens[t], out_vals ? &out_vals[t] : nullptr);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    hipStream_t st = ctx->stream;
+    std::vector<int> tk(tokens, tokens + M);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data(), (size_t)M * 4, hipMemcpyHostToDevice, st));
+    rc = run_verify_pass(ctx, M, &pos0, VOUT_ALL);
+    if (rc) return rc;
     std::vector<unsigned long long> keys(M);
     HIPCHK(ctx, hipMemcpyAsync(keys.data(), ctx->vslots, (size_t)M * 8, hipMemcpyDeviceToHost, st));
     HIPCHK(ctx, hipStreamSynchronize(st));
-    for (int t = 0; t < M; t++) {
-        const unsigned long long k = keys[t];
-        out_tokens[t] = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
-        if (out_vals) {
-            uint32_t u = (uint32_t)(k >> 32);
-            u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
-            std::memcpy(&out_vals[t], &u, 4);
+    for (int t = 0; t < M; t++) unpack_key(keys[t], &out_tokens[t], out_vals ? &out_vals[t] : nullptr);
+    return 0;
+}
+
+int fl_prefill(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, float *out_logits, int32_t *out_token,
+               float *out_val) {
+    if (!ctx || !tokens) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n_tokens < 1) return fail(ctx, FL_E_INVALID, "prefill of %d tokens", n_tokens);
+    int rc = verify_check(ctx, tokens, n_tokens, pos0);
+    if (rc) return rc;
+    if (ctx->exact) {
+        // reference-order mode: the prompt as sequential decode steps, which
+        // forward_prefill equals (test_batched_prefill_matches_sequential,
+        // flare-core/src/generate.rs:657)
+        for (int i = 0; i + 1 < n_tokens; i++) {
+            rc = decode_step(ctx, tokens[i], nullptr, pos0 + i, nullptr, nullptr, nullptr);
+            if (rc) return rc;
         }
+        return decode_step(ctx, tokens[n_tokens - 1], nullptr, pos0 + n_tokens - 1, out_logits, out_token, out_val);
+    }
+    hipStream_t st = ctx->stream;
+    const int C = kVerifyMaxTokens;
+    const int nchunks = (n_tokens + C - 1) / C;
+    // host copies stay alive until the final synchronisation
+    std::vector<int> tk(tokens, tokens + n_tokens), pos(nchunks);
+    for (int k = 0; k < nchunks; k++) {
+        const int t0 = k * C, M = std::min(C, n_tokens - t0);
+        pos[k] = pos0 + t0;
+        HIPCHK(ctx, hipMemcpyAsync(ctx->vtok, tk.data() + t0, (size_t)M * 4, hipMemcpyHostToDevice, st));
+        const int mode = k + 1 < nchunks ? VOUT_NONE : out_logits ? VOUT_LAST_LOGITS : VOUT_LAST_ARGMAX;
+        rc = run_verify_pass(ctx, M, &pos[k], mode);
+        if (rc) return rc;
+    }
+    const int Mlast = n_tokens - (nchunks - 1) * C;
+    unsigned long long key = 0;
+    HIPCHK(ctx, hipMemcpyAsync(&key, ctx->vslots + (Mlast - 1), 8, hipMemcpyDeviceToHost, st));
+    if (out_logits)
+        HIPCHK(ctx, hipMemcpyAsync(out_logits, ctx->logits, (size_t)ctx->cfg.vocab_size * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(ctx, hipStreamSynchronize(st));
+    if (out_logits) {
+        int bi = 0;
+        float bv = -INFINITY;
+        for (int i = 0; i < ctx->cfg.vocab_size; i++)
+            if (out_logits[i] > bv) { bv = out_logits[i]; bi = i; }
+        if (out_token) *out_token = bi;
+        if (out_val) *out_val = bv;
+    } else {
+        unpack_key(key, out_token, out_val);
     }
     return 0;
+}
+
+// ---- device sampling ----------------------------------------------------------
+
+static int sample_alloc(fl_ctx *ctx, int n, int n_prev) {
+    if (n > ctx->sample_cap) {
+        void **bufs[] = {(void **)&ctx->sp, (void **)&ctx->scounts, (void **)&ctx->svals, (void **)&ctx->ssvals,
+                         (void **)&ctx->skeys, (void **)&ctx->sskeys, &ctx->ssort};
+        for (void **b : bufs) {
+            if (*b) (void)hipFree(*b);
+            *b = nullptr;
+        }
+        ctx->sample_cap = 0;
+        ALLOC(ctx, ctx->sp, (size_t)n * 4);
+        ALLOC(ctx, ctx->scounts, (size_t)n * 4);
+        ALLOC(ctx, ctx->svals, (size_t)n * 4);
+        ALLOC(ctx, ctx->ssvals, (size_t)n * 4);
+        ALLOC(ctx, ctx->skeys, (size_t)n * 4);
+        ALLOC(ctx, ctx->sskeys, (size_t)n * 4);
+        ctx->ssort_bytes = std::max<size_t>(fl::sample_sort_bytes(n), 256);
+        ALLOC(ctx, ctx->ssort, ctx->ssort_bytes);
+        HIPCHK(ctx, hipMemset(ctx->scounts, 0, (size_t)n * 4));  // the sampler leaves them at zero
+        ctx->sample_cap = n;
+    }
+    if (!ctx->sstate) ALLOC(ctx, ctx->sstate, 16);
+    if (n_prev > ctx->sample_prev_cap) {
+        if (ctx->sprev) (void)hipFree(ctx->sprev);
+        ctx->sprev = nullptr;
+        ctx->sample_prev_cap = 0;
+        const int cap = std::max(n_prev, 1024);
+        ALLOC(ctx, ctx->sprev, (size_t)cap * 4);
+        ctx->sample_prev_cap = cap;
+    }
+    return 0;
+}
+
+// Enqueue the sampler over `logits` (device) and read the token back.
+static int sample_logits(fl_ctx *ctx, const float *logits, int n, const fl_sampling_params *sp,
+                         const uint32_t *prev, int n_prev, float u, int32_t *out) {
+    if (!sp || !out || (n_prev > 0 && !prev)) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n < 1 || n_prev < 0) return fail(ctx, FL_E_INVALID, "sampling %d logits with %d previous tokens", n, n_prev);
+    int rc = sample_alloc(ctx, n, n_prev);
+    if (rc) return rc;
+    fl::SampleArgs a{};
+    a.logits = logits;
+    a.n = n;
+    a.p = ctx->sp;
+    a.counts = ctx->scounts;
+    a.prev = ctx->sprev;
+    a.n_prev = n_prev;
+    a.penalty = sp->repeat_penalty;
+    a.temperature = sp->temperature;
+    a.top_p = sp->top_p;
+    a.min_p = sp->min_p;
+    // the priority of Generator::step (generate.rs:220-230)
+    if (sp->temperature == 0.0f) {
+        a.mode = fl::SM_GREEDY;
+        a.K = 1;
+    } else if (sp->top_p < 1.0f) {
+        a.mode = fl::SM_TOP_P;
+        a.K = std::min(512, n);
+    } else if (sp->min_p > 0.0f) {
+        a.mode = fl::SM_MIN_P;
+        a.K = n;
+    } else if (sp->top_k > 0) {
+        a.mode = fl::SM_TOP_K;
+        a.K = std::max(1, std::min(sp->top_k, n));
+    } else {
+        a.mode = fl::SM_TOP_P;  // sample_top_p(logits, 1.0, rng_val)
+        a.top_p = 1.0f;
+        a.K = std::min(512, n);
+    }
+    a.u = u;
+    a.exact = ctx->exact ? 1 : 0;
+    a.keys = ctx->skeys;
+    a.vals = ctx->svals;
+    a.skeys = ctx->sskeys;
+    a.svals = ctx->ssvals;
+    a.state = ctx->sstate;
+    // host copy alive until the synchronisation below
+    std::vector<int> pv(prev, prev + n_prev);
+    if (n_prev > 0) HIPCHK(ctx, hipMemcpyAsync(ctx->sprev, pv.data(), (size_t)n_prev * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, fl::launch_sample(ctx->stream, a, ctx->ssort, ctx->ssort_bytes));
+    int st[4] = {0, 0, 0, 0};
+    HIPCHK(ctx, hipMemcpyAsync(st, ctx->sstate, 16, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
+    *out = st[0];
+    return 0;
+}
+
+int fl_op_sample(fl_ctx *ctx, const float *logits, int n, const fl_sampling_params *params, const uint32_t *prev_tokens,
+                 int n_prev, float rng_val, int32_t *out_token) {
+    if (!ctx || !logits) return fail(ctx, FL_E_INVALID, "null argument");
+    return sample_logits(ctx, logits, n, params, prev_tokens, n_prev, rng_val, out_token);
+}
+
+int fl_decode_step_sample(fl_ctx *ctx, uint32_t token, int pos, const fl_sampling_params *params,
+                          const uint32_t *prev_tokens, int n_prev, float rng_val, int32_t *out_token) {
+    if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
+    if (!ctx->have_weights) return fail(ctx, FL_E_STATE, "weights not uploaded");
+    const fl_model_config &c = ctx->cfg;
+    if (pos < 0 || pos >= c.max_seq_len)
+        return fail(ctx, FL_E_INVALID, "pos %d outside the KV cache (max_seq_len %d)", pos, c.max_seq_len);
+    if ((int)token >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", token);
+    const int tok = (int)token;
+    DevState hs{};
+    hs.step = pos;
+    hs.pos = pos;
+    hs.n_prompt = pos + 1;
+    HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + pos, &tok, 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
+    int rc = enqueue_step(ctx, true);
+    if (rc) return rc;
+    return sample_logits(ctx, ctx->logits, c.vocab_size, params, prev_tokens, n_prev, rng_val, out_token);
 }
 
 // Launch `iters` copies of one layer kernel on the context stream, cycling

@@ -121,8 +121,11 @@ const char *fl_backend_name(void);
  * the f32 output dot in column order -- so logits equal the CPU reference's
  * bit for bit.  The matvecs are the same streaming kernels with an in-order
  * fold; attention and the f32 output projection run simple sequential
- * kernels (slow).  F32 / F16 KV caches only.  Default: tree-order sums (fast;
- * outputs within 1e-3 relative). */
+ * kernels (slow).  fl_verify and fl_prefill then run their tokens as
+ * sequential decode steps (the reference's sequential verification; its
+ * forward_prefill equals sequential steps, generate.rs:657), and fl_op_sample
+ * sums in the reference's order.  F32 / F16 KV caches only.  Default:
+ * tree-order sums (fast; outputs within 1e-3 relative). */
 #define FL_OPT_EXACT 3
 int fl_set_option(fl_ctx *ctx, int option, int value);
 
@@ -279,12 +282,106 @@ int fl_generate(fl_ctx *ctx, const uint32_t *prompt, int n_prompt, int n_gen,
 int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32_t *out_tokens,
               float *out_vals);
 
+/* Model::forward_prefill (model.rs:2578-3040): n_tokens prompt tokens at
+ * positions pos0..pos0+n_tokens-1 in batched passes of up to 16 tokens (the
+ * fl_verify pass: int8-MFMA projections, causal attention over the cache
+ * and the tokens before each one in the batch, K/V written to the cache),
+ * then the output projection of the last token only.  The reference starts
+ * from an empty cache (pos0 = 0); pos0 > 0 continues a cache whose slots
+ * 0..pos0-1 are written.  out_logits (vocab_size host floats) may be NULL:
+ * then only the fused argmax runs; *out_token / *out_val (either may be
+ * NULL) receive the greedy token after the last prompt token. */
+int fl_prefill(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, float *out_logits,
+               int32_t *out_token, float *out_val);
+
+/* n_steps greedy steps (forward_greedy, model.rs:1872-1942) starting with
+ * `token` at position `pos`, device-resident (one HIP graph replay per step,
+ * one host synchronisation at the end): out_tokens[i] is the greedy token
+ * after step pos+i, which is the input of step pos+i+1.  The Generator's
+ * plain greedy steps (generate.rs:186-206) after fl_prefill. */
+int fl_decode_run(fl_ctx *ctx, uint32_t token, int pos, int n_steps, uint32_t *out_tokens);
+
 /* Enqueue n_steps more device-resident greedy steps after fl_generate (no
  * host synchronisation; tokens land in the device token buffer). */
 int fl_decode_continue(fl_ctx *ctx, int n_steps);
 /* Copy tokens[start, start+n) of the device token buffer (prompt tokens
  * followed by generated tokens) to the host. */
 int fl_read_tokens(fl_ctx *ctx, int start, int n, uint32_t *out);
+
+/* ---- sampling (flare-core/src/sampling.rs) ------------------------------------ */
+/* SamplingParams (sampling.rs:19-54) without the self-speculation fields
+ * (layer-skipping drafts are not built). */
+typedef struct {
+    float temperature, top_p;
+    int top_k;
+    float repeat_penalty, min_p;
+    int speculative; /* n-gram speculative decoding (greedy only) */
+} fl_sampling_params;
+/* SamplingParams::default (sampling.rs:56-70). */
+void fl_sampling_params_default(fl_sampling_params *p);
+/* One token from a logits row on the device, as Generator::step does after
+ * its forward (generate.rs:210-230): apply_repeat_penalty over prev_tokens
+ * (host array, every occurrence counts), apply_temperature, then
+ * sample_greedy (temperature 0) / sample_top_p / sample_min_p / sample_top_k
+ * by the reference's priority, with rng_val as the uniform draw.  logits: n
+ * device floats (left unchanged).  Candidate sets are ordered by descending
+ * probability, ties by ascending index (top-k: the reference walks them in
+ * select_nth_unstable's order instead).  Synchronises. */
+int fl_op_sample(fl_ctx *ctx, const float *logits, int n, const fl_sampling_params *params,
+                 const uint32_t *prev_tokens, int n_prev, float rng_val, int32_t *out_token);
+/* forward_single_token_gpu (model.rs:555) for `token` at `pos`, then
+ * fl_op_sample over the device logits: no logits readback. */
+int fl_decode_step_sample(fl_ctx *ctx, uint32_t token, int pos, const fl_sampling_params *params,
+                          const uint32_t *prev_tokens, int n_prev, float rng_val, int32_t *out_token);
+
+/* ---- generation loop (flare-core/src/generate.rs), host code ----------------- */
+/* NgramCache (generate.rs:37-103): n = 2, 3, 4; at most 5 drafts; cleared
+ * when it exceeds 10 000 entries.  Host only (no GPU needed). */
+typedef struct fl_ngram fl_ngram;
+fl_ngram *fl_ngram_create(void);
+void fl_ngram_destroy(fl_ngram *c);
+/* record (generate.rs:55-75): the n-grams ending at tokens[n-1]. */
+void fl_ngram_record(fl_ngram *c, const uint32_t *tokens, size_t n);
+/* record_prompt_ngrams (generate.rs:166-182): every n-gram of tokens. */
+void fl_ngram_record_all(fl_ngram *c, const uint32_t *tokens, size_t n);
+/* lookup_drafts (generate.rs:79-92): writes up to 5 drafts, returns the count. */
+int fl_ngram_lookup(const fl_ngram *c, const uint32_t *tokens, size_t n, uint32_t *out);
+size_t fl_ngram_entries(const fl_ngram *c);
+
+/* SpeculativeStats (generate.rs:22-30). */
+typedef struct {
+    uint64_t attempts, drafted, accepted;
+} fl_spec_stats;
+typedef float (*fl_rng_fn)(void *user);
+/* on_token (generate.rs:409-416): return 0 to stop. */
+typedef int (*fl_token_fn)(uint32_t token, size_t step, void *user);
+/* Generator (generate.rs:106-560) over a context holding a model, positions
+ * from 0.  Speculative steps verify the n-gram drafts in one fl_verify pass
+ * over the inputs the reference's sequential forwards take
+ * ([last, d0, .., d(k-2)]); accepted tokens, positions and statistics are
+ * the reference's.  Self-speculation (layer skipping) is not built. */
+typedef struct fl_generator fl_generator;
+int fl_generator_create(fl_ctx *ctx, const fl_sampling_params *params, fl_generator **out);
+void fl_generator_destroy(fl_generator *g);
+/* Generator::prefill (generate.rs:139-163) through fl_prefill; out_logits
+ * (vocab floats) may be NULL. */
+int fl_generator_prefill(fl_generator *g, const uint32_t *prompt, int n, float *out_logits);
+/* Generator::step (generate.rs:186-238): the forward of the last token at
+ * the current position, then greedy / sampled token. */
+int fl_generator_step(fl_generator *g, float rng_val, uint32_t *out_token);
+/* Generator::generate (generate.rs:409-531): prefill, then up to max_tokens
+ * tokens (speculative steps when enabled and greedy), stopping at eos (< 0:
+ * none) or when on_token returns 0.  out_tokens holds max_tokens entries;
+ * *n_out = tokens written.  rng / on_token may be NULL. */
+int fl_generator_generate(fl_generator *g, const uint32_t *prompt, int n_prompt, int max_tokens,
+                          int64_t eos, fl_rng_fn rng, void *rng_user, fl_token_fn on_token,
+                          void *token_user, uint32_t *out_tokens, int *n_out);
+/* speculative_stats (generate.rs:555-557). */
+int fl_generator_stats(const fl_generator *g, fl_spec_stats *out);
+/* position / tokens (generate.rs:547-553): tokens returns the count and
+ * copies up to cap of them when out != NULL. */
+int fl_generator_position(const fl_generator *g);
+int fl_generator_tokens(const fl_generator *g, uint32_t *out, int cap);
 
 /* ---- measurement helpers ---------------------------------------------------- */
 /* Enqueue `iters` launches of one decode kernel for `which` (0=qkv, 1=wo,

@@ -959,3 +959,155 @@ void or_generate_greedy(or_model *m, const uint32_t *prompt, size_t n_prompt, si
         if (i + 1 < n_gen) tok = (uint32_t)or_forward_greedy(m, tok, pos++, NULL);
     }
 }
+
+
+/* ========================================================================
+ * Sampling: flare-core/src/sampling.rs
+ * ======================================================================== */
+
+typedef struct {
+    float p;
+    uint32_t idx;
+} or_cand;
+
+/* descending probability; ties by ascending index (the reference's
+ * sort_unstable_by leaves equal probabilities in an unspecified order) */
+static int or_cand_cmp(const void *a, const void *b) {
+    const or_cand *x = (const or_cand *)a, *y = (const or_cand *)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx ? 1 : 0);
+}
+
+/* sample_greedy (sampling.rs:101-111) */
+static uint32_t or_sample_greedy(const float *v, size_t n) {
+    uint32_t best = 0;
+    float bv = -INFINITY;
+    for (size_t i = 0; i < n; i++)
+        if (v[i] > bv) {
+            bv = v[i];
+            best = (uint32_t)i;
+        }
+    return best;
+}
+
+/* The walk shared by the three samplers over a descending candidate list:
+ * total = sequential sum, threshold = u * total, first prefix >= threshold
+ * (sampling.rs:170-180, 206-216, 257-267). */
+static uint32_t or_walk(const or_cand *c, size_t L, float u) {
+    float total = 0.0f;
+    for (size_t i = 0; i < L; i++) total += c[i].p;
+    const float thr = u * total;
+    float acc = 0.0f;
+    for (size_t i = 0; i < L; i++) {
+        acc += c[i].p;
+        if (acc >= thr) return c[i].idx;
+    }
+    return c[L - 1].idx;
+}
+
+int64_t or_sample(const float *logits, size_t n, float temperature, float top_p, int top_k,
+                  float repeat_penalty, float min_p, const uint32_t *prev, size_t n_prev,
+                  float rng_val) {
+    if (n == 0) return -1;
+    float *v = (float *)malloc(n * sizeof(float));
+    or_cand *c = (or_cand *)malloc(n * sizeof(or_cand));
+    memcpy(v, logits, n * sizeof(float));
+    /* apply_repeat_penalty (sampling.rs:83-96) */
+    if (repeat_penalty != 1.0f)
+        for (size_t j = 0; j < n_prev; j++) {
+            const size_t t = prev[j];
+            if (t < n) v[t] = v[t] > 0.0f ? v[t] / repeat_penalty : v[t] * repeat_penalty;
+        }
+    /* apply_temperature (sampling.rs:73-81) */
+    if (temperature != 0.0f && temperature != 1.0f) {
+        const float inv = 1.0f / temperature;
+        for (size_t i = 0; i < n; i++) v[i] *= inv;
+    }
+    int64_t out;
+    if (temperature == 0.0f) {
+        out = or_sample_greedy(v, n);
+        goto done;
+    }
+    {
+        /* softmax pieces: max fold, exps, sequential sum (sampling.rs:115-119, 132-135) */
+        float mx = -INFINITY;
+        for (size_t i = 0; i < n; i++) mx = fmaxf(mx, v[i]);
+        float sum = 0.0f;
+        for (size_t i = 0; i < n; i++) {
+            v[i] = expf(v[i] - mx);
+            sum += v[i];
+        }
+        const int mode = top_p < 1.0f ? 1 : (min_p > 0.0f ? 2 : (top_k > 0 ? 3 : 1));
+        const float tp = top_p < 1.0f ? top_p : 1.0f;
+        if (mode == 2) {
+            /* sample_min_p (sampling.rs:228-268): softmax() divides */
+            float pmax = 0.0f;
+            for (size_t i = 0; i < n; i++) {
+                v[i] = v[i] / sum;
+                pmax = fmaxf(pmax, v[i]);
+            }
+            const float thr = min_p * pmax;
+            size_t L = 0;
+            for (size_t i = 0; i < n; i++)
+                if (v[i] >= thr) {
+                    c[L].p = v[i];
+                    c[L].idx = (uint32_t)i;
+                    L++;
+                }
+            if (L == 0) {
+                /* sample_greedy(logits): the penalized, scaled logits */
+                memcpy(v, logits, n * sizeof(float));
+                out = -2;
+                goto fallback;
+            }
+            qsort(c, L, sizeof(or_cand), or_cand_cmp);
+            out = or_walk(c, L, rng_val);
+            goto done;
+        }
+        const float inv_sum = 1.0f / sum;
+        for (size_t i = 0; i < n; i++) {
+            c[i].p = v[i] * inv_sum;
+            c[i].idx = (uint32_t)i;
+        }
+        /* the K largest (select_nth_unstable_by + truncate), ordered */
+        qsort(c, n, sizeof(or_cand), or_cand_cmp);
+        if (mode == 1) {
+            /* sample_top_p (sampling.rs:131-181): INITIAL_K = 512, cumulative cut */
+            const size_t K = n < 512 ? n : 512;
+            size_t cutoff = K;
+            float cum = 0.0f;
+            for (size_t i = 0; i < K; i++) {
+                cum += c[i].p;
+                if (cum >= tp) {
+                    cutoff = i + 1;
+                    break;
+                }
+            }
+            out = or_walk(c, cutoff, rng_val);
+        } else {
+            /* sample_top_k (sampling.rs:186-217) */
+            size_t K = (size_t)top_k < n ? (size_t)top_k : n;
+            if (K < 1) K = 1;
+            out = or_walk(c, K, rng_val);
+        }
+        goto done;
+    }
+fallback:
+    /* min-p with no candidate: greedy over the transformed logits */
+    if (repeat_penalty != 1.0f)
+        for (size_t j = 0; j < n_prev; j++) {
+            const size_t t = prev[j];
+            if (t < n) v[t] = v[t] > 0.0f ? v[t] / repeat_penalty : v[t] * repeat_penalty;
+        }
+    {
+        const float inv = 1.0f / temperature;
+        if (temperature != 1.0f)
+            for (size_t i = 0; i < n; i++) v[i] *= inv;
+    }
+    out = or_sample_greedy(v, n);
+done:
+    free(v);
+    free(c);
+    return out;
+}

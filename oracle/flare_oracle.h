@@ -133,6 +133,18 @@ const float *or_model_final_normed(const or_model *m);
 void or_generate_greedy(or_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                         uint32_t *out);
 
+/* ---- sampling (flare-core/src/sampling.rs) ----------------------------- */
+/* Generator::step's transforms and sampler (generate.rs:210-230) on a copy
+ * of logits[n]: apply_repeat_penalty (sampling.rs:83-96) over prev[n_prev],
+ * apply_temperature (73-81), then sample_greedy (101-111) when temperature
+ * is 0, else sample_top_p (131-181) when top_p < 1, else sample_min_p
+ * (228-268) when min_p > 0, else sample_top_k (186-217) when top_k > 0, else
+ * sample_top_p(1.0).  rng_val is the uniform draw.  Candidate sets are
+ * ordered by descending probability, ties by ascending index. */
+int64_t or_sample(const float *logits, size_t n, float temperature, float top_p, int top_k,
+                  float repeat_penalty, float min_p, const uint32_t *prev, size_t n_prev,
+                  float rng_val);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,7 @@ def lib() -> C.CDLL:
             "or_forward_logits": (None, [vp, C.c_uint32, sz, vp]),
             "or_model_final_normed": (C.POINTER(f32), [vp]),
             "or_generate_greedy": (None, [vp, vp, sz, sz, vp]),
+            "or_sample": (i64, [vp, sz, f32, f32, C.c_int, f32, f32, vp, sz, f32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -253,6 +254,15 @@ def kivi_quantize_to_packed(v: np.ndarray):
     s, m = C.c_float(), C.c_float()
     lib().or_kivi_quantize_to_packed(_p(v), v.size, _p(packed), C.byref(s), C.byref(m))
     return packed, s.value, m.value
+
+
+def sample(logits, temperature=0.7, top_p=0.9, top_k=40, repeat_penalty=1.1, min_p=0.0, prev=(), u=0.5) -> int:
+    """Generator::step's penalty, temperature and sampler (generate.rs:210-230,
+    sampling.rs); defaults are SamplingParams::default."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    prev = np.ascontiguousarray(prev, np.uint32)
+    return int(lib().or_sample(_p(logits), logits.size, temperature, top_p, int(top_k), repeat_penalty, min_p,
+                               _p(prev) if prev.size else None, prev.size, u))
 
 
 # ---- whole model -------------------------------------------------------------
