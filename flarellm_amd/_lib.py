@@ -141,6 +141,22 @@ SIGNATURES = {
     "fl_generator_stats": (i32, [vp, vp]),
     "fl_generator_position": (i32, [vp]),
     "fl_generator_tokens": (i32, [vp, vp, i32]),
+    "fl_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "fl_gguf_open_memory": (i32, [vp, sz, C.POINTER(vp)]),
+    "fl_gguf_close": (None, [vp]),
+    "fl_gguf_version": (i32, [vp]),
+    "fl_gguf_data_offset": (C.c_uint64, [vp]),
+    "fl_gguf_tensor_count": (i32, [vp]),
+    "fl_gguf_find_tensor": (i32, [vp, C.c_char_p]),
+    "fl_gguf_tensor_info": (i32, [vp, i32, C.POINTER(C.c_char_p), C.POINTER(i32), vp, C.POINTER(C.c_uint32),
+                                   C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "fl_gguf_meta_u64": (i32, [vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "fl_gguf_meta_f32": (i32, [vp, C.c_char_p, C.POINTER(f32)]),
+    "fl_gguf_meta_str": (C.c_char_p, [vp, C.c_char_p]),
+    "fl_gguf_model_config": (i32, [vp, C.POINTER(ModelConfig), C.POINTER(i32)]),
+    "fl_gguf_raw_weight": (i32, [vp, C.c_char_p, C.POINTER(RawWeight)]),
+    "fl_gguf_tensor_f32": (i32, [vp, C.c_char_p, vp, sz]),
+    "fl_model_load_gguf": (i32, [vp, vp, i32, i32]),
     "fl_bench_layer_kernel": (i32, [vp, i32, i32, i32, C.POINTER(C.c_double)]),
     "fl_bench_kernel_name": (C.c_char_p, [vp, i32]),
     "fl_synth_normal": (None, [C.c_uint64, C.c_uint64, sz, f32, f32, vp]),

@@ -274,6 +274,28 @@ class HipBackend:
         check(self.lib.fl_upload_weights(self.ctx, raws, an, fn, model.output_norm.ctypes.data, C.byref(emb),
                                          C.byref(out) if out is not None else None), self.ctx)
 
+    def load_gguf(self, path: str, kv_format: int = FL_KV_F16, max_seq_len: int = 0) -> ModelSpec:
+        """init_gpu_kv_cache + upload_weights_to_gpu from a GGUF file
+        (fl_model_load_gguf: memory-mapped, weights streamed from the
+        mapping).  Returns the model's spec."""
+        from .gguf import GgufFile
+
+        g = GgufFile(path)
+        try:
+            cfg, _arch = g.model_config()
+            fmts = {}
+            for name in ("blk.0.attn_q.weight", "token_embd.weight", "output.weight"):
+                if g.find_tensor(name) >= 0:
+                    fmts[name] = g.raw_weight(name)[1]
+            check(self.lib.fl_model_load_gguf(self.ctx, g.h, kv_format, max_seq_len), self.ctx)
+        finally:
+            g.close()
+        self.spec = ModelSpec(path, cfg.hidden_dim, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                              cfg.intermediate_dim, cfg.vocab_size, max_seq_len or cfg.max_seq_len,
+                              fmts["blk.0.attn_q.weight"], fmts["token_embd.weight"], fmts.get("output.weight"),
+                              cfg.rms_norm_eps, cfg.rope_theta)
+        return self.spec
+
     def has_gpu_weights(self) -> bool:
         return bool(self.lib.fl_has_weights(self.ctx))
 

@@ -326,6 +326,8 @@ static int fail(fl_ctx *ctx, int code, const char *fmt, ...) {
     return code;
 }
 
+int fl_host_fail(fl_ctx *ctx, int code, const char *msg) { return fail(ctx, code, "%s", msg); }
+
 #define HIPCHK(ctx, expr)                                                                   \
     do {                                                                                    \
         hipError_t e_ = (expr);                                                             \

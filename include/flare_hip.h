@@ -383,6 +383,47 @@ int fl_generator_stats(const fl_generator *g, fl_spec_stats *out);
 int fl_generator_position(const fl_generator *g);
 int fl_generator_tokens(const fl_generator *g, uint32_t *out, int cap);
 
+/* ---- GGUF files (flare-loader/src/gguf.rs), host code ------------------------- */
+/* A parsed GGUF v2 / v3 file (GgufFile::parse_header, gguf.rs:131-204): magic,
+ * version, the reference's limits (1e6 tensors, 1e5 metadata entries, 1 MiB
+ * strings), metadata, tensor infos, tensor data at the next 32-byte boundary.
+ * fl_gguf_open memory-maps the file read-only; fl_gguf_open_memory copies a
+ * buffer.  Errors: FL_E_INVALID / FL_E_UNSUPPORTED with fl_last_error(NULL). */
+typedef struct fl_gguf fl_gguf;
+int fl_gguf_open(const char *path, fl_gguf **out);
+int fl_gguf_open_memory(const void *data, size_t len, fl_gguf **out);
+void fl_gguf_close(fl_gguf *g);
+int fl_gguf_version(const fl_gguf *g);
+uint64_t fl_gguf_data_offset(const fl_gguf *g);
+int fl_gguf_tensor_count(const fl_gguf *g);
+/* find_tensor (gguf.rs:207): index, or -1. */
+int fl_gguf_find_tensor(const fl_gguf *g, const char *name);
+/* TensorInfo (gguf.rs:103-124): dims (up to 8) in file order [cols, rows, ...],
+ * ggml type id, offset within the data section, byte size (0 when the type's
+ * block size is unknown). */
+int fl_gguf_tensor_info(const fl_gguf *g, int index, const char **name, int *n_dims, uint64_t *dims,
+                        uint32_t *ggml_type, uint64_t *offset, uint64_t *nbytes);
+/* Metadata as an integer (meta_usize: u8/u16/u32/u64/i32/i64, gguf.rs:218),
+ * a float (meta_f32: f32/f64, gguf.rs:240) or a string (NULL if absent). */
+int fl_gguf_meta_u64(const fl_gguf *g, const char *key, uint64_t *out);
+int fl_gguf_meta_f32(const fl_gguf *g, const char *key, float *out);
+const char *fl_gguf_meta_str(const fl_gguf *g, const char *key);
+/* to_model_config (gguf.rs:241-346): llama / qwen2 / mistral / phi3 / gemma2
+ * (*arch = 0..4), vocab from token_embd.weight's second dimension, the
+ * reference's defaults for optional keys; head_dim = hidden / heads. */
+int fl_gguf_model_config(const fl_gguf *g, fl_model_config *cfg, int *arch);
+/* read_raw_weight (gguf.rs:616-653) without a copy: data points into the
+ * mapping; num_rows = last dimension, blocks_per_row = ceil(cols / block).
+ * Q8_0, Q4_K, Q6_K and F32 tensors (the formats of this backend's path). */
+int fl_gguf_raw_weight(const fl_gguf *g, const char *name, fl_raw_weight *out);
+/* An F32 / F16 tensor of n elements as f32 (norm weights). */
+int fl_gguf_tensor_f32(const fl_gguf *g, const char *name, float *out, size_t n);
+/* A whole model from a GGUF file: the config (max_seq_len > 0 overrides the
+ * context length), init_gpu_kv_cache, the blk.N.* weights and norms
+ * (weights.rs:30-66, gguf.rs:661-688; output tied to token_embd when absent),
+ * upload_weights_to_gpu streaming from the mapping.  llama / mistral only. */
+int fl_model_load_gguf(fl_ctx *ctx, const fl_gguf *g, int kv_format, int max_seq_len);
+
 /* ---- measurement helpers ---------------------------------------------------- */
 /* Enqueue `iters` launches of one decode kernel for `which` (0=qkv, 1=wo,
  * 2=gate_up, 3=down, 4=output argmax, 5=attention at the current position;
