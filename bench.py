@@ -284,37 +284,19 @@ def bench_verify_c5(args) -> int:
     return 0 if accepted else 1
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=40)
-    ap.add_argument("--kernel-iters", type=int, default=50)
-    ap.add_argument("--prompt", type=int, default=None,
-                    help="override the workload's prompt length (profiling runs of the weight-streaming kernels, "
-                         "whose bytes do not depend on the context; the reported line names the length used)")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the decode path "
-              "would shard by output rows / KV heads, which is not built here.", file=sys.stderr)
-        return 2
-
+def run_decode(args, config: str, with_cpu: bool) -> dict:
+    """One decode workload (c1 / c2 / c3): synthetic model, the prompt fed
+    through the decode step (untimed), warmup steps, then args.steps greedy
+    steps timed with HIP events on the context stream; per-kernel HBM rates
+    (HIP events around back-to-back launches); a timed fl_prefill of the same
+    prompt; optionally the CPU baseline.  Returns the JSON fields."""
     import torch
 
     from flarellm_amd import FL_KV_F16, FL_KV_F32
     from flarellm_amd import synth as S
     from flarellm_amd.backend import HipBackend
 
-    if args.config == "c4":
-        return bench_attention_c4(args)
-    if args.config == "c5":
-        return bench_verify_c5(args)
-    wl = WORKLOADS[args.config]
+    wl = WORKLOADS[config]
     spec = S.CONFIGS[wl["spec"]]
     n_prompt = wl["prompt"] if args.prompt is None else max(1, args.prompt)
     need = n_prompt + args.warmup + args.steps
@@ -322,19 +304,19 @@ def main() -> int:
         spec = S.replace(spec, max_seq=need)
     t0 = time.time()
     model = S.make_model(spec, seed=1)
-    log(f"[bench] synthetic {spec.name} built in {time.time() - t0:.1f}s")
+    log(f"[bench {config}] synthetic {spec.name} built in {time.time() - t0:.1f}s")
     b = HipBackend(0)
     b.init_gpu_kv_cache(spec, FL_KV_F16 if wl["kv"] == "f16" else FL_KV_F32)
     t0 = time.time()
     b.upload_weights_to_gpu(model)
-    log(f"[bench] uploaded in {time.time() - t0:.1f}s")
+    log(f"[bench {config}] uploaded in {time.time() - t0:.1f}s")
     prompt = S.random_tokens(7, n_prompt, spec.vocab)
 
     stream = torch.cuda.ExternalStream(b.stream)
     # prompt (untimed), then warmup steps
     t0 = time.time()
     b.generate(prompt, 1)
-    log(f"[bench] prompt of {n_prompt} tokens in {time.time() - t0:.2f}s")
+    log(f"[bench {config}] prompt of {n_prompt} tokens through the decode step in {time.time() - t0:.2f}s")
     b.decode_continue(args.warmup)
     b.sync()
     torch.cuda.synchronize()
@@ -351,7 +333,7 @@ def main() -> int:
     ms_per_step = ms_total / args.steps
     tok_s = 1000.0 / ms_per_step
     toks = b.read_tokens(n_prompt, 8)
-    log(f"[bench] {args.steps} steps: {ms_total:.2f} ms (wall {wall * 1e3:.2f} ms) -> {tok_s:.1f} tok/s; "
+    log(f"[bench {config}] {args.steps} steps: {ms_total:.2f} ms (wall {wall * 1e3:.2f} ms) -> {tok_s:.1f} tok/s; "
         f"first tokens {toks.tolist()}")
 
     # per-kernel HBM bandwidth: HIP events on the context stream around
@@ -372,18 +354,36 @@ def main() -> int:
         kernels[name] = {"kernel": b.bench_kernel_name(which), "us": round(us, 2), "bytes": int(nbytes),
                          "GB_s": round(nbytes / us / 1e3, 1)}
     for k, v in kernels.items():
-        log(f"[bench] {k:14s} {v['kernel']:12s} {v['us']:8.2f} us  {v['bytes'] / 1e6:8.2f} MB  {v['GB_s']:7.1f} GB/s")
+        log(f"[bench {config}] {k:14s} {v['kernel']:12s} {v['us']:8.2f} us  {v['bytes'] / 1e6:8.2f} MB  "
+            f"{v['GB_s']:7.1f} GB/s")
     # dominant kernel: largest total time per token
     per_token = {"qkv": spec.layers, "wo": spec.layers, "gate_up": spec.layers, "down": spec.layers,
                  "output+argmax": 1, "attention": spec.layers}
     dom = max(kernels, key=lambda k: kernels[k]["us"] * per_token[k])
     d = kernels[dom]
     bytes_per_token = spec.weight_bytes_per_token()
-    traffic = measured_traffic(args.config).get(dom)
+    traffic = measured_traffic(config).get(dom)
     roofline = {"bound": "hbm", "achieved": d["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(d["GB_s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": "calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, read from "
+                                  "profiles/hbm_traffic.md (not measured in this run)",
                 "kernel": f"{dom} ({d['kernel']})", "bytes_per_launch": d["bytes"],
                 "avg_launch_us": d["us"]}
+
+    # time to first token through fl_prefill (16-token int8-MFMA passes) of
+    # the same prompt, against the decode-step path above
+    prefill = None
+    if n_prompt > 1:
+        b.reset()
+        b.forward_prefill(prompt[:32], logits=False)  # capture the pass graphs
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _, ptok, _ = b.forward_prefill(prompt, logits=False)
+        pms = (time.perf_counter() - t0) * 1000.0
+        prefill = {"tokens": n_prompt, "ms": round(pms, 2), "tok_s": round(n_prompt * 1000.0 / pms, 1),
+                   "first_token": ptok, "decode_path_first_token": int(toks[0])}
+        log(f"[bench {config}] prefill of {n_prompt} tokens: {pms:.2f} ms ({n_prompt * 1000.0 / pms:.0f} tok/s); "
+            f"first token {ptok} (decode path {int(toks[0])})")
     b.close()
     if args.calibrate_copy:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE
@@ -397,34 +397,75 @@ def main() -> int:
         del src, dst
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if with_cpu:
         log("[bench] CPU baseline ...")
         cpu = cpu_baseline(model, spec, 4, args.cpu_tokens, 2 * args.cpu_tokens)
         log(f"[bench] CPU baseline {cpu['value']} tok/s (1 thread), {cpu['parallel']['value']} tok/s "
             f"({cpu['parallel']['cores']} threads)")
+    return {
+        "value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "spec": spec, "n_prompt": n_prompt,
+        "wl": wl, "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "prefill": prefill,
+        "decode_weight_roofline": {"bytes_per_token": bytes_per_token,
+                                   "achieved_GB_s": round(bytes_per_token * tok_s / 1e9, 1),
+                                   "frac": round(bytes_per_token * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
+    }
 
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="default run: skip the Llama-3-8B (C3) decode line reported under extra_configs")
+    ap.add_argument("--cpu-tokens", type=int, default=40)
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="override the workload's prompt length (profiling runs of the weight-streaming kernels, "
+                         "whose bytes do not depend on the context; the reported line names the length used)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the decode path "
+              "would shard by output rows / KV heads, which is not built here.", file=sys.stderr)
+        return 2
+    if args.config == "c4":
+        return bench_attention_c4(args)
+    if args.config == "c5":
+        return bench_verify_c5(args)
+    r = run_decode(args, args.config, not args.no_cpu_baseline)
+    spec, wl = r["spec"], r["wl"]
     out = {
         "metric": METRIC,
-        "value": round(tok_s, 2),
+        "value": r["value"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (random N(0,0.02) weights quantized to GGUF blocks; uniform-random prompt)",
-        "config": {"workload": wl["desc"], "model": spec.name, "global_batch": 1, "seq_len": n_prompt,
+        "config": {"workload": wl["desc"], "model": spec.name, "global_batch": 1, "seq_len": r["n_prompt"],
                    "parallelism": "none (1 GPU)"},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "decode_weight_roofline": {"bytes_per_token": bytes_per_token,
-                                   "achieved_GB_s": round(bytes_per_token * tok_s / 1e9, 1),
-                                   "frac": round(bytes_per_token * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
-        "kernels": kernels,
+        "roofline": r["roofline"],
+        "cpu_baseline": r["cpu_baseline"],
+        "decode_weight_roofline": r["decode_weight_roofline"],
+        "prefill": r["prefill"],
+        "kernels": r["kernels"],
     }
+    if args.config == "c2" and not args.no_c3 and args.prompt is None:
+        # the north-star shape, driver-timed in the same run
+        c3 = run_decode(args, "c3", False)
+        out["extra_configs"] = {"c3": {
+            "workload": c3["wl"]["desc"], "value": c3["value"], "unit": "tok/s", "ms_per_step": c3["ms_per_step"],
+            "steps": args.steps, "decode_weight_roofline": c3["decode_weight_roofline"],
+            "roofline": c3["roofline"], "prefill": c3["prefill"], "kernels": c3["kernels"]}}
     print(json.dumps(out), flush=True)
     return 0
 
