@@ -1018,9 +1018,9 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
             ctx->nsplit = ns;
     }
     const int G = c.num_heads / c.num_kv_heads;
-    // split partials for up to kVerifyMaxTokens queries (decode uses 1), so
+    // split partials for up to kPrefillTokens queries (decode uses 1), so
     // a verify batch never reallocates them
-    int rc = ensure_part(ctx, (size_t)kVerifyMaxTokens * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    int rc = ensure_part(ctx, (size_t)kPrefillTokens * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
     if (rc) return rc;
     ALLOC(ctx, ctx->x, H * 4);
     ALLOC(ctx, ctx->qkv, (qd + 2 * kvd) * 4);
@@ -1618,7 +1618,8 @@ int fl_bench_attention(fl_ctx *ctx, int seq_len, int iters, double *bytes_per_la
 static int verify_alloc(fl_ctx *ctx) {
     if (ctx->have_verify) return 0;
     const fl_model_config &c = ctx->cfg;
-    const size_t M = kVerifyMaxTokens, H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim;
+    // sized for prefill passes (the largest batches)
+    const size_t M = kPrefillTokens, H = c.hidden_dim, qd = (size_t)c.num_heads * c.head_dim;
     const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, F = c.intermediate_dim;
     const size_t kmax = std::max({H, qd, F});
     const size_t rmax = std::max({qd + 2 * kvd, 2 * F, H});
@@ -1627,7 +1628,7 @@ static int verify_alloc(fl_ctx *ctx) {
     ALLOC(ctx, ctx->vq, M * qd * 4);
     ALLOC(ctx, ctx->vk, M * kvd * 4);
     ALLOC(ctx, ctx->vv, M * kvd * 4);
-    ctx->vpart_floats = (size_t)kVerifyMaxKsplit * M * rmax;
+    ctx->vpart_floats = (size_t)kPrefillMaxKsplit * M * rmax;
     ALLOC(ctx, ctx->vpart, ctx->vpart_floats * 4);
     ALLOC(ctx, ctx->vxq, M * kmax);
     ALLOC(ctx, ctx->vxs, M * (kmax / 32) * 4);
@@ -1652,13 +1653,44 @@ static int verify_alloc(fl_ctx *ctx) {
 // sets the chunk (units per split, every chunk non-empty: the reducers sum
 // all ksplit partial sets).  The paired Q8_0 kernel (M <= 8) walks rounds of
 // 8 blocks, so its chunks are whole rounds.
+// Largest dynamic LDS one workgroup may use on this device.
+static size_t max_lds_per_block() {
+    static const size_t v = [] {
+        int dev = 0, b = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || b <= 0)
+            return (size_t)65536;
+        return (size_t)b;
+    }();
+    return v;
+}
+
+// (The M > 16 prefill batches allow up to kPrefillMaxKsplit splits and
+// shrink the chunk until the staged activations of all M rows fit in LDS.)
 static int verify_split(const fl_weight &w, int M, int &chunk) {
     const int tiles = (w.rows + 15) / 16;
     const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
+    const int ubytes = w.format == FL_Q4K ? 256 : 32;
+    const int maxks = M > kVerifyMaxTokens ? kPrefillMaxKsplit : kVerifyMaxKsplit;
     static const int target = getenv("FLARE_VG_WAVES") ? atoi(getenv("FLARE_VG_WAVES")) : 2048;  // tuning
-    const int want = std::max(1, std::min({units, kVerifyMaxKsplit, (target + tiles - 1) / tiles}));
+    const int want = std::max(1, std::min({units, maxks, (target + tiles - 1) / tiles}));
+    if (M > kVerifyMaxTokens && w.cols % 256 == 0) {
+        // the prefill kernel walks 256-value steps: chunk counts steps
+        const int steps = w.cols / 256;
+        const int ks = std::max(1, std::min({steps, maxks, (target + tiles - 1) / tiles}));
+        chunk = (steps + ks - 1) / ks;
+        return (steps + chunk - 1) / chunk;
+    }
     chunk = (units + want - 1) / want;
     if (w.format == FL_Q8_0 && M <= 8) chunk = std::min(units, (chunk + 7) / 8 * 8);
+    if (M > kVerifyMaxTokens) {
+        auto lds = [&](int ch) {
+            const size_t kn = (size_t)ch * ubytes;
+            return (((size_t)M * (kn + 32) + 15) & ~(size_t)15) + (size_t)M * (kn / 32) * 8;
+        };
+        while (chunk > 1 && lds(chunk) > max_lds_per_block()) chunk--;
+        if ((units + chunk - 1) / chunk > maxks) chunk = (units + maxks - 1) / maxks;
+    }
     return (units + chunk - 1) / chunk;
 }
 
@@ -1683,8 +1715,8 @@ static int verify_gemm(fl_ctx *ctx, const fl_weight &w, int M, const int8_t *xq,
 int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q, const float *scales,
                                const int32_t *sums, float *out) {
     if (!ctx || !w || !q || !scales || !sums || !out) return fail(ctx, FL_E_INVALID, "null argument");
-    if (n_tokens < 1 || n_tokens > kVerifyMaxTokens)
-        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kVerifyMaxTokens);
+    if (n_tokens < 1 || n_tokens > kPrefillTokens)
+        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kPrefillTokens);
     if (w->format != FL_Q8_0 && w->format != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
     // partials of this op live in their own buffer (sized for this weight)
     int chunk = 0;
@@ -2008,7 +2040,7 @@ static int verify_check(fl_ctx *ctx, const uint32_t *tokens, int M, int pos0) {
     if (pos0 < 0 || pos0 + M > c.max_seq_len)
         return fail(ctx, FL_E_INVALID, "positions [%d, %d) outside the KV cache (max_seq_len %d)", pos0, pos0 + M,
                     c.max_seq_len);
-    if (std::min(M, kVerifyMaxTokens) * c.num_kv_heads > 1024)
+    if (std::min(M, kPrefillTokens) * c.num_kv_heads > 1024)
         return fail(ctx, FL_E_INVALID, "too many kv heads for a verify batch");
     for (int i = 0; i < M; i++)
         if ((int)tokens[i] >= c.vocab_size) return fail(ctx, FL_E_INVALID, "token %u >= vocab", tokens[i]);
@@ -2100,7 +2132,10 @@ int fl_prefill(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, floa
         return decode_step(ctx, tokens[n_tokens - 1], nullptr, pos0 + n_tokens - 1, out_logits, out_token, out_val);
     }
     hipStream_t st = ctx->stream;
-    const int C = kVerifyMaxTokens;
+    // FLARE_PREFILL_TOKENS: pass size (measurement switch; 1..64)
+    static const int C = getenv("FLARE_PREFILL_TOKENS")
+                             ? std::max(1, std::min(kPrefillTokens, atoi(getenv("FLARE_PREFILL_TOKENS"))))
+                             : kPrefillTokens;
     const int nchunks = (n_tokens + C - 1) / C;
     // host copies stay alive until the final synchronisation
     std::vector<int> tk(tokens, tokens + n_tokens), pos(nchunks);

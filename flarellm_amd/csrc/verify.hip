@@ -7,7 +7,15 @@ namespace fl {
 hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     const int tiles = (a.W.rows + 15) / 16;
     const dim3 grid((tiles + 3) / 4, a.ksplit);
-    if (a.M < 1 || a.M > kVerifyMaxTokens || a.ksplit < 1 || a.chunk < 1) return hipErrorInvalidValue;
+    if (a.M < 1 || a.M > kPrefillTokens || a.ksplit < 1 || a.chunk < 1) return hipErrorInvalidValue;
+    const int nt = (a.M + 15) / 16;  // token tiles of the M > 8 kernels
+    if (a.M > kVerifyMaxTokens && a.W.cols % 256 == 0 && !a.post) {
+        // prefill batches: activations staged per 256-value step (chunk = steps)
+        if (fmt == F_Q4K) hipLaunchKernelGGL(k_pgemm<F_Q4K>, grid, dim3(256), 0, st, a);
+        else if (fmt == F_Q8_0) hipLaunchKernelGGL(k_pgemm<F_Q8_0>, grid, dim3(256), 0, st, a);
+        else return hipErrorNotSupported;
+        return hipGetLastError();
+    }
     if (a.W.cols % 32) return hipErrorInvalidValue;
     size_t kn;
     if (fmt == F_Q4K) {
@@ -26,8 +34,14 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
             const size_t lds = 8 * (kn + 32) + 8 * (kn / 32) * 8;
             hipLaunchKernelGGL(k_vgemm_q4k8<1>, grid, dim3(256), lds, st, a);
         } else {
-            const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
-            hipLaunchKernelGGL(k_vgemm_q4k, grid, dim3(256), lds, st, a);
+            if (a.post) return hipErrorInvalidValue;
+            const size_t lds = (((size_t)a.M * (kn + 32) + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+            switch (nt) {
+            case 1: hipLaunchKernelGGL(k_vgemm_q4k<1>, grid, dim3(256), lds, st, a); break;
+            case 2: hipLaunchKernelGGL(k_vgemm_q4k<2>, grid, dim3(256), lds, st, a); break;
+            case 3: hipLaunchKernelGGL(k_vgemm_q4k<3>, grid, dim3(256), lds, st, a); break;
+            default: hipLaunchKernelGGL(k_vgemm_q4k<4>, grid, dim3(256), lds, st, a); break;
+            }
         }
     } else {
         if (fmt != F_Q8_0 || a.post) return hipErrorNotSupported;
@@ -36,8 +50,13 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
         if (a.M <= 8) {
             hipLaunchKernelGGL(k_vgemm_q8_08, grid, dim3(256), 8 * (kn + 32) + 8 * (kn / 32) * 8, st, a);
         } else {
-            const size_t lds = ((kVerifyMaxTokens * kn + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
-            hipLaunchKernelGGL(k_vgemm_q8_0, grid, dim3(256), lds, st, a);
+            const size_t lds = (((size_t)a.M * (kn + 32) + 15) & ~(size_t)15) + (size_t)a.M * (kn / 32) * 8;
+            switch (nt) {
+            case 1: hipLaunchKernelGGL(k_vgemm_q8_0<1>, grid, dim3(256), lds, st, a); break;
+            case 2: hipLaunchKernelGGL(k_vgemm_q8_0<2>, grid, dim3(256), lds, st, a); break;
+            case 3: hipLaunchKernelGGL(k_vgemm_q8_0<3>, grid, dim3(256), lds, st, a); break;
+            default: hipLaunchKernelGGL(k_vgemm_q8_0<4>, grid, dim3(256), lds, st, a); break;
+            }
         }
     }
     return hipGetLastError();

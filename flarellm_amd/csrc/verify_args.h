@@ -6,7 +6,9 @@
 
 namespace fl {
 
-constexpr int kVerifyMaxTokens = 16;  // the MFMA tile's token side
+constexpr int kVerifyMaxTokens = 16;  // the MFMA tile's token side (fl_verify batches)
+constexpr int kPrefillTokens = 64;    // prefill passes: four token tiles per weight fragment
+constexpr int kPrefillMaxKsplit = 32;
 
 typedef long long i64x1_t;
 typedef int v4i32_t __attribute__((ext_vector_type(4)));

@@ -74,6 +74,10 @@ __device__ __forceinline__ v4i32_t vg_mfma(i64x1_t a, i64x1_t b) {
 
 // Q8_0 weights: unit = one 32-block.  Block term of matvec_q8_0_preq_into
 // (model.rs:8082-8099): (f16(w_scale) * x_scale) * (int dot as f32).
+// NT token tiles of 16 (M <= 16 NT): each weight fragment feeds NT MFMAs.
+// Activation rows sit xst = kn + 32 bytes apart in LDS (the 16 lanes of a
+// tile read distinct banks).
+template <int NT>
 __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
@@ -82,16 +86,20 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
     const int chunk = a.chunk;
     const int b0 = blockIdx.y * chunk, b1 = min(nbk, b0 + chunk);
     if (b0 >= b1) return;
-    const int kn = (b1 - b0) * 32;
+    const int kn = (b1 - b0) * 32, xst = a.chunk * 32 + 32;
     int8_t *lx = (int8_t *)smem;
-    float2 *lsc = (float2 *)(smem + ((kVerifyMaxTokens * kn + 15) & ~15));
-    vg_stage<F_Q8_0>(a, b0 * 32, kn, lx, lsc);
+    float2 *lsc = (float2 *)(smem + ((a.M * xst + 15) & ~15));
+    vg_stage<F_Q8_0>(a, b0 * 32, kn, lx, lsc, xst);
     const int tile = blockIdx.x * 4 + wave;
     if (tile * 16 >= W.rows) return;
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
     const int row = min(n, W.rows - 1);
     const int nbc = b1 - b0;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[NT][4];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[tt][i] = 0.f;
     const int8_t *wq = (const int8_t *)W.q + (size_t)row * K + 8 * kg;
     const uint16_t *ws = W.s + (size_t)row * nbk;
     i64x1_t wn = *(const i64x1_t *)(wq + 32 * b0);
@@ -104,28 +112,36 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
             sn = ws[b + 1];
         }
         const int bl = b - b0;
-        const i64x1_t x = tA < a.M ? *(const i64x1_t *)(lx + tA * kn + 32 * bl + 8 * kg) : 0;
-        const v4i32_t d = vg_mfma(x, wcur);
         const float wsc = h2f(scur);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * kg + i;
-            if (t < a.M) acc[i] += (wsc * lsc[t * nbc + bl].x) * (float)d[i];
+        for (int tt = 0; tt < NT; tt++) {
+            const int tx = tA + 16 * tt;
+            const i64x1_t x = tx < a.M ? *(const i64x1_t *)(lx + tx * xst + 32 * bl + 8 * kg) : 0;
+            const v4i32_t d = vg_mfma(x, wcur);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * tt + 4 * kg + i;
+                if (t < a.M) acc[tt][i] += (wsc * lsc[t * nbc + bl].x) * (float)d[i];
+            }
         }
     }
     if (n < W.rows) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * kg + i;
-            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[i];
-        }
+        for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * tt + 4 * kg + i;
+                if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[tt][i];
+            }
     }
 }
 
 // Q4_K weights (flarellm layout): unit = one 256-value super-block, 8 MFMAs
-// (sub-block j: low nibbles of qs[32j..32j+32) for j < 4, high nibbles of
-// qs[32(j-4)..] for j >= 4).  Block term of dot_q4k_q8_0_scalar
-// (model.rs:8969-9025): s_x * (d*sc*dot - dmin*mn*sum(q_x)).
+// per token tile (sub-block j: low nibbles of qs[32j..32j+32) for j < 4,
+// high nibbles of qs[32(j-4)..] for j >= 4).  Block term of
+// dot_q4k_q8_0_scalar (model.rs:8969-9025): s_x * (d*sc*dot - dmin*mn*sum(q_x)).
+// NT token tiles of 16 as in k_vgemm_q8_0.
+template <int NT>
 __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
@@ -134,13 +150,17 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     const int chunk = a.chunk;
     const int s0 = blockIdx.y * chunk, s1 = min(nsb, s0 + chunk);
     if (s0 >= s1) return;
-    const int kn = (s1 - s0) * 256, nbc = kn >> 5;
+    const int kn = (s1 - s0) * 256, nbc = kn >> 5, xst = a.chunk * 256 + 32;
     int8_t *lx = (int8_t *)smem;
-    float2 *lsc = (float2 *)(smem + ((kVerifyMaxTokens * kn + 15) & ~15));
+    float2 *lsc = (float2 *)(smem + ((a.M * xst + 15) & ~15));
     const int tile = blockIdx.x * 4 + wave;
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
     const int row = min(n, W.rows - 1);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[NT][4];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[tt][i] = 0.f;
     const uint8_t *qs = W.q + (size_t)row * nsb * 128 + 8 * kg;
     const uint8_t *hd = W.h + (size_t)row * nsb * 16;
     auto load = [&](int sb, i64x1_t *w, v4i_t &h) {
@@ -151,7 +171,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
     i64x1_t wn[4];
     v4i_t hn;
     load(s0, wn, hn);
-    vg_stage<F_Q4K>(a, s0 * 256, kn, lx, lsc);
+    vg_stage<F_Q4K>(a, s0 * 256, kn, lx, lsc, xst);
     if (tile * 16 >= W.rows) return;
     for (int sb = s0; sb < s1; sb++) {
         i64x1_t w[4];
@@ -167,8 +187,6 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
             const int jj = j & 3;
             const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
             const i64x1_t wb = j < 4 ? (w[jj] & m4) : ((w[jj] >> 4) & m4);
-            const i64x1_t x = tA < a.M ? *(const i64x1_t *)(lx + tA * kn + sl * 256 + 32 * j + 8 * kg) : 0;
-            const v4i32_t dd = vg_mfma(x, wb);
             // unpack_q4k_scales (model.rs:8709-8719), flare packing
             const uint32_t sa = byte_of((uint32_t)h.y, jj), sbb = byte_of((uint32_t)h.z, jj),
                            scc = byte_of((uint32_t)h.w, jj);
@@ -177,21 +195,187 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
             const float dsc = d * (float)sc, dmn = dmin * (float)mn;
             const int bl = sl * 8 + j;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = 4 * kg + i;
-                if (t < a.M) {
-                    const float2 xs = lsc[t * nbc + bl];
-                    acc[i] += xs.x * (dsc * (float)dd[i] - dmn * xs.y);
+            for (int tt = 0; tt < NT; tt++) {
+                const int tx = tA + 16 * tt;
+                const i64x1_t x = tx < a.M ? *(const i64x1_t *)(lx + tx * xst + sl * 256 + 32 * j + 8 * kg) : 0;
+                const v4i32_t dd = vg_mfma(x, wb);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = 16 * tt + 4 * kg + i;
+                    if (t < a.M) {
+                        const float2 xs = lsc[t * nbc + bl];
+                        acc[tt][i] += xs.x * (dsc * (float)dd[i] - dmn * xs.y);
+                    }
                 }
             }
         }
     }
     if (n < W.rows) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * kg + i;
-            if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[i];
+        for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * tt + 4 * kg + i;
+                if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[tt][i];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM, 17..64 tokens (kPrefillTokens): each wave owns 16 weight rows
+// and all four 16-token tiles, so every weight fragment read from HBM feeds
+// four MFMAs.  K is walked in 256-value steps (one Q4_K super-block, or eight
+// Q8_0 blocks); the 64 activation rows of a step (16 KB of codes plus the
+// (scale, sum) pairs) are staged through a double-buffered LDS slot, the next
+// step's loads in flight while this one is consumed, so the LDS footprint
+// does not grow with K.  Same per-block terms as k_vgemm_q8_0 / k_vgemm_q4k.
+// ---------------------------------------------------------------------------
+constexpr int kPgStride = 256 + 32;  // LDS row stride of one step's codes (bank spread)
+
+struct PgStage {
+    v4i_t q[4];    // 4 x 16 B of the 64 x 256 codes per thread
+    float2 sc[2];  // 2 of the 64 x 8 (scale, sum) pairs per thread
+};
+
+__device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage &r) {
+    const int K = a.W.cols, t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = t + 256 * u;  // 1024 pieces of 16 B: token i / 16, bytes 16 (i % 16)
+        const int tok = min(i >> 4, a.M - 1);
+        r.q[u] = *(const v4i_t *)(a.xq + (size_t)tok * K + k0 + 16 * (i & 15));
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int i = t + 256 * u;  // 512 pairs: token i / 8, block i % 8
+        const int tok = min(i >> 3, a.M - 1);
+        const size_t o = (size_t)tok * (K >> 5) + (k0 >> 5) + (i & 7);
+        r.sc[u] = make_float2(a.xs[o], (float)a.xsum[o]);
+    }
+}
+
+__device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float2 *lsc) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = t + 256 * u;
+        *(v4i_t *)(lx + (i >> 4) * kPgStride + 16 * (i & 15)) = r.q[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) lsc[t + 256 * u] = r.sc[u];
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
+    __shared__ __align__(16) int8_t lx[2][64 * kPgStride];
+    __shared__ float2 lsc[2][64 * 8];
+    const WDesc &W = a.W;
+    const int K = W.cols, nst = K >> 8;  // 256-value steps
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s0 = blockIdx.y * a.chunk, s1 = min(nst, s0 + a.chunk);
+    if (s0 >= s1) return;
+    const int tile = blockIdx.x * 4 + wave;
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int row = min(n, W.rows - 1);
+    float acc[4][4];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[tt][i] = 0.f;
+    // weights of one step for this lane: Q4_K qs 4 x 8 B + the 16-B header;
+    // Q8_0 8 blocks x 8 B + 8 scales
+    i64x1_t wn[8];
+    v4i_t hn;
+    uint16_t sn[8];
+    auto wload = [&](int st) {
+        if constexpr (FMT == F_Q4K) {
+            const uint8_t *qs = W.q + ((size_t)row * nst + st) * 128 + 8 * kg;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) wn[jj] = *(const i64x1_t *)(qs + 32 * jj);
+            hn = *(const v4i_t *)(W.h + ((size_t)row * nst + st) * 16);
+        } else {
+            const int8_t *wq = (const int8_t *)W.q + (size_t)row * K + 256 * st + 8 * kg;
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) wn[jj] = *(const i64x1_t *)(wq + 32 * jj);
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) sn[jj] = W.s[(size_t)row * (K >> 5) + 8 * st + jj];
         }
+    };
+    PgStage xr;
+    wload(s0);
+    pg_load(a, s0 * 256, xr);
+    pg_store(xr, lx[0], lsc[0]);
+    __syncthreads();
+    for (int st = s0; st < s1; st++) {
+        const int cur = (st - s0) & 1;
+        i64x1_t w[8];
+        v4i_t h = hn;
+        uint16_t sc8[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            w[jj] = wn[jj];
+            sc8[jj] = sn[jj];
+        }
+        if (st + 1 < s1) {
+            wload(st + 1);
+            pg_load(a, (st + 1) * 256, xr);
+        }
+        const int8_t *bx = lx[cur];
+        const float2 *bs = lsc[cur];
+        if (tile * 16 < W.rows) {
+            float d = 0.f, dmin = 0.f;
+            if constexpr (FMT == F_Q4K) {
+                const uint32_t h0 = (uint32_t)h.x;
+                d = h2f((uint16_t)(h0 & 0xFFFF));
+                dmin = h2f((uint16_t)(h0 >> 16));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                i64x1_t wb;
+                float dsc, dmn = 0.f;
+                if constexpr (FMT == F_Q4K) {
+                    const int jj = j & 3;
+                    const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
+                    wb = j < 4 ? (w[jj] & m4) : ((w[jj] >> 4) & m4);
+                    // unpack_q4k_scales (model.rs:8709-8719), flare packing
+                    const uint32_t sa = byte_of((uint32_t)h.y, jj), sbb = byte_of((uint32_t)h.z, jj),
+                                   scc = byte_of((uint32_t)h.w, jj);
+                    const uint32_t sc = j < 4 ? (sa & 63) : ((sa >> 6) | ((scc & 0xF) << 2));
+                    const uint32_t mn = j < 4 ? (sbb & 63) : ((sbb >> 6) | ((scc >> 4) << 2));
+                    dsc = d * (float)sc;
+                    dmn = dmin * (float)mn;
+                } else {
+                    wb = w[j];
+                    dsc = h2f(sc8[j]);
+                }
+                // Q4_K sub-block j: low nibbles pair with activation bytes 32j of
+                // the step for j < 4 (qs bytes 32jj..), high nibbles with 32j
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const int tx = tA + 16 * tt;
+                    const i64x1_t x = *(const i64x1_t *)(bx + tx * kPgStride + 32 * j + 8 * kg);
+                    const v4i32_t dd = vg_mfma(x, wb);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int t = 16 * tt + 4 * kg + i;
+                        const float2 xs = bs[t * 8 + j];
+                        if constexpr (FMT == F_Q4K) acc[tt][i] += xs.x * (dsc * (float)dd[i] - dmn * xs.y);
+                        else acc[tt][i] += (dsc * xs.x) * (float)dd[i];
+                    }
+                }
+            }
+        }
+        if (st + 1 < s1) pg_store(xr, lx[cur ^ 1], lsc[cur ^ 1]);
+        __syncthreads();
+    }
+    if (n < W.rows) {
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * tt + 4 * kg + i;
+                if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[tt][i];
+            }
     }
 }
 

@@ -152,7 +152,7 @@ int fl_op_rmsnorm(fl_ctx *ctx, const float *x, const float *w, int n, float eps,
 int fl_op_matvec_q8in(fl_ctx *ctx, const fl_weight *w, const int8_t *q, const float *scales,
                       const int32_t *sums, float *out);
 /* CpuBackend::batched_dequant_matmul (model.rs:740-1036) over n_tokens
- * (1..16) Q8_0-quantized input rows: q [n][cols] int8, scales / sums
+ * (1..64; more than 16 take the prefill kernel) Q8_0-quantized input rows: q [n][cols] int8, scales / sums
  * [n][cols/32]; out [n][rows] f32.  Every row of out is the single-token
  * matvec_q8_0_preq_into / matvec_q4k_q8_into of that input row (the same
  * per-block integer dots, formed on int8 MFMA).  Synchronises. */

@@ -36,7 +36,10 @@ def _close(got, want, rel=REL):
 
 GEMM_SHAPES = [(FL_Q8_0, 96, 256, 1), (FL_Q8_0, 1001, 2048, 8), (FL_Q8_0, 64, 576, 3), (FL_Q8_0, 200, 8192, 16),
                (FL_Q4K, 96, 256, 8), (FL_Q4K, 130, 4096, 5), (FL_Q4K, 64, 14336, 8), (FL_Q4K, 6144, 4096, 8),
-               (FL_Q4K, 1536, 4096, 16)]
+               (FL_Q4K, 1536, 4096, 16),
+               # prefill batches (17..64 tokens): 256-value steps staged through LDS
+               (FL_Q8_0, 3072, 2048, 64), (FL_Q8_0, 513, 8192, 37), (FL_Q4K, 6144, 4096, 64),
+               (FL_Q4K, 4096, 14336, 50), (FL_Q4K, 130, 4096, 17)]
 
 
 @pytest.mark.parametrize("fmt,rows,cols,M", GEMM_SHAPES)
