@@ -290,6 +290,7 @@ def run_decode(args, config: str, with_cpu: bool) -> dict:
     steps timed with HIP events on the context stream; per-kernel HBM rates
     (HIP events around back-to-back launches); a timed fl_prefill of the same
     prompt; optionally the CPU baseline.  Returns the JSON fields."""
+    import numpy as np
     import torch
 
     from flarellm_amd import FL_KV_F16, FL_KV_F32
@@ -380,8 +381,16 @@ def run_decode(args, config: str, with_cpu: bool) -> dict:
         t0 = time.perf_counter()
         _, ptok, _ = b.forward_prefill(prompt, logits=False)
         pms = (time.perf_counter() - t0) * 1000.0
+        # the same prefill with logits: the top-2 gap of the last token (a
+        # first token that differs from the decode path's is a near-tie of
+        # two tree orders when this gap is small)
+        b.reset()
+        plg, _, _ = b.forward_prefill(prompt, logits=True)
+        top2 = np.sort(plg)[-2:]
         prefill = {"tokens": n_prompt, "ms": round(pms, 2), "tok_s": round(n_prompt * 1000.0 / pms, 1),
-                   "first_token": ptok, "decode_path_first_token": int(toks[0])}
+                   "pass_tokens": 64, "first_token": ptok, "decode_path_first_token": int(toks[0]),
+                   "top2_gap_rel": round(float((top2[1] - top2[0]) / abs(top2[1])), 5),
+                   "decode_path_token_rank": int((plg > plg[int(toks[0])]).sum())}
         log(f"[bench {config}] prefill of {n_prompt} tokens: {pms:.2f} ms ({n_prompt * 1000.0 / pms:.0f} tok/s); "
             f"first token {ptok} (decode path {int(toks[0])})")
     b.close()
