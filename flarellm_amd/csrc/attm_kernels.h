@@ -54,12 +54,24 @@ __device__ __forceinline__ v8h_t as_h8(const v4i_t &v) {
     return r;
 }
 
-// int8 codes -> exact f16 values
+// int8 codes -> exact f16 values: bias each byte to unsigned (xor 0x80), make
+// it the low byte of binary16 0x64XX = 1024 + XX with one byte permute per two
+// codes (v_perm_b32 picks bytes of the codes and of 0x64646464), then
+// subtract 1152 = 1024 + 128 in packed f16 (every value is an integer below
+// 2048, so each step is exact).
 __device__ __forceinline__ v8h_t i8x8_to_h8(const v2i_t &c) {
+    const uint32_t u0 = (uint32_t)c.x ^ 0x80808080u, u1 = (uint32_t)c.y ^ 0x80808080u;
+    constexpr uint32_t m = 0x64646464u;
+    uint32_t d[4];
+    d[0] = __builtin_amdgcn_perm(m, u0, 0x04010400u);  // bytes: u0.b0, 0x64, u0.b1, 0x64
+    d[1] = __builtin_amdgcn_perm(m, u0, 0x04030402u);
+    d[2] = __builtin_amdgcn_perm(m, u1, 0x04010400u);
+    d[3] = __builtin_amdgcn_perm(m, u1, 0x04030402u);
     v8h_t r;
-#pragma unroll
-    for (int i = 0; i < 8; i++) r[i] = (_Float16)(int8_t)(((uint32_t)(i < 4 ? c.x : c.y) >> (8 * (i & 3))) & 0xFF);
-    return r;
+    __builtin_memcpy(&r, d, 16);
+    const _Float16 k = (_Float16)1152.0f;
+    const v8h_t bias = {k, k, k, k, k, k, k, k};
+    return r - bias;
 }
 
 template <typename KT, int D>
@@ -87,16 +99,19 @@ struct AttmTile<__half, D> {
     }
 };
 
-// Q8: int8 codes + f16 scale per (slot, 32-channel block)
+// Q8: int8 codes + f16 scale per (slot, 32-channel block).  K and V halves
+// load separately: a wave issues the next block's K as soon as the current
+// scores are formed and its V once P V is done, so each half is in flight
+// over the other half's arithmetic without a second tile of registers.
 template <int D>
 struct AttmTile<KvQ8, D> {
-    static constexpr int DT = D / 32, NT = D / 16;
+    static constexpr int DT = D / 32, NT = D / 16, VW = (DT + 1) / 2;
     v2i_t k[2][DT];
     v2i_t v[NT];
-    uint32_t ksc[2][(DT + 1) / 2];  // this lane's slot: K scales (2 per word)
-    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
+    uint32_t ksc[2][VW];  // this lane's slot: K scales (2 per word)
+    uint32_t vsc[VW];     // slot tb + lane % 32: V scales (2 per word)
+    __device__ __forceinline__ void load_k(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
         const int8_t *kc = (const int8_t *)a.kc + (size_t)kvh * a.head_stride;
-        const int8_t *vc = (const int8_t *)a.vc + (size_t)kvh * a.head_stride;
         const int kg = lane >> 4, r = lane & 15;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -105,10 +120,22 @@ struct AttmTile<KvQ8, D> {
             for (int dt = 0; dt < DT; dt++) k[h][dt] = *(const v2i_t *)(kc + (size_t)t * D + 32 * dt + 8 * kg);
             const uint32_t *sp = (const uint32_t *)(a.ks + ((size_t)kvh * a.S + t) * DT);
 #pragma unroll
-            for (int w = 0; w < (DT + 1) / 2; w++) ksc[h][w] = sp[w];
+            for (int w = 0; w < VW; w++) ksc[h][w] = sp[w];
         }
+    }
+    __device__ __forceinline__ void load_v(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
+        const int8_t *vc = (const int8_t *)a.vc + (size_t)kvh * a.head_stride;
+        const int kg = lane >> 4, r = lane & 15;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) v[nt] = *(const v2i_t *)(vc + vt_off(tb, 16 * nt + r, D) + 8 * kg);
+        const int t = min(tb + (lane & 31), tlast);
+        const uint32_t *sp = (const uint32_t *)(a.vs + ((size_t)kvh * a.S + t) * DT);
+#pragma unroll
+        for (int w = 0; w < VW; w++) vsc[w] = sp[w];
+    }
+    __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
+        load_k(a, kvh, tb, tlast, lane);
+        load_v(a, kvh, tb, tlast, lane);
     }
 };
 
@@ -323,7 +350,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
 
     // one 32-slot block (slots tb .. tb+31) with its tile in registers
-    auto process = [&](auto &tile, int bi) {
+    // nxt >= 0 (Q8): block index whose K / V the tile loads once the current
+    // block's K / V registers are consumed
+    auto process = [&](auto &tile, int bi, int nxt) {
         using TT = typename std::remove_reference<decltype(tile)>::type;
         constexpr bool KQ = std::is_same<TT, AttmKiviQ<D>>::value;                 // 2-bit block
         constexpr bool H16 = std::is_same<KT, __half>::value || (KIVI && !KQ);    // fp16 operands
@@ -484,6 +513,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             sc[h][0] = ok && t != lastA0 ? (acc[0] + acc[1] + kbh[0]) * scale : -INFINITY;
             sc[h][1] = ok && t != lastA1 ? (acc[2] + acc[3] + kbh[1]) * scale : -INFINITY;
         }
+        if constexpr (std::is_same<KT, KvQ8>::value)
+            if (nxt >= 0) tile.load_k(a, kvh, t0 + nxt * kAttmBlock, t1 - 1, lane);
         if (bi == wave) ATTN_TS(2);
         // ---- online softmax per head (rows of 16 lanes hold one head pair) --
         float alpha[2];
@@ -505,10 +536,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         if constexpr (std::is_same<KT, KvQ8>::value) {
             // V scales of the block's 32 slots (lane = slot, one word per 2 blocks)
             if (lane < kAttmBlock) {
-                const int t = min(tb + lane, t1 - 1);
 #pragma unroll
                 for (int b = 0; b < DT; b++) {
-                    uint16_t sv = a.vs[((size_t)kvh * a.S + t) * DT + b];
+                    uint16_t sv = (uint16_t)(tile.vsc[b >> 1] >> (16 * (b & 1)));
                     if (has_new && tb + lane == pos) sv = nvs[b];
                     const float v = (tb + lane < t1) ? h2f(sv) : 0.0f;
                     vsc[wave][lane][b] = v;
@@ -601,6 +631,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 }
             }
         }
+        if constexpr (std::is_same<KT, KvQ8>::value)
+            if (nxt >= 0) tile.load_v(a, kvh, t0 + nxt * kAttmBlock, t1 - 1, lane);
         __builtin_amdgcn_wave_barrier();
     };
     if constexpr (std::is_same<KT, __half>::value) {
@@ -608,33 +640,31 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         AttmTile<KT, D> tile2;
         for (int bi = wave; bi < nblk; bi += 2 * NW) {
             if (bi + NW < nblk) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi);
+            process(tile, bi, -1);
             if (bi + NW >= nblk) break;
             if (bi + 2 * NW < nblk) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW);
+            process(tile2, bi + NW, -1);
         }
     } else if constexpr (KIVI) {
         // 2-bit blocks ping-pong (small tiles), then the ring blocks
         Tile0 tile2;
         for (int bi = wave; bi < nqb; bi += 2 * NW) {
             if (bi + NW < nqb) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi);
+            process(tile, bi, -1);
             if (bi + NW >= nqb) break;
             if (bi + 2 * NW < nqb) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW);
+            process(tile2, bi + NW, -1);
         }
         AttmTile<KvKivi, D> rt;
         const int bi0 = nqb > wave ? wave + (nqb - wave + NW - 1) / NW * NW : wave;
         for (int bi = bi0; bi < nblk; bi += NW) {
             rt.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
-            process(rt, bi);
+            process(rt, bi, -1);
         }
     } else {
-        // Q8 (more registers per block): one tile, loaded at the top
-        for (int bi = wave; bi < nblk; bi += NW) {
-            if (bi != wave) tile.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
-            process(tile, bi);
-        }
+        // Q8 (more registers per block): one tile, loaded at the top; the
+        // next block's K and V halves load as the current halves are consumed
+        for (int bi = wave; bi < nblk; bi += NW) process(tile, bi, bi + NW < nblk ? bi + NW : -1);
     }
     if constexpr (KIVI) {
         // decode step that ages group qlen/32 out of the fp16 residual: split

@@ -33,6 +33,30 @@ static hipError_t launch_attm_t(int D, int G, hipStream_t st, const AttnArgs &a,
     return hipErrorNotSupported;
 }
 
+template <typename KT>
+static int attm_resident_t(int D, int G, int waves) {
+    int n = 0;
+#define C(DD, GG)                                                                                       \
+    if (D == DD && G == GG) {                                                                           \
+        if (waves == 4)                                                                                 \
+            (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attm<KT, DD, GG, 256>, 256, 0);     \
+        else                                                                                            \
+            (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attm<KT, DD, GG>, kAttmThreads, 0); \
+        return n;                                                                                       \
+    }
+    C(64, 1) C(64, 2) C(64, 3) C(64, 4) C(64, 8)
+    C(128, 1) C(128, 2) C(128, 3) C(128, 4) C(128, 8)
+#undef C
+    return 0;
+}
+
+int attm_resident_per_cu(int kvfmt, int D, int G, int waves) {
+    if (kvfmt == KV_F16) return attm_resident_t<__half>(D, G, waves);
+    if (kvfmt == KV_Q8) return attm_resident_t<KvQ8>(D, G, waves);
+    if (kvfmt == KV_KIVI) return attm_resident_t<KvKivi>(D, G, waves);
+    return 0;
+}
+
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq) {
     if (nq < 1) return hipErrorInvalidValue;
     if (nq > 1 && a.knew) return hipErrorInvalidValue;  // new-token stores are single-query

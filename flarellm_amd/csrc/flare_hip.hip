@@ -1000,6 +1000,11 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         // 4-wave workgroups for D=64 and 8-wave ones for D=128.  More,
         // smaller splits spread the K/V stream over more CUs; the split merge
         // (publish, count, one round trip of partial loads) costs ~3-4 us.
+        // The split count stops where every workgroup of a decode launch is
+        // resident at once (CUs x resident workgroups per CU / kv heads):
+        // beyond that, a second dispatch round repeats the whole latency
+        // chain (Llama-3-8B heads at 32k / 128k: 32 splits against 64 cut
+        // fp16 44 -> 32 / 109 -> 99 us, Q8 49 -> 32 / 100 -> 88 us).
         ctx->attn_waves = c.head_dim <= 64 ? 4 : 8;
         ctx->single = 0;
         if (const char *ev = getenv("FLARE_ATTN_WAVES")) ctx->attn_waves = atoi(ev) == 4 ? 4 : 8;  // tuning override
@@ -1007,7 +1012,12 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         ctx->chmin = pass;
         if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(pass, atoi(ev) / pass * pass);
         if (const char *ev = getenv("FLARE_ATTN_SINGLE")) ctx->single = std::max(0, atoi(ev));  // tuning override
-        ctx->nsplit = std::max(1, std::min(kAttmMaxSplit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin));
+        int ncu = 0, dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        const int res = attm_resident_per_cu(kv_format, c.head_dim, c.num_heads / c.num_kv_heads, ctx->attn_waves);
+        const int fit = ncu > 0 && res > 0 ? std::max(1, ncu * res / c.num_kv_heads) : kAttmMaxSplit;
+        ctx->nsplit = std::max(1, std::min({kAttmMaxSplit, fit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin}));
     } else {
         choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
         if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
