@@ -448,10 +448,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     for (int b = 0; b < DT; b++) {
                         const uint32_t sm = okt ? tile.vp[b] : 0u;
                         const float sv = h2f((uint16_t)(sm & 0xFFFF));
-                        vsc[wave][lane][b] = sv;
                         vmn[wave][lane][b] = h2f((uint16_t)(sm >> 16));
                         float mx = row_max<16>(sv);
                         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                        vsc[wave][lane][b] = mx > 0.0f ? sv * __builtin_amdgcn_rcpf(mx) : 0.0f;
                         if (lane == 0) vmax[wave][b] = mx;
                     }
                 }
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     const uint32_t w = tile.ksc[h][dt >> 1];
                     const float ks = h2f((uint16_t)((dt & 1) ? (w >> 16) : (w & 0xFFFF)));
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i] += part[i] * ks;
+                    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(part[i], ks, acc[i]);
                 }
             }
             const int t = tb + 16 * h + r;
@@ -541,9 +541,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     uint16_t sv = (uint16_t)(tile.vsc[b >> 1] >> (16 * (b & 1)));
                     if (has_new && tb + lane == pos) sv = nvs[b];
                     const float v = (tb + lane < t1) ? h2f(sv) : 0.0f;
-                    vsc[wave][lane][b] = v;
                     float mx = row_max<16>(v);
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                    vsc[wave][lane][b] = mx > 0.0f ? v * __builtin_amdgcn_rcpf(mx) : 0.0f;
                     if (lane == 0) vmax[wave][b] = mx;
                 }
             }
@@ -576,11 +576,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                     for (int b = 0; b < DT; b++) {
                         const float vref = vmax[wave][b];
-                        const float inv = vref > 0.0f ? 1.0f / vref : 0.0f;
                         float pb[8], vb = 0.0f;
 #pragma unroll
                         for (int i = 0; i < 8; i++) {
-                            pb[i] = p[i] * (vsc[wave][8 * kg + i][b] * inv);
+                            pb[i] = p[i] * vsc[wave][8 * kg + i][b];
                             vb += p[i] * vmn[wave][8 * kg + i][b];
                         }
                         vb += __shfl_xor(vb, 16, 64);
@@ -595,7 +594,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                             const v4f32_t part = mfma16(ap, c2x8_to_h8((vw[nt >> 1] >> (16 * (nt & 1))) & 0xFFFFu),
                                                         v4f32_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                            for (int i = 0; i < 4; i++) oacc[nt][i] += part[i] * vref;
+                            for (int i = 0; i < 4; i++) oacc[nt][i] = __builtin_fmaf(part[i], vref, oacc[nt][i]);
                         }
                     }
                     __builtin_amdgcn_s_waitcnt(0);
@@ -614,10 +613,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                 for (int b = 0; b < DT; b++) {
                     const float vref = vmax[wave][b];
-                    const float inv = vref > 0.0f ? 1.0f / vref : 0.0f;
                     float pb[8];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) pb[i] = p[i] * (vsc[wave][8 * kg + i][b] * inv);
+                    for (int i = 0; i < 8; i++) pb[i] = p[i] * vsc[wave][8 * kg + i][b];
                     v8h_t hi, lo;
                     split8(pb, hi, lo);
                     const v8h_t ap = (m & 1) ? lo : hi;
@@ -626,7 +624,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                         const v4f32_t part =
                             mfma16(ap, i8x8_to_h8(tile.v[2 * b + u]), v4f32_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                        for (int i = 0; i < 4; i++) oacc[2 * b + u][i] += part[i] * vref;
+                        for (int i = 0; i < 4; i++) oacc[2 * b + u][i] = __builtin_fmaf(part[i], vref, oacc[2 * b + u][i]);
                     }
                 }
             }
