@@ -38,13 +38,23 @@ __device__ __forceinline__ v4f32_t mfma16(const v8h_t &a, const v8h_t &b, const 
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// 8 floats -> f16 high parts and f16 residuals
+// 8 floats -> f16 high parts and f16 residuals.  The high part is rounded
+// toward zero by v_cvt_pkrtz_f16_f32, an operation the compiler cannot
+// re-derive from the expression that produced x: a plain conversion let it
+// form the high part straight from a product (one rounding, v_fma_mix) for
+// the residual while storing the conversion of the rounded fp32 product, so
+// the two could differ by one f16 unit.  x - hi is exact in fp32 and leaves
+// one f16 rounding for the residual (~22 bits together).
 __device__ __forceinline__ void split8(const float *x, v8h_t &hi, v8h_t &lo) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const _Float16 h = (_Float16)x[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(x[i] - (float)h);
+    for (int i = 0; i < 8; i += 2) {
+        const auto h2 = __builtin_amdgcn_cvt_pkrtz(x[i], x[i + 1]);
+        _Float16 h[2];
+        __builtin_memcpy(h, &h2, 4);
+        hi[i] = h[0];
+        hi[i + 1] = h[1];
+        lo[i] = (_Float16)(x[i] - (float)h[0]);
+        lo[i + 1] = (_Float16)(x[i + 1] - (float)h[1]);
     }
 }
 
@@ -214,6 +224,16 @@ __device__ __forceinline__ v8h_t c2x8_to_h8(uint32_t w) {
     return r - bias;
 }
 
+// LDS written by other lanes of this wave becomes readable: wait for this
+// wave's LDS operations only (lgkmcnt 0; vector memory loads stay in flight)
+// and keep the compiler from moving LDS accesses across.
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // One workgroup = (split s, kv head kvh, query z); waves take 32-token
 // blocks of the split's chunk round-robin.
 template <typename KT, int D, int G, int NTH = kAttmThreads>
@@ -221,8 +241,12 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     constexpr int DT = D / 32, NT = D / 16, NW = NTH / 64;
     constexpr int OPT = (G * D + NTH - 1) / NTH;
     static_assert(2 * G <= 16, "query heads (hi/lo rows) exceed the MFMA tile");
-    __shared__ float sp[NW][G][kAttmBlock];  // p of the current block (per wave)
-    __shared__ float vsc[NW][kAttmBlock][DT];  // Q8: V scales of the block's slots
+    constexpr bool KIVI = std::is_same<KT, KvKivi>::value;
+    constexpr bool QV = KIVI || std::is_same<KT, KvQ8>::value;  // quantized V: scales folded into P
+    __shared__ __align__(16) float sp[NW][G][kAttmBlock];  // p of the current block (per wave)
+    __shared__ __align__(16) float vrat[QV ? NW : 1][DT][kAttmBlock];  // V scale / block maximum per (32-ch group, slot)
+    // PV A operands of the quantized-V paths, per 32-channel group: rows (head, high / residual) x slots
+    __shared__ __align__(16) _Float16 apb[QV ? NW : 1][DT][2 * G][kAttmBlock];
     __shared__ float vmax[NW][DT];             // Q8: their maximum per 32-channel block
     __shared__ float red[NW][G * D];         // per-wave O, then the workgroup output
     __shared__ float wm[NW][G], wl[NW][G];
@@ -230,12 +254,13 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     __shared__ int is_last;
     __shared__ int8_t nk[D], nv[D];              // Q8 decode step: the new token's codes
     __shared__ uint16_t nks[D / 32], nvs[D / 32];  // and scales
-    constexpr bool KIVI = std::is_same<KT, KvKivi>::value;
-    __shared__ uint32_t kpar[KIVI ? NW : 1][KIVI ? D : 1];   // KIVI: K (scale, min) of the block's group
-    __shared__ float vmn[KIVI ? NW : 1][KIVI ? kAttmBlock : 1][KIVI ? DT : 1];  // KIVI: V min per (slot, 32-ch group)
+    __shared__ __align__(16) uint32_t kpar[KIVI ? NW : 1][KIVI ? D : 1];   // KIVI: K (scale, min) of the block's group
+    __shared__ __align__(16) float vmn[KIVI ? NW : 1][KIVI ? DT : 1][KIVI ? kAttmBlock : 1];  // KIVI: V min per (32-ch group, slot)
+    // KIVI scores A operand: rows (head, high / residual) x channels of q * K scale
+    __shared__ __align__(16) _Float16 akb[KIVI ? NW : 1][KIVI ? 2 * G : 1][KIVI ? D : 8];
     __shared__ float kbias[KIVI ? NW : 1][G], vbias[KIVI ? NW : 1][G][DT];
     __shared__ uint16_t nkh[KIVI ? D : 1], nvh[KIVI ? D : 1];  // KIVI decode step: the new token in binary16
-    __shared__ float qs[KIVI ? G : 1][KIVI ? D : 1];             // KIVI: the query rows
+    __shared__ __align__(16) float qs[KIVI ? G : 1][KIVI ? D : 1];  // KIVI: the query rows
 
     AttnArgs a = a0;
     const int zq = (int)blockIdx.z;
@@ -448,38 +473,46 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     for (int b = 0; b < DT; b++) {
                         const uint32_t sm = okt ? tile.vp[b] : 0u;
                         const float sv = h2f((uint16_t)(sm & 0xFFFF));
-                        vmn[wave][lane][b] = h2f((uint16_t)(sm >> 16));
+                        vmn[wave][b][lane] = h2f((uint16_t)(sm >> 16));
                         float mx = row_max<16>(sv);
                         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                        vsc[wave][lane][b] = mx > 0.0f ? sv * __builtin_amdgcn_rcpf(mx) : 0.0f;
+                        vrat[wave][b][lane] = mx > 0.0f ? sv * __builtin_amdgcn_rcpf(mx) : 0.0f;
                         if (lane == 0) vmax[wave][b] = mx;
                     }
                 }
-                __builtin_amdgcn_s_waitcnt(0);
-                __builtin_amdgcn_wave_barrier();
-                // A operand (q * scale, high / residual) and the bias sum(q * min)
-                float kb = 0.0f;
-                const int gq = min(r >> 1, G - 1);
-                const float qz = (r >> 1) < G ? 1.0f : 0.0f;
+                lds_wave_sync();
+                // scores A operand: each lane forms 8 distinct products
+                // q[g][c] * scale[c] (channels 8j .. 8j+7 of head g), split
+                // high / residual into rows 2g / 2g+1, and its part of the
+                // head's bias sum_c q[g][c] * min[c]
+                constexpr int CJ = D / 8, KU = G * CJ;
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    float x[8];
+                for (int u0 = 0; u0 < KU; u0 += 64) {
+                    const int u = min(u0 + lane, KU - 1), g = u / CJ, j = u % CJ;
+                    const v4f_t q0 = *(const v4f_t *)&qs[g][8 * j], q1 = *(const v4f_t *)&qs[g][8 * j + 4];
+                    const v4i_t k0 = *(const v4i_t *)&kpar[wave][8 * j], k1 = *(const v4i_t *)&kpar[wave][8 * j + 4];
+                    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    const uint32_t sm[8] = {(uint32_t)k0.x, (uint32_t)k0.y, (uint32_t)k0.z, (uint32_t)k0.w,
+                                            (uint32_t)k1.x, (uint32_t)k1.y, (uint32_t)k1.z, (uint32_t)k1.w};
+                    float x[8], kb = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
-                        const uint32_t sm = kpar[wave][32 * dt + 8 * kg + i];
-                        const float qv = qs[gq][32 * dt + 8 * kg + i] * qz;
-                        x[i] = qv * h2f((uint16_t)(sm & 0xFFFF));
-                        kb += qv * h2f((uint16_t)(sm >> 16));
+                        x[i] = qv[i] * h2f((uint16_t)(sm[i] & 0xFFFF));
+                        kb = __builtin_fmaf(qv[i], h2f((uint16_t)(sm[i] >> 16)), kb);
                     }
                     v8h_t hi, lo;
                     split8(x, hi, lo);
-                    ak[dt] = (r & 1) ? lo : hi;
+                    kb = row_sum<(CJ < 16 ? CJ : 16)>(kb);  // the CJ lanes of head g (aligned)
+                    if (u0 + lane < KU) {
+                        *(v8h_t *)&akb[wave][2 * g][8 * j] = hi;
+                        *(v8h_t *)&akb[wave][2 * g + 1][8 * j] = lo;
+                        if (j == 0) kbias[wave][g] = kb;
+                    }
                 }
-                kb += __shfl_xor(kb, 16, 64);
-                kb += __shfl_xor(kb, 32, 64);
-                if (kg == 0 && !(r & 1) && (r >> 1) < G) kbias[wave][r >> 1] = kb;
-                __builtin_amdgcn_s_waitcnt(0);
-                __builtin_amdgcn_wave_barrier();
+                lds_wave_sync();
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+                    ak[dt] = r < 2 * G ? *(const v8h_t *)&akb[wave][r][32 * dt + 8 * kg] : v8h_t{};
             }
         }
         // ---- scores: two 16-slot halves -------------------------------------
@@ -543,7 +576,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     const float v = (tb + lane < t1) ? h2f(sv) : 0.0f;
                     float mx = row_max<16>(v);
                     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                    vsc[wave][lane][b] = mx > 0.0f ? v * __builtin_amdgcn_rcpf(mx) : 0.0f;
+                    vrat[wave][b][lane] = mx > 0.0f ? v * __builtin_amdgcn_rcpf(mx) : 0.0f;
                     if (lane == 0) vmax[wave][b] = mx;
                 }
             }
@@ -557,12 +590,47 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             oacc[nt][2] *= alpha[1];
             oacc[nt][3] *= alpha[1];
         }
+        if constexpr (QV && !H16) {
+            // quantized V: each lane forms 8 distinct products p[g][t] *
+            // ratio[b][t] (slots 8kq .. 8kq+7, head g, channel group b),
+            // split high / residual into rows 2g / 2g+1 of group b's A
+            // operand; KIVI: its part of the bias sum_t p[g][t] min[b][t]
+            constexpr int PU = G * DT * 4;
+#pragma unroll
+            for (int u0 = 0; u0 < PU; u0 += 64) {
+                const int u = min(u0 + lane, PU - 1), kq = u & 3, b = (u >> 2) % DT, g = u / (4 * DT);
+                const v4f_t p0 = *(const v4f_t *)&sp[wave][g][8 * kq], p1 = *(const v4f_t *)&sp[wave][g][8 * kq + 4];
+                const v4f_t r0 = *(const v4f_t *)&vrat[wave][b][8 * kq], r1 = *(const v4f_t *)&vrat[wave][b][8 * kq + 4];
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) x[i] = pv[i] * rv[i];
+                v8h_t hi, lo;
+                split8(x, hi, lo);
+                float vb = 0.0f;
+                if constexpr (KIVI) {
+                    const v4f_t n0 = *(const v4f_t *)&vmn[wave][b][8 * kq], n1 = *(const v4f_t *)&vmn[wave][b][8 * kq + 4];
+                    const float nv8[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) vb = __builtin_fmaf(pv[i], nv8[i], vb);
+                    vb = row_sum<4>(vb);  // the 4 slot chunks of (g, b)
+                }
+                if (u0 + lane < PU) {
+                    *(v8h_t *)&apb[wave][b][2 * g][8 * kq] = hi;
+                    *(v8h_t *)&apb[wave][b][2 * g + 1][8 * kq] = lo;
+                    if constexpr (KIVI)
+                        if (kq == 0) vbias[wave][g][b] = vb;
+                }
+            }
+            lds_wave_sync();
+        }
         {
             const int m = r, g = m >> 1;
-            float p[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) p[i] = g < G ? sp[wave][g][8 * kg + i] : 0.0f;
             if constexpr (H16) {
+                float p[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) p[i] = g < G ? sp[wave][g][8 * kg + i] : 0.0f;
                 v8h_t hi, lo;
                 split8(p, hi, lo);
                 const v8h_t ap = (m & 1) ? lo : hi;
@@ -576,18 +644,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                     for (int b = 0; b < DT; b++) {
                         const float vref = vmax[wave][b];
-                        float pb[8], vb = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < 8; i++) {
-                            pb[i] = p[i] * vsc[wave][8 * kg + i][b];
-                            vb += p[i] * vmn[wave][8 * kg + i][b];
-                        }
-                        vb += __shfl_xor(vb, 16, 64);
-                        vb += __shfl_xor(vb, 32, 64);
-                        if (kg == 0 && !(m & 1) && g < G) vbias[wave][g][b] = vb;
-                        v8h_t hi, lo;
-                        split8(pb, hi, lo);
-                        const v8h_t ap = (m & 1) ? lo : hi;
+                        const v8h_t ap = m < 2 * G ? *(const v8h_t *)&apb[wave][b][m][8 * kg] : v8h_t{};
 #pragma unroll
                         for (int u = 0; u < 2; u++) {
                             const int nt = 2 * b + u;
@@ -597,8 +654,6 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                             for (int i = 0; i < 4; i++) oacc[nt][i] = __builtin_fmaf(part[i], vref, oacc[nt][i]);
                         }
                     }
-                    __builtin_amdgcn_s_waitcnt(0);
-                    __builtin_amdgcn_wave_barrier();
                     // rows 4kg + i of oacc: head 2kg + i/2, (hi, lo); the bias goes on the hi row
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
@@ -613,12 +668,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                 for (int b = 0; b < DT; b++) {
                     const float vref = vmax[wave][b];
-                    float pb[8];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) pb[i] = p[i] * vsc[wave][8 * kg + i][b];
-                    v8h_t hi, lo;
-                    split8(pb, hi, lo);
-                    const v8h_t ap = (m & 1) ? lo : hi;
+                    const v8h_t ap = m < 2 * G ? *(const v8h_t *)&apb[wave][b][m][8 * kg] : v8h_t{};
 #pragma unroll
                     for (int u = 0; u < 2; u++) {
                         const v4f32_t part =

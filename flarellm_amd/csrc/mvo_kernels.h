@@ -106,7 +106,12 @@ __global__ __launch_bounds__(kMvoThreads) void k_mvo(MvoArgs a) {
         if (a.nw) inv = wg_inv_rms(x, K, a.eps, red);
         for (int i = threadIdx.x; i < K; i += blockDim.x) {
             const float v = a.nw ? (x[i] * inv) * a.nw[i] : x[i];
-            const _Float16 h = (_Float16)v;
+            // high part rounded toward zero by v_cvt_pkrtz (the compiler
+            // cannot re-form it from the product, so hi and the residual
+            // come from the same fp32 v)
+            const auto h2 = __builtin_amdgcn_cvt_pkrtz(v, 0.0f);
+            _Float16 h;
+            __builtin_memcpy(&h, &h2, 2);
             xa[(size_t)(2 * t) * K + i] = h;
             xa[(size_t)(2 * t + 1) * K + i] = (_Float16)(v - (float)h);
         }
