@@ -169,8 +169,8 @@ __device__ __forceinline__ void ld_words(const void *p, uint32_t *w) {
 template <int D>
 struct AttmKiviQ {
     static constexpr int DT = D / 32, KW = D / 64;
-    uint32_t k[2][KW];  // [slot half] 16 bits per 32-channel tile
-    uint32_t v[DT];     // 16 bits per 16-channel tile
+    uint32_t k[2][KW];  // [slot half] word w: 32-channel tiles 2w, 2w+1 (runs A, B)
+    uint32_t v[DT];     // word w: 16-channel tiles 2w, 2w+1 (runs A, B)
     uint32_t kp[KW];    // K pairs of channels lane + 64i (the block's group)
     uint32_t vp[DT];    // V pairs of slot tb + lane % 32, per 32-channel group
     __device__ __forceinline__ void load(const AttnArgs &a, int kvh, int tb, int tlast, int lane) {
@@ -209,19 +209,27 @@ struct AttmTile<KvKivi, D> {
     }
 };
 
-// 8 two-bit codes (bits 2j of w, w < 2^16) -> f16 0..3, exact: code 2i to
-// bits 4i, code 2i+1 to bits 16+4i, then each half-word of 0x6400 | c is
-// binary16 1024 + c, and subtracting 1024 leaves c.
-__device__ __forceinline__ v8h_t c2x8_to_h8(uint32_t w) {
-    const uint32_t t = (w & 0x3333u) | ((w & 0xCCCCu) << 14);
+// Run `run` of a KIVI code word (kivi_bit placement) -> 8 x binary16
+// 1 + code/4, exact: one shift moves each code pair to bits 8 and 24, which
+// go under 0x3C00 (1.0).  Operands of the form 1 + c/4 keep the MFMA sums'
+// magnitudes near those of the codes; the callers scale the other operand
+// by 4 and subtract its sum (a bias term): sum a (1 + c/4) * 4 - 4 sum a =
+// sum a c.
+// m: 0x03000300 held in a vector register (kivi_mask), so that each pair is
+// one v_and_or_b32 (a VOP3 instruction reads at most one scalar / constant
+// operand here).
+__device__ __forceinline__ uint32_t kivi_mask() {
+    uint32_t m = 0x03000300u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ v8h_t kivi_unpack(uint32_t w, int run, uint32_t m) {
     uint32_t d[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) d[i] = ((t >> (4 * i)) & 0x00030003u) | 0x64006400u;
+    for (int k = 0; k < 4; k++) d[k] = ((run ? w << (8 - 2 * k) : w >> (2 * k)) & m) | 0x3C003C00u;
     v8h_t r;
     __builtin_memcpy(&r, d, 16);
-    const _Float16 k = (_Float16)1024.0f;
-    const v8h_t bias = {k, k, k, k, k, k, k, k};
-    return r - bias;
+    return r;
 }
 
 // LDS written by other lanes of this wave becomes readable: wait for this
@@ -353,10 +361,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 for (int i = 0; i < 8; i++) x[i] = 0.0f;
             }
             if constexpr (KIVI) {
-                // the f32 query in LDS (scaled per 2-bit channel in each quantized block)
+                // 4 x the f32 query in LDS (scaled per 2-bit channel in each quantized block)
                 if (!(m & 1) && (m >> 1) < G) {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) qs[g][32 * dt + 8 * kg + i] = x[i];
+                    for (int i = 0; i < 8; i++) qs[g][32 * dt + 8 * kg + i] = 4.0f * x[i];  // exact
                 }
             }
             v8h_t hi, lo;
@@ -366,6 +374,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     }
     const float scale = 1.0f / sqrtf((float)D);
     if constexpr (KIVI) __syncthreads();  // qs
+    const uint32_t kmask = KIVI ? kivi_mask() : 0u;
     ATTN_TS(1);
 
     // wave-private online softmax state; lane group kg holds heads 2kg, 2kg+1
@@ -476,15 +485,16 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                         vmn[wave][b][lane] = h2f((uint16_t)(sm >> 16));
                         float mx = row_max<16>(sv);
                         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                        vrat[wave][b][lane] = mx > 0.0f ? sv * __builtin_amdgcn_rcpf(mx) : 0.0f;
+                        vrat[wave][b][lane] = mx > 0.0f ? 4.0f * (sv * __builtin_amdgcn_rcpf(mx)) : 0.0f;  // 4 x ratio
                         if (lane == 0) vmax[wave][b] = mx;
                     }
                 }
                 lds_wave_sync();
                 // scores A operand: each lane forms 8 distinct products
-                // q[g][c] * scale[c] (channels 8j .. 8j+7 of head g), split
+                // 4 q[g][c] scale[c] (channels 8j .. 8j+7 of head g), split
                 // high / residual into rows 2g / 2g+1, and its part of the
-                // head's bias sum_c q[g][c] * min[c]
+                // head's bias sum_c q[g][c] min[c] - sum_c (high + residual)
+                // (the B operand is 1 + code/4)
                 constexpr int CJ = D / 8, KU = G * CJ;
 #pragma unroll
                 for (int u0 = 0; u0 < KU; u0 += 64) {
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
                     const uint32_t sm[8] = {(uint32_t)k0.x, (uint32_t)k0.y, (uint32_t)k0.z, (uint32_t)k0.w,
                                             (uint32_t)k1.x, (uint32_t)k1.y, (uint32_t)k1.z, (uint32_t)k1.w};
-                    float x[8], kb = 0.0f;
+                    float x[8], kb = 0.0f, hs = 0.0f;  // qs holds 4 q
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
                         x[i] = qv[i] * h2f((uint16_t)(sm[i] & 0xFFFF));
@@ -502,6 +512,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                     }
                     v8h_t hi, lo;
                     split8(x, hi, lo);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) hs += (float)hi[i] + (float)lo[i];  // exact pair sums
+                    kb = __builtin_fmaf(kb, 0.25f, -hs);
                     kb = row_sum<(CJ < 16 ? CJ : 16)>(kb);  // the CJ lanes of head g (aligned)
                     if (u0 + lane < KU) {
                         *(v8h_t *)&akb[wave][2 * g][8 * j] = hi;
@@ -525,10 +538,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) acc = mfma16(aq[dt], as_h8(tile.k[h][dt]), acc);
             } else if constexpr (KQ) {
-                // codes of this lane's slot: 16 bits per 32-channel tile
+                // codes of this lane's slot: word dt/2, run dt%2 per 32-channel tile
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
-                    acc = mfma16(ak[dt], c2x8_to_h8((tile.k[h][dt >> 1] >> (16 * (dt & 1))) & 0xFFFFu), acc);
+                    acc = mfma16(ak[dt], kivi_unpack(tile.k[h][dt >> 1], dt & 1, kmask), acc);
                 kbh[0] = 2 * kg < G ? kbias[wave][2 * kg] : 0.0f;
                 kbh[1] = 2 * kg + 1 < G ? kbias[wave][2 * kg + 1] : 0.0f;
             } else {
@@ -603,6 +616,8 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 const v4f_t r0 = *(const v4f_t *)&vrat[wave][b][8 * kq], r1 = *(const v4f_t *)&vrat[wave][b][8 * kq + 4];
                 const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
                 const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+                // KIVI: the B operand is 1 + code/4, so the ratios carry a
+                // factor 4 and the bias also takes vref * sum_t (high + residual)
                 float x[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++) x[i] = pv[i] * rv[i];
@@ -612,8 +627,13 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 if constexpr (KIVI) {
                     const v4f_t n0 = *(const v4f_t *)&vmn[wave][b][8 * kq], n1 = *(const v4f_t *)&vmn[wave][b][8 * kq + 4];
                     const float nv8[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+                    float hs = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) vb = __builtin_fmaf(pv[i], nv8[i], vb);
+                    for (int i = 0; i < 8; i++) {
+                        vb = __builtin_fmaf(pv[i], nv8[i], vb);
+                        hs += (float)hi[i] + (float)lo[i];  // exact pair sum
+                    }
+                    vb = __builtin_fmaf(-vmax[wave][b], hs, vb);
                     vb = row_sum<4>(vb);  // the 4 slot chunks of (g, b)
                 }
                 if (u0 + lane < PU) {
@@ -648,7 +668,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                         for (int u = 0; u < 2; u++) {
                             const int nt = 2 * b + u;
-                            const v4f32_t part = mfma16(ap, c2x8_to_h8((vw[nt >> 1] >> (16 * (nt & 1))) & 0xFFFFu),
+                            const v4f32_t part = mfma16(ap, kivi_unpack(vw[nt >> 1], nt & 1, kmask),
                                                         v4f32_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                             for (int i = 0; i < 4; i++) oacc[nt][i] = __builtin_fmaf(part[i], vref, oacc[nt][i]);

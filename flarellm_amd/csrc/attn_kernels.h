@@ -231,19 +231,17 @@ struct NewRow<KvQ8> {
         }
     }
 };
-// KIVI code placement.
-//  K (token rows of D/4 bytes): channel c = 32dt + 8kg + j sits at byte
-//    kg*(D/16) + 2dt + j/4, bits 2(j%4), so the codes an MFMA lane group kg
-//    needs for one token (8 channels of every 32-channel tile) are contiguous.
-//  V (D*8 bytes per 32-token group): channel c = 16nt + r and group token
-//    8kg + j sit at byte ((kg*16 + r)*(D/16) + nt)*2 + j/4, bits 2(j%4): one
-//    lane (kg, r) reads the 8 tokens of its channel in every 16-channel tile.
-__host__ __device__ inline int kivi_kbyte(int c, int D) {
-    return ((c & 31) >> 3) * (D / 16) + 2 * (c >> 5) + ((c & 7) >> 2);
-}
-__host__ __device__ inline int kivi_vbyte(int c, int tl, int D) {
-    return (((tl >> 3) * 16 + (c & 15)) * (D / 16) + (c >> 4)) * 2 + ((tl & 7) >> 2);
-}
+// KIVI code placement: 32-bit words of 16 codes, two runs of 8 (run A, run
+// B); code j of run A at bit 8 + 2(j/2) + 16(j%2), of run B at bit 2(j/2) +
+// 16(j%2), so that code pair (2k, 2k+1) of a run reaches bits 8 and 24 (the
+// units of 1/4 under binary16 1.0 in each half-word) with a single shift.
+//  K (token rows of D/16 words): word kg*(D/64) + w holds channels
+//    64w + 8kg + j (run A, 32-channel tile 2w) and 64w + 32 + 8kg + j (run B,
+//    tile 2w+1): the codes an MFMA lane group kg needs for one token.
+//  V (2D words per 32-token group): word (kg*16 + r)*(D/32) + w holds group
+//    tokens 8kg + j of channel 32w + r (run A, 16-channel tile 2w) and of
+//    channel 32w + 16 + r (run B, tile 2w+1): what lane (kg, r) reads.
+__host__ __device__ inline int kivi_bit(int j, int run) { return (run ? 0 : 8) + 2 * (j >> 1) + 16 * (j & 1); }
 // ring slot of token t; the ring V is stored in 32-slot transposed blocks
 __host__ __device__ inline size_t kivi_ring_k(int kvh, int t, int c, int D) {
     return ((size_t)kvh * kKiviRing + (size_t)(t % kKiviRing)) * D + c;
@@ -288,27 +286,41 @@ template <typename Src>
 __device__ __forceinline__ void kivi_quantize_group(const AttnArgs &a, int D, int kvh, int gi, Src src, float *lds) {
     const int tid = threadIdx.x, nt = blockDim.x, DT = D >> 5;
     const int t0 = gi * kKiviGroup;
-    for (int idx = tid; idx < D / 4; idx += nt) {
-        KiviQ qz[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float lo = INFINITY, hi = -INFINITY;
-            for (int t = 0; t < kKiviGroup; t++) {
-                const float v = src(t0 + t, 4 * idx + i, false);
-                lo = v < lo ? v : lo;
-                hi = v > hi ? v : hi;
-            }
-            qz[i].init(lo, hi);
-            a.kp[((size_t)kvh * (a.S >> 5) + gi) * D + 4 * idx + i] = qz[i].packed();
-        }
-        const int kb = kivi_kbyte(4 * idx, D);
+    // K parameters per channel over the group's 32 tokens
+    for (int c = tid; c < D; c += nt) {
+        float lo = INFINITY, hi = -INFINITY;
         for (int t = 0; t < kKiviGroup; t++) {
-            uint32_t b = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) b |= qz[i].code(src(t0 + t, 4 * idx + i, false)) << (2 * i);
-            ((uint8_t *)a.kc)[((size_t)kvh * a.S + t0 + t) * (D >> 2) + kb] = (uint8_t)b;
+            const float v = src(t0 + t, c, false);
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
         }
+        KiviQ qz;
+        qz.init(lo, hi);
+        a.kp[((size_t)kvh * (a.S >> 5) + gi) * D + c] = qz.packed();
+        lds[3 * c] = qz.mn;
+        lds[3 * c + 1] = qz.inv;
+        lds[3 * c + 2] = qz.scale;
     }
+    __syncthreads();
+    // K codes: one word (16 channels of one token) per thread
+    const int KWR = D / 16;
+    for (int idx = tid; idx < kKiviGroup * KWR; idx += nt) {
+        const int t = idx / KWR, wi = idx % KWR, kg = wi / (D / 64), w = wi % (D / 64);
+        uint32_t word = 0;
+#pragma unroll
+        for (int run = 0; run < 2; run++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int c = 64 * w + 32 * run + 8 * kg + j;
+                KiviQ qz;
+                qz.mn = lds[3 * c];
+                qz.inv = lds[3 * c + 1];
+                qz.scale = lds[3 * c + 2];
+                word |= qz.code(src(t0 + t, c, false)) << kivi_bit(j, run);
+            }
+        ((uint32_t *)a.kc)[((size_t)kvh * a.S + t0 + t) * KWR + wi] = word;
+    }
+    __syncthreads();  // lds is reused for the V parameters
     // V parameters per (token, 32-channel group)
     for (int idx = tid; idx < kKiviGroup * DT; idx += nt) {
         const int tl = idx % kKiviGroup, cg = idx / kKiviGroup;
@@ -327,20 +339,25 @@ __device__ __forceinline__ void kivi_quantize_group(const AttnArgs &a, int D, in
     }
     __syncthreads();
     // V codes: one byte = 4 tokens of one channel
-    uint8_t *vg = (uint8_t *)a.vc + ((size_t)kvh * (a.S >> 5) + gi) * (size_t)(D * 8);
-    for (int idx = tid; idx < D * 8; idx += nt) {
-        const int c = idx >> 3, q = idx & 7;
-        uint32_t b = 0;
+    // V codes: one word (8 tokens of two channels) per thread
+    uint32_t *vg = (uint32_t *)a.vc + ((size_t)kvh * (a.S >> 5) + gi) * (size_t)(2 * D);
+    for (int idx = tid; idx < 2 * D; idx += nt) {
+        const int ln = idx / DT, w = idx % DT, kg = ln >> 4, r = ln & 15;
+        uint32_t word = 0;
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const int tl = 4 * q + jj, li = (c >> 5) * kKiviGroup + tl;
-            KiviQ qz;
-            qz.mn = lds[3 * li];
-            qz.inv = lds[3 * li + 1];
-            qz.scale = lds[3 * li + 2];
-            b |= qz.code(src(t0 + tl, c, true)) << (2 * jj);
+        for (int run = 0; run < 2; run++) {
+            const int c = 32 * w + 16 * run + r;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int tl = 8 * kg + j, li = (c >> 5) * kKiviGroup + tl;
+                KiviQ qz;
+                qz.mn = lds[3 * li];
+                qz.inv = lds[3 * li + 1];
+                qz.scale = lds[3 * li + 2];
+                word |= qz.code(src(t0 + tl, c, true)) << kivi_bit(j, run);
+            }
         }
-        vg[kivi_vbyte(c, 4 * q, D)] = (uint8_t)b;
+        vg[idx] = word;
     }
     __syncthreads();
 }
