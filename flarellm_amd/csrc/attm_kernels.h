@@ -109,10 +109,8 @@ struct AttmTile<__half, D> {
     }
 };
 
-// Q8: int8 codes + f16 scale per (slot, 32-channel block).  K and V halves
-// load separately: a wave issues the next block's K as soon as the current
-// scores are formed and its V once P V is done, so each half is in flight
-// over the other half's arithmetic without a second tile of registers.
+// Q8: int8 codes + f16 scale per (slot, 32-channel block), with the V
+// scales of slot tb + lane % 32.
 template <int D>
 struct AttmTile<KvQ8, D> {
     static constexpr int DT = D / 32, NT = D / 16, VW = (DT + 1) / 2;
@@ -384,9 +382,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
 
     // one 32-slot block (slots tb .. tb+31) with its tile in registers
-    // nxt >= 0 (Q8): block index whose K / V the tile loads once the current
-    // block's K / V registers are consumed
-    auto process = [&](auto &tile, int bi, int nxt) {
+    auto process = [&](auto &tile, int bi) {
         using TT = typename std::remove_reference<decltype(tile)>::type;
         constexpr bool KQ = std::is_same<TT, AttmKiviQ<D>>::value;                 // 2-bit block
         constexpr bool H16 = std::is_same<KT, __half>::value || (KIVI && !KQ);    // fp16 operands
@@ -559,8 +555,6 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             sc[h][0] = ok && t != lastA0 ? (acc[0] + acc[1] + kbh[0]) * scale : -INFINITY;
             sc[h][1] = ok && t != lastA1 ? (acc[2] + acc[3] + kbh[1]) * scale : -INFINITY;
         }
-        if constexpr (std::is_same<KT, KvQ8>::value)
-            if (nxt >= 0) tile.load_k(a, kvh, t0 + nxt * kAttmBlock, t1 - 1, lane);
         if (bi == wave) ATTN_TS(2);
         // ---- online softmax per head (rows of 16 lanes hold one head pair) --
         float alpha[2];
@@ -699,40 +693,36 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 }
             }
         }
-        if constexpr (std::is_same<KT, KvQ8>::value)
-            if (nxt >= 0) tile.load_v(a, kvh, t0 + nxt * kAttmBlock, t1 - 1, lane);
         __builtin_amdgcn_wave_barrier();
     };
-    if constexpr (std::is_same<KT, __half>::value) {
+    if constexpr (!KIVI) {
         // ping-pong: the wave's next block is in flight while this one computes
+        // (Q8 at D = 128: 248 VGPRs with both tiles, no spills; 128k slots
+        // 74 -> 71 us against reloading each half as it is consumed)
         AttmTile<KT, D> tile2;
         for (int bi = wave; bi < nblk; bi += 2 * NW) {
             if (bi + NW < nblk) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi, -1);
+            process(tile, bi);
             if (bi + NW >= nblk) break;
             if (bi + 2 * NW < nblk) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW, -1);
+            process(tile2, bi + NW);
         }
     } else if constexpr (KIVI) {
         // 2-bit blocks ping-pong (small tiles), then the ring blocks
         Tile0 tile2;
         for (int bi = wave; bi < nqb; bi += 2 * NW) {
             if (bi + NW < nqb) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi, -1);
+            process(tile, bi);
             if (bi + NW >= nqb) break;
             if (bi + 2 * NW < nqb) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW, -1);
+            process(tile2, bi + NW);
         }
         AttmTile<KvKivi, D> rt;
         const int bi0 = nqb > wave ? wave + (nqb - wave + NW - 1) / NW * NW : wave;
         for (int bi = bi0; bi < nblk; bi += NW) {
             rt.load(a, kvh, t0 + bi * kAttmBlock, t1 - 1, lane);
-            process(rt, bi, -1);
+            process(rt, bi);
         }
-    } else {
-        // Q8 (more registers per block): one tile, loaded at the top; the
-        // next block's K and V halves load as the current halves are consumed
-        for (int bi = wave; bi < nblk; bi += NW) process(tile, bi, bi + NW < nblk ? bi + NW : -1);
     }
     if constexpr (KIVI) {
         // decode step that ages group qlen/32 out of the fp16 residual: split
