@@ -1,5 +1,6 @@
 // Decode attention launchers and the Q8 / KIVI cache writers.
 #include "attm_kernels.h"
+#include "attq_kernels.h"
 #include "launch.h"
 
 namespace fl {
@@ -55,6 +56,25 @@ int attm_resident_per_cu(int kvfmt, int D, int G, int waves) {
     if (kvfmt == KV_Q8) return attm_resident_t<KvQ8>(D, G, waves);
     if (kvfmt == KV_KIVI) return attm_resident_t<KvKivi>(D, G, waves);
     return 0;
+}
+
+// Several queries over an fp16 cache (V in transposed blocks): query pairs
+// in groups of NW per workgroup (4 or 8 waves), K/V blocks shared in LDS.
+hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a) {
+    const int npairs = a.nq / 2;
+    if (a.nq < 2 || a.nq % 2 || !a.v_tblk || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32 || a.chmin < 1)
+        return hipErrorInvalidValue;
+    const int NW = npairs <= 4 ? 4 : 8;
+    const dim3 grid(a.nsplit, a.nkv, (npairs + NW - 1) / NW);
+#define C(DD, GG)                                                                                     \
+    if (D == DD && G == GG) {                                                                         \
+        if (NW == 4) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4>), grid, dim3(256), 0, st, a);          \
+        else hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8>), grid, dim3(512), 0, st, a);                  \
+        return hipGetLastError();                                                                     \
+    }
+    C(64, 1) C(64, 2) C(64, 4) C(128, 1) C(128, 2) C(128, 4)
+#undef C
+    return hipErrorNotSupported;
 }
 
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq) {

@@ -52,6 +52,7 @@ struct AttnArgs {
     // query heads of queries 2z and 2z+1 (kernel G = 2 x the model's) share
     // each K/V block, query 2z masking slot *posp + 2z + 1
     int qpair;
+    int nq;  // k_attq: queries of the pass (even)
 };
 
 // Offset of (slot t, channel d) in one kv head's transposed V store.

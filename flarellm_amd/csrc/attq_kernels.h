@@ -1,0 +1,297 @@
+// Causal GQA attention for several consecutive query tokens over an fp16
+// cache (speculative-verify and prefill passes).
+//
+// Same semantics as k_attm's query-pair mode (cpu_grouped_query_attention_into,
+// flare-core/src/model.rs:9849-9966; causal prefill attention 336-368):
+// query j of the pass sits at position *posp + j and attends slots
+// 0 .. *posp + j.  The difference is the data flow: k_attm gives every query
+// pair its own workgroup, each streaming the whole K/V prefix of its kv head,
+// so a pass of M tokens reads the cache M/2 times.  Here one workgroup holds
+// NW query pairs (one per wave) and stages each 32-slot K/V block in LDS once
+// for all of them:
+//  * grid (split, kv head, pair group); the split's chunk of slots is walked
+//    block by block, the next block's global loads in flight (registers)
+//    while the waves compute on the current one (double-buffered LDS, one
+//    workgroup barrier per block);
+//  * per wave, the fp16 MFMA scheme of k_attm: rows (query, head, high /
+//    residual) of the pair's 2G heads, S = Q K^T and O += P V on
+//    v_mfma_f32_16x16x32_f16, wave-private online softmax;
+//  * splits publish (o, m, l) per wave with agent-scope stores; the last
+//    arriving workgroup of a (pair group, kv head) merges them (weights per
+//    row formed once, then one load per partial and output) and writes the
+//    f32 output and / or its Q8_0 copy.
+#pragma once
+
+#include "attm_kernels.h"
+
+namespace fl {
+
+constexpr int kAttqKPad = 8;  // halves of padding per staged K row
+constexpr int kAttqVPad = 8;  // per staged V channel row
+
+template <int D, int NW>
+struct AttqLds {
+    static constexpr int KS = D + kAttqKPad, VS = 32 + kAttqVPad;
+    static constexpr int KH = 32 * KS, VH = D * VS;  // halves per staged block
+    static constexpr size_t LOOP = (size_t)2 * (KH + VH) * 2;  // double-buffered K and V
+    static constexpr size_t SP = (size_t)NW * 8 * 32 * 4;       // p of the current block per wave
+    static constexpr size_t RED = (size_t)NW * 8 * D * 4;       // per-wave outputs (after the loop)
+    static constexpr size_t WT = (size_t)NW * 8 * kAttmMaxSplit * 4;  // merge weights
+    static constexpr size_t BYTES = (LOOP + SP > RED + WT ? LOOP + SP : RED + WT);
+};
+
+// G2 = rows of a query pair: the model's G heads of each of its 2 queries
+template <int D, int G2, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
+    constexpr int DT = D / 32, NT = D / 16, NTH = NW * 64, GH = G2 / 2;
+    using L = AttqLds<D, NW>;
+    constexpr int KS = L::KS, VS = L::VS;
+    static_assert(G2 <= 8 && G2 % 2 == 0, "2G rows of a query pair (hi / lo) fill at most one MFMA tile");
+    __shared__ __align__(16) char smem[L::BYTES];
+    __shared__ int is_last;
+    _Float16 *lk = (_Float16 *)smem;             // [2][32][KS]
+    _Float16 *lv = lk + 2 * L::KH;               // [2][D][VS]
+    float *sp = (float *)(smem + L::LOOP);       // [NW][8][32]
+    float *red = (float *)smem;                  // [NW][8][D], after the loop
+    float *wt = (float *)(smem + L::RED);        // [NW][8][kAttmMaxSplit]
+
+    const int kvh = blockIdx.y, s = blockIdx.x, zg = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
+    const int npairs = a.nq / 2, p = zg * NW + wave;
+    const bool live = p < npairs;  // wave-uniform
+    const int q0 = 2 * min(p, npairs - 1), q1 = q0 + 1;
+    const int glast = 2 * min(npairs, (zg + 1) * NW) - 1;  // last query of the group
+
+    // query rows first (independent of the position)
+    v4f_t qv[DT][2];
+    {
+        const int g = min(r >> 1, G2 - 1);
+        const size_t qo = (size_t)(g >= GH ? q1 : q0) * a.qstride + (size_t)(kvh * GH + g % GH) * D;
+        const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            qv[dt][0] = qp[8 * dt];
+            qv[dt][1] = qp[8 * dt + 1];
+        }
+    }
+    const int base = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int Tg = base + glast + 1;  // slots the group's last query sees
+    int CH = max(a.chmin, (Tg + a.nsplit - 1) / a.nsplit);
+    CH = (CH + kAttmBlock - 1) / kAttmBlock * kAttmBlock;
+    const int t0 = s * CH;
+    if (t0 >= Tg) return;  // whole workgroup
+    const int t1 = min(Tg, t0 + CH), nact = (Tg + CH - 1) / CH;
+    const int nblk = (t1 - t0 + kAttmBlock - 1) / kAttmBlock;
+    // rows of lane group kg: head rows 2kg + e; their query's last slot
+    int lim[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) lim[e] = base + ((2 * kg + e) >= GH ? q1 : q0);
+    const int wlim = base + q1;  // last slot any row of this wave sees
+
+    // block staging: K rows tb..tb+31 (contiguous [slot][D]) and the transposed
+    // V block ([D][32], contiguous), 16 B per thread and piece
+    constexpr int NP = 32 * D / 8, PPT = (NP + NTH - 1) / NTH;
+    const __half *kc = (const __half *)a.kc + (size_t)kvh * a.head_stride;
+    const __half *vc = (const __half *)a.vc + (size_t)kvh * a.head_stride;
+    // two register sets: block j's pieces live in set j & 1, loaded two
+    // iterations before they are staged
+    v4i_t kr[2][PPT], vr[2][PPT];
+    auto gload = [&](v4i_t(&kk)[PPT], v4i_t(&vv)[PPT], int tb) {
+        const v4i_t *ks = (const v4i_t *)(kc + (size_t)tb * D);
+        const v4i_t *vs = (const v4i_t *)(vc + vt_off(tb, 0, D));
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int i = min(tid + u * NTH, NP - 1);
+            kk[u] = ks[i];
+            vv[u] = vs[i];
+        }
+    };
+    auto lstore = [&](const v4i_t(&kk)[PPT], const v4i_t(&vv)[PPT], int buf) {
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int i = tid + u * NTH;
+            if (NP % NTH == 0 || i < NP) {
+                *(v4i_t *)(lk + buf * L::KH + (i / (D / 8)) * KS + 8 * (i % (D / 8))) = kk[u];
+                *(v4i_t *)(lv + buf * L::VH + (i >> 2) * VS + 8 * (i & 3)) = vv[u];
+            }
+        }
+    };
+    gload(kr[0], vr[0], t0);
+    if (nblk > 1) gload(kr[1], vr[1], t0 + kAttmBlock);
+
+    // A operand of S: row m = 2g + (hi / lo) of head row g (rows >= 2 G2 zero)
+    v8h_t aq[DT];
+    {
+        const int m = r;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const v4f_t x0 = qv[dt][0], x1 = qv[dt][1];
+            float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if ((m >> 1) >= G2) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) x[i] = 0.0f;
+            }
+            v8h_t hi, lo;
+            split8(x, hi, lo);
+            aq[dt] = (m & 1) ? lo : hi;
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)D);
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    v4f32_t oacc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
+    float *spw = sp + wave * 8 * 32;
+
+    lstore(kr[0], vr[0], 0);
+    if (nblk > 2) gload(kr[0], vr[0], t0 + 2 * kAttmBlock);
+    __syncthreads();
+    // block bi: computed from LDS buffer bi & 1; then block bi + 1 (register
+    // set (bi + 1) & 1) goes to the other buffer and that set loads block bi + 3
+    auto block = [&](int bi, v4i_t(&kn)[PPT], v4i_t(&vn)[PPT]) {
+        const int cur = bi & 1, tb = t0 + bi * kAttmBlock;
+        if (live && tb <= wlim) {  // wave-uniform: some row sees the block
+            const _Float16 *bk = lk + cur * L::KH, *bv = lv + cur * L::VH;
+            float sc[2][2];  // [half][head row parity] for slot tb + 16h + r
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                v4f32_t acc = v4f32_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+                    acc = mfma16(aq[dt], *(const v8h_t *)(bk + (16 * h + r) * KS + 32 * dt + 8 * kg), acc);
+                const int t = tb + 16 * h + r;
+                sc[h][0] = t < t1 && t <= lim[0] ? (acc[0] + acc[1]) * scale : -INFINITY;
+                sc[h][1] = t < t1 && t <= lim[1] ? (acc[2] + acc[3]) * scale : -INFINITY;
+            }
+            float alpha[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float bm = row_max<16>(fmaxf(sc[0][e], sc[1][e]));
+                const float mn = fmaxf(m_run[e], bm);
+                // a row that has seen nothing yet keeps m = -inf (and p = 0)
+                alpha[e] = (m_run[e] == -INFINITY) ? 0.0f : __expf(m_run[e] - mn);
+                const float p0 = sc[0][e] == -INFINITY ? 0.0f : __expf(sc[0][e] - mn);
+                const float p1 = sc[1][e] == -INFINITY ? 0.0f : __expf(sc[1][e] - mn);
+                l_run[e] = l_run[e] * alpha[e] + row_sum<16>(p0 + p1);
+                m_run[e] = mn;
+                const int g = 2 * kg + e;
+                if (g < G2) {
+                    spw[g * 32 + r] = p0;
+                    spw[g * 32 + 16 + r] = p1;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                oacc[nt][0] *= alpha[0];
+                oacc[nt][1] *= alpha[0];
+                oacc[nt][2] *= alpha[1];
+                oacc[nt][3] *= alpha[1];
+            }
+            {
+                const int m = r, g = m >> 1;
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) pv[i] = g < G2 ? spw[g * 32 + 8 * kg + i] : 0.0f;
+                v8h_t hi, lo;
+                split8(pv, hi, lo);
+                const v8h_t ap = (m & 1) ? lo : hi;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    oacc[nt] = mfma16(ap, *(const v8h_t *)(bv + (16 * nt + r) * VS + 8 * kg), oacc[nt]);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (bi + 1 < nblk) {
+            lstore(kn, vn, cur ^ 1);
+            if (bi + 3 < nblk) gload(kn, vn, tb + 3 * kAttmBlock);
+        }
+        __syncthreads();
+    };
+    for (int bi = 0; bi < nblk; bi += 2) {
+        block(bi, kr[1], vr[1]);
+        if (bi + 1 < nblk) block(bi + 1, kr[0], vr[0]);
+    }
+
+    // per-wave result: head row g = 2kg + e, channel 16nt + r
+    // (rows 4kg + 2e / + 1 of oacc: high / residual parts of P)
+    float *mypart = nullptr;
+    constexpr int P = G2 * (D + 2);
+    if (nact > 1)
+        mypart = a.part + ((((size_t)zg * a.nkv + kvh) * a.nsplit + s) * NW + wave) * P;
+    float *rw = red + wave * 8 * D;
+    if (live) {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int g = 2 * kg + e;
+            if (g < G2) {
+                const float il = nact == 1 ? 1.0f / l_run[e] : 1.0f;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const float o = oacc[nt][2 * e] + oacc[nt][2 * e + 1];
+                    if (nact == 1) rw[g * D + 16 * nt + r] = o * il;
+                    else st_agent(mypart + g * D + 16 * nt + r, o);
+                }
+                if (nact > 1 && r == 0) {
+                    st_agent(mypart + G2 * D + 2 * g, m_run[e]);
+                    st_agent(mypart + G2 * D + 2 * g + 1, l_run[e]);
+                }
+            }
+        }
+    }
+    if (nact > 1) {
+        if (!split_arrive_last<true>(&a.counters[(size_t)zg * a.nkv + kvh], nact, &is_last)) return;
+        // last workgroup: merge weights per (wave, head row), then each
+        // output over the nact partials (all loads of an output independent)
+        const float *pb = a.part + (((size_t)zg * a.nkv + kvh) * a.nsplit) * NW * P;
+        for (int i = tid; i < NW * G2; i += NTH) {
+            const int w = i / G2, g = i % G2;
+            float M = -INFINITY;
+            for (int j = 0; j < nact; j++) M = fmaxf(M, ld_agent(pb + ((size_t)j * NW + w) * P + G2 * D + 2 * g));
+            float Ls = 0.0f;
+            for (int j = 0; j < nact; j++) {
+                const float *pj = pb + ((size_t)j * NW + w) * P + G2 * D + 2 * g;
+                const float mj = ld_agent(pj);
+                const float wj = mj == -INFINITY ? 0.0f : __expf(mj - M);
+                Ls += ld_agent(pj + 1) * wj;
+                wt[(w * 8 + g) * kAttmMaxSplit + j] = wj;
+            }
+            const float il = 1.0f / Ls;
+            for (int j = 0; j < nact; j++) wt[(w * 8 + g) * kAttmMaxSplit + j] *= il;
+        }
+        __syncthreads();
+        for (int i = tid; i < NW * G2 * D; i += NTH) {
+            const int w = i / (G2 * D), gd = i % (G2 * D), g = gd / D;
+            if (zg * NW + w >= npairs) continue;
+            const float *wr = wt + (w * 8 + g) * kAttmMaxSplit;
+            float O = 0.0f;
+            int j = 0;
+            for (; j + 8 <= nact; j += 8) {
+                float ov[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) ov[k] = ld_agent(pb + ((size_t)(j + k) * NW + w) * P + gd);
+#pragma unroll
+                for (int k = 0; k < 8; k++) O += ov[k] * wr[j + k];
+            }
+            for (; j < nact; j++) O += ld_agent(pb + ((size_t)j * NW + w) * P + gd) * wr[j];
+            red[w * 8 * D + gd] = O;
+        }
+        __syncthreads();
+    } else {
+        __syncthreads();
+    }
+    // outputs of head row g of wave w: query (g >= GH ? q1 : q0), model head
+    // kvh * GH + g % GH; the f32 rows and / or their Q8_0 blocks (32 lanes each)
+    for (int b = tid >> 5; b < NW * G2 * D / 32; b += NTH / 32) {
+        const int w = b / (G2 * D / 32), gd = (b % (G2 * D / 32)) * 32, g = gd / D, c = gd % D;
+        const int pw = zg * NW + w;
+        if (pw >= npairs) continue;  // 32-lane groups: uniform
+        const int q = 2 * pw + (g >= GH ? 1 : 0);
+        const size_t e0 = (size_t)q * a.ostride + (size_t)(kvh * GH + g % GH) * D + c;
+        const float v = red[w * 8 * D + gd + (tid & 31)];
+        if (a.out) a.out[e0 + (tid & 31)] = v;
+        if (a.oq) quant_block32_lanes(v, a.oq + e0, a.os + e0 / 32, a.osum + e0 / 32);
+    }
+}
+
+}  // namespace fl

@@ -263,6 +263,7 @@ struct fl_ctx {
     size_t kvstage_rows = 0;
     float *rope = nullptr;
     int nsplit = 1, chmin = 1, single = kAttmSingle, attn_waves = 8;
+    int ncu = 256;  // compute units of the device (fl_model_init)
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
     float *bench_out = nullptr;  // output of fl_bench_layer_kernel launches
@@ -610,6 +611,12 @@ static void drop_graphs(fl_ctx *c) {
     c->graph_ready = false;
     for (auto &kv : c->vgraphs) (void)hipGraphExecDestroy(kv.second);
     c->vgraphs.clear();
+}
+
+// Split partial sets per (query, kv head) the attention kernels may publish:
+// the decode split count, or up to kAttmMaxSplit for k_attq (fp16 caches).
+static int part_splits(const fl_ctx *ctx) {
+    return ctx->kv_format == FL_KV_F16 ? std::max(ctx->nsplit, kAttmMaxSplit) : ctx->nsplit;
 }
 
 static int ensure_part(fl_ctx *ctx, size_t floats) {
@@ -1016,6 +1023,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
         const int res = attm_resident_per_cu(kv_format, c.head_dim, c.num_heads / c.num_kv_heads, ctx->attn_waves);
+        if (ncu > 0) ctx->ncu = ncu;
         const int fit = ncu > 0 && res > 0 ? std::max(1, ncu * res / c.num_kv_heads) : kAttmMaxSplit;
         ctx->nsplit = std::max(1, std::min({kAttmMaxSplit, fit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin}));
     } else {
@@ -1030,7 +1038,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     const int G = c.num_heads / c.num_kv_heads;
     // split partials for up to kPrefillTokens queries (decode uses 1), so
     // a verify batch never reallocates them
-    int rc = ensure_part(ctx, (size_t)kPrefillTokens * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    int rc = ensure_part(ctx, (size_t)kPrefillTokens * c.num_kv_heads * part_splits(ctx) * G * (c.head_dim + 2));
     if (rc) return rc;
     ALLOC(ctx, ctx->x, H * 4);
     ALLOC(ctx, ctx->qkv, (qd + 2 * kvd) * 4);
@@ -1967,7 +1975,24 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         a.osum = ctx->vasum;
         a.qstride = qd;
         a.ostride = qd;
-        {
+        // fp16 caches, even M: the query pairs of a group share each staged
+        // K/V block (k_attq), so the pass reads the cache once per group
+        static const bool no_attq = getenv("FLARE_NO_ATTQ") != nullptr;  // measurement switch
+        static const int attq_chmin = getenv("FLARE_ATTQ_CHMIN") ? std::max(32, atoi(getenv("FLARE_ATTQ_CHMIN"))) : 64;
+        // (prefill passes; the verify batches of up to 8 tokens keep k_attm's
+        // query pairs, which measured faster at 8 tokens)
+        if (!no_attq && a.qpair && M > kVerifyMaxTokens && ctx->kv_format == FL_KV_F16 && (D == 64 || D == 128)) {
+            // splits: about one workgroup per CU over (kv heads x pair groups)
+            static const int attq_ns = getenv("FLARE_ATTQ_NSPLIT") ? atoi(getenv("FLARE_ATTQ_NSPLIT")) : 0;
+            const int groups = (M / 2 + (M / 2 <= 4 ? 4 : 8) - 1) / (M / 2 <= 4 ? 4 : 8);
+            int ns = attq_ns > 0 ? attq_ns : ctx->ncu / (c.num_kv_heads * groups);
+            a.nsplit = std::max(1, std::min(kAttmMaxSplit, ns));
+            a.nq = M;
+            a.chmin = attq_chmin;
+            const hipError_t e = launch_attq(D, G, st, a);
+            if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "attention shape");
+            HIPCHK(ctx, e);
+        } else {
             const hipError_t e = launch_attn(ctx->kv_format, D, G, st, a, M);
             if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "attention shape");
             HIPCHK(ctx, e);
@@ -2066,7 +2091,7 @@ static int run_verify_pass(fl_ctx *ctx, int M, const int *pos_host, int out_mode
     const int G = c.num_heads / c.num_kv_heads;
     HIPCHK(ctx, hipMemcpyAsync(ctx->vpos, pos_host, 4, hipMemcpyHostToDevice, st));
     if (out_mode != VOUT_NONE) HIPCHK(ctx, hipMemsetAsync(ctx->vslots, 0, (size_t)M * 8, st));
-    int rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * ctx->nsplit * G * (c.head_dim + 2));
+    int rc = ensure_part(ctx, (size_t)M * c.num_kv_heads * part_splits(ctx) * G * (c.head_dim + 2));
     if (rc) return rc;
     // F32 / F16 / Q8 caches: one captured graph per (batch size, output
     // mode) (the positions are read from the device); KIVI plans its group

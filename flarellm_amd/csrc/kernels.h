@@ -163,13 +163,15 @@ __device__ __forceinline__ float fl_expf(float x) {
 // agent-scope atomic stores; returns true (in every thread) in the workgroup
 // that arrives last, after which its agent-scope loads see every other
 // workgroup's partials.  RESET: the last arrival sets the counter back to 0.
-//   FLARE_SPLIT_SYNC 2 (default): each wave's agent-scope release fence (its
-//     stores complete and visible at agent scope) before the barrier, thread
-//     0 counts with an acq_rel RMW, the last workgroup's waves acquire at
-//     agent scope before loading.
-//   1: wait for the wave's own stores (s_waitcnt 0), barrier, relaxed RMW.
+//   FLARE_SPLIT_SYNC 1 (default): each wave waits for its own stores
+//     (s_waitcnt 0), workgroup barrier, thread 0 counts with a relaxed
+//     agent-scope RMW; the partials themselves move only through agent-scope
+//     atomic stores / loads.
+//   2: each wave's agent-scope release fence before the barrier, thread 0
+//     counts with an acq_rel RMW, the last workgroup's waves acquire at agent
+//     scope before loading (an L2 writeback + invalidate on gfx950).
 //   0: barrier, thread 0's acq_rel RMW only.
-// (1 and 0 are measurement builds.)
+// (2 and 0 are measurement builds.)
 // ------------------------------------------------------------------------
 #ifndef FLARE_SPLIT_SYNC
 #define FLARE_SPLIT_SYNC 1

@@ -130,6 +130,7 @@ hipError_t launch_mvs_gu_q8_0(const MvsPlan &p, hipStream_t st, const MvsArgs &a
 hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a);
 enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2, KV_KIVI = 3 };  // == FL_KV_*
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq = 1);
+hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a);
 // workgroups of the MFMA attention kernel (format, D, G, waves) resident on one CU at once
 int attm_resident_per_cu(int kvfmt, int D, int G, int waves);
 // Write n token rows (device f32 [n][nkv][D]) at positions p0.. into a Q8 or

@@ -232,9 +232,11 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kPgStride = 256 + 32;  // LDS row stride of one step's codes (bank spread)
 
+// One step's activation pieces in registers: 4 x 16 B of the 64 x 256 codes
+// and 2 of the 64 x 8 (scale, scale * code sum) pairs per thread.
 struct PgStage {
-    v4i_t q[4];    // 4 x 16 B of the 64 x 256 codes per thread
-    float2 sc[2];  // 2 of the 64 x 8 (scale, sum) pairs per thread
+    v4i_t q[4];
+    float2 sc[2];
 };
 
 __device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage &r) {
@@ -254,7 +256,9 @@ __device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage &r) {
     }
 }
 
-__device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float2 *lsc) {
+// codes [token][kPgStride]; scales and scale * code sums as [block][token]
+// planes, so the four tokens of an MFMA output lane are one 16-B read each
+__device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls, float *lq) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -262,13 +266,31 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float2 *l
         *(v4i_t *)(lx + (i >> 4) * kPgStride + 16 * (i & 15)) = r.q[u];
     }
 #pragma unroll
-    for (int u = 0; u < 2; u++) lsc[t + 256 * u] = r.sc[u];
+    for (int u = 0; u < 2; u++) {
+        const int i = t + 256 * u, o = (i & 7) * 64 + (i >> 3);
+        ls[o] = r.sc[u].x;
+        lq[o] = r.sc[u].x * r.sc[u].y;
+    }
 }
 
+// Prefill GEMM, 17..64 tokens (kPrefillTokens): each wave owns 16 weight rows
+// and all four 16-token tiles, so every weight fragment read from HBM feeds
+// four MFMAs.  K is walked in 256-value steps (one Q4_K super-block, or eight
+// Q8_0 blocks); the 64 activation rows of a step (16 KB of codes plus the
+// per-block scale terms) are staged through a double-buffered LDS slot, the
+// next step's loads in flight while this one is consumed, so the LDS
+// footprint does not grow with K.  Per 32-block the four token tiles' MFMAs
+// issue back to back, then their outputs take the block term of
+// k_vgemm_q8_0 / k_vgemm_q4k with fused multiply-adds:
+//   Q4_K  acc += (s * d*sc) * dot - (d_min*mn) * (s * sum q)
+//   Q8_0  acc += (s * d_w) * dot
+// (the same terms as the reference's s * (d*sc*dot - dmin*mn*sum q), in
+// another rounding order).
 template <int FMT>
 __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
     __shared__ __align__(16) int8_t lx[2][64 * kPgStride];
-    __shared__ float2 lsc[2][64 * 8];
+    __shared__ __align__(16) float lsc[2][8 * 64];  // [block][token] activation scales
+    __shared__ __align__(16) float lsq[2][8 * 64];  // [block][token] scale * code sum
     const WDesc &W = a.W;
     const int K = W.cols, nst = K >> 8;  // 256-value steps
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -304,7 +326,7 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
     PgStage xr;
     wload(s0);
     pg_load(a, s0 * 256, xr);
-    pg_store(xr, lx[0], lsc[0]);
+    pg_store(xr, lx[0], lsc[0], lsq[0]);
     __syncthreads();
     for (int st = s0; st < s1; st++) {
         const int cur = (st - s0) & 1;
@@ -321,7 +343,6 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
             pg_load(a, (st + 1) * 256, xr);
         }
         const int8_t *bx = lx[cur];
-        const float2 *bs = lsc[cur];
         if (tile * 16 < W.rows) {
             float d = 0.f, dmin = 0.f;
             if constexpr (FMT == F_Q4K) {
@@ -350,22 +371,31 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
                 }
                 // Q4_K sub-block j: low nibbles pair with activation bytes 32j of
                 // the step for j < 4 (qs bytes 32jj..), high nibbles with 32j
+                v4i32_t dd[4];
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+                    dd[tt] = vg_mfma(*(const i64x1_t *)(bx + (tA + 16 * tt) * kPgStride + 32 * j + 8 * kg), wb);
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
-                    const int tx = tA + 16 * tt;
-                    const i64x1_t x = *(const i64x1_t *)(bx + tx * kPgStride + 32 * j + 8 * kg);
-                    const v4i32_t dd = vg_mfma(x, wb);
+                    const int t0 = 16 * tt + 4 * kg;  // tokens t0 .. t0+3 of this lane
+                    const v4f_t xs = *(const v4f_t *)&lsc[cur][j * 64 + t0];
+                    const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
+                    if constexpr (FMT == F_Q4K) {
+                        const v4f_t xq = *(const v4f_t *)&lsq[cur][j * 64 + t0];
+                        const float qv[4] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int t = 16 * tt + 4 * kg + i;
-                        const float2 xs = bs[t * 8 + j];
-                        if constexpr (FMT == F_Q4K) acc[tt][i] += xs.x * (dsc * (float)dd[i] - dmn * xs.y);
-                        else acc[tt][i] += (dsc * xs.x) * (float)dd[i];
+                        for (int i = 0; i < 4; i++) {
+                            const float a1 = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
+                            acc[tt][i] = __builtin_fmaf(-dmn, qv[i], a1);
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
                     }
                 }
             }
         }
-        if (st + 1 < s1) pg_store(xr, lx[cur ^ 1], lsc[cur ^ 1]);
+        if (st + 1 < s1) pg_store(xr, lx[cur ^ 1], lsc[cur ^ 1], lsq[cur ^ 1]);
         __syncthreads();
     }
     if (n < W.rows) {
