@@ -28,6 +28,11 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-ffp-contract=off"]
 
 
+# Per-source flags.  verify.hip: MFMA results in VGPRs (no accumulator-
+# register copies before the fp32 block terms of the GEMM epilogues).
+SOURCE_FLAGS = {"verify.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _run(cmd: list[str]) -> None:
     print("+", " ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
@@ -48,7 +53,7 @@ def build(verbose: bool = True) -> str:
     objs = []
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        jobs.append([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     for src in HOST_SOURCES:
         obj = os.path.join(BUILD, src.replace(".cpp", ".o"))

@@ -12,6 +12,7 @@ constexpr int kPrefillMaxKsplit = 32;
 
 typedef long long i64x1_t;
 typedef int v4i32_t __attribute__((ext_vector_type(4)));
+typedef float v4f32_t __attribute__((ext_vector_type(4)));
 
 struct VgArgs {
     WDesc W;          // weight planes (Q8_0: int8 quants + f16 scales; Q4_K: qs + 16-B headers)

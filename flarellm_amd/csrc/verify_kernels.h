@@ -282,7 +282,8 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls
 // footprint does not grow with K.  Per 32-block the four token tiles' MFMAs
 // issue back to back, then their outputs take the block term of
 // k_vgemm_q8_0 / k_vgemm_q4k with fused multiply-adds:
-//   Q4_K  acc += (s * d*sc) * dot - (d_min*mn) * (s * sum q)
+//   Q4_K  acc += (s * d*sc) * dot, then per step the min terms
+//         - sum_j (d_min*mn_j) * (s * sum q)_j as one K = 8 f32 MFMA per tile
 //   Q8_0  acc += (s * d_w) * dot
 // (the same terms as the reference's s * (d*sc*dot - dmin*mn*sum q), in
 // another rounding order).
@@ -353,18 +354,15 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 i64x1_t wb;
-                float dsc, dmn = 0.f;
+                float dsc;
                 if constexpr (FMT == F_Q4K) {
                     const int jj = j & 3;
                     const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
                     wb = j < 4 ? (w[jj] & m4) : ((w[jj] >> 4) & m4);
                     // unpack_q4k_scales (model.rs:8709-8719), flare packing
-                    const uint32_t sa = byte_of((uint32_t)h.y, jj), sbb = byte_of((uint32_t)h.z, jj),
-                                   scc = byte_of((uint32_t)h.w, jj);
+                    const uint32_t sa = byte_of((uint32_t)h.y, jj), scc = byte_of((uint32_t)h.w, jj);
                     const uint32_t sc = j < 4 ? (sa & 63) : ((sa >> 6) | ((scc & 0xF) << 2));
-                    const uint32_t mn = j < 4 ? (sbb & 63) : ((sbb >> 6) | ((scc >> 4) << 2));
                     dsc = d * (float)sc;
-                    dmn = dmin * (float)mn;
                 } else {
                     wb = w[j];
                     dsc = h2f(sc8[j]);
@@ -380,18 +378,24 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
                     const int t0 = 16 * tt + 4 * kg;  // tokens t0 .. t0+3 of this lane
                     const v4f_t xs = *(const v4f_t *)&lsc[cur][j * 64 + t0];
                     const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
-                    if constexpr (FMT == F_Q4K) {
-                        const v4f_t xq = *(const v4f_t *)&lsq[cur][j * 64 + t0];
-                        const float qv[4] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const float a1 = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
-                            acc[tt][i] = __builtin_fmaf(-dmn, qv[i], a1);
-                        }
-                    } else {
+                    for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
+                }
+            }
+            if constexpr (FMT == F_Q4K) {
+                // the min terms of the step's 8 sub-blocks, as a K = 8 f32 MFMA
+                // per token tile: A = s * sum q [token][sub-block], B = -d_min*mn
+                // [sub-block][row]; lane (row, kg) supplies sub-blocks kg, 4 + kg
+                const uint32_t sbb = byte_of((uint32_t)h.z, kg), scc = byte_of((uint32_t)h.w, kg);
+                const float nm0 = -(dmin * (float)(sbb & 63));
+                const float nm1 = -(dmin * (float)((sbb >> 6) | ((scc >> 4) << 2)));
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
-                    }
+                for (int tt = 0; tt < 4; tt++) {
+                    v4f32_t c = {acc[tt][0], acc[tt][1], acc[tt][2], acc[tt][3]};
+                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][kg * 64 + tA + 16 * tt], nm0, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][(4 + kg) * 64 + tA + 16 * tt], nm1, c, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[tt][i] = c[i];
                 }
             }
         }
