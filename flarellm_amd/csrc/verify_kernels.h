@@ -21,8 +21,8 @@ namespace fl {
 // Every load of a round goes out before the first LDS store, so a round
 // costs one L2 round trip.
 // T8: (scale, sum) pairs block-major, 8 tokens per block ([b][8]); else
-// token-major ([t][nb]).
-template <int FMT, bool T8 = false>
+// token-major ([t][nb]).  SQ: the second member is scale * sum instead.
+template <int FMT, bool T8 = false, bool SQ = false>
 __device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t *lx, float2 *lsc, int xs = 0) {
     if (!xs) xs = kn;  // LDS row stride of the activations
     constexpr int U = 8;
@@ -58,7 +58,7 @@ __device__ __forceinline__ void vg_stage(const VgArgs &a, int k0, int kn, int8_t
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int i = base + u * blockDim.x;
-            if (i < ns) lsc[T8 ? (i % nb) * 8 + i / nb : i] = make_float2(sv[u], (float)mv[u]);
+            if (i < ns) lsc[T8 ? (i % nb) * 8 + i / nb : i] = make_float2(sv[u], SQ ? sv[u] * (float)mv[u] : (float)mv[u]);
         }
     }
     __syncthreads();
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * tt + 4 * kg + i;
-                if (t < a.M) acc[tt][i] += (wsc * lsc[t * nbc + bl].x) * (float)d[i];
+                if (t < a.M) acc[tt][i] = __builtin_fmaf(wsc * lsc[t * nbc + bl].x, (float)d[i], acc[tt][i]);
             }
         }
     }
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_08(VgArgs a) {
                 const float4 l0 = ls[0], l1 = ls[1];
                 const float xs[4] = {l0.x, l0.z, l1.x, l1.z};
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[e] += (wsc * xs[e]) * (float)dd[p][e];
+                for (int e = 0; e < 4; e++) acc[e] = __builtin_fmaf(wsc * xs[e], (float)dd[p][e], acc[e]);
             }
         }
     }
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
 #pragma unroll
         for (int u = 0; u < PD; u++) load(u, min(s0 + u, s1 - 1));
     }
-    vg_stage<F_Q4K, true>(a, s0 * 256, kn, lx, lsc, xst);
+    vg_stage<F_Q4K, true, true>(a, s0 * 256, kn, lx, lsc, xst);
     if (!live) return;
     const int sh = 4 * hi;
     const i64x1_t m4 = 0x0F0F0F0F0F0F0F0FLL;
@@ -591,7 +591,11 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
             const float4 l0 = ls[0], l1 = ls[1];
             const float xs[4] = {l0.x, l0.z, l1.x, l1.z}, xm[4] = {l0.y, l0.w, l1.y, l1.w};
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] += xs[e] * (dsc * (float)dd[p][e] - dmn * xm[e]);
+            for (int e = 0; e < 4; e++) {
+                // s * (d*sc*dot - dmin*mn*sum q) as (s * d*sc) * dot - (dmin*mn) * (s * sum q)
+                const float a1 = __builtin_fmaf(xs[e] * dsc, (float)dd[p][e], acc[e]);
+                acc[e] = __builtin_fmaf(-dmn, xm[e], a1);
+            }
         }
     }
     // lanes kg and kg+2 hold sub-blocks 0-3 and 4-7 of the same outputs
