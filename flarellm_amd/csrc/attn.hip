@@ -64,12 +64,15 @@ hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a) {
     const int npairs = a.nq / 2;
     if (a.nq < 2 || a.nq % 2 || !a.v_tblk || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32 || a.chmin < 1)
         return hipErrorInvalidValue;
-    const int NW = npairs <= 4 ? 4 : 8;
-    const dim3 grid(a.nsplit, a.nkv, (npairs + NW - 1) / NW);
+    // 8 waves with one query pair each (two pairs per wave, sharing each LDS
+    // fragment read, measured slower at the Llama-3-8B prefill shape: C3
+    // 4096-token prefill 452 against 515 ms)
+    const int NW = npairs <= 4 ? 4 : 8, RP = 1;
+    const dim3 grid(a.nsplit, a.nkv, (npairs + NW * RP - 1) / (NW * RP));
 #define C(DD, GG)                                                                                     \
     if (D == DD && G == GG) {                                                                         \
-        if (NW == 4) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4>), grid, dim3(256), 0, st, a);          \
-        else hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8>), grid, dim3(512), 0, st, a);                  \
+        if (NW == 4) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4, RP>), grid, dim3(256), 0, st, a);      \
+        else hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8, RP>), grid, dim3(512), 0, st, a);               \
         return hipGetLastError();                                                                     \
     }
     C(64, 1) C(64, 2) C(64, 4) C(128, 1) C(128, 2) C(128, 4)

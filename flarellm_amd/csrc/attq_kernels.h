@@ -29,49 +29,56 @@ namespace fl {
 constexpr int kAttqKPad = 8;  // halves of padding per staged K row
 constexpr int kAttqVPad = 8;  // per staged V channel row
 
-template <int D, int NW>
+template <int D, int NPW>  // NPW = query pairs per workgroup
 struct AttqLds {
     static constexpr int KS = D + kAttqKPad, VS = 32 + kAttqVPad;
     static constexpr int KH = 32 * KS, VH = D * VS;  // halves per staged block
     static constexpr size_t LOOP = (size_t)2 * (KH + VH) * 2;  // double-buffered K and V
-    static constexpr size_t SP = (size_t)NW * 8 * 32 * 4;       // p of the current block per wave
-    static constexpr size_t RED = (size_t)NW * 8 * D * 4;       // per-wave outputs (after the loop)
-    static constexpr size_t WT = (size_t)NW * 8 * kAttmMaxSplit * 4;  // merge weights
+    static constexpr size_t SP = (size_t)NPW * 8 * 32 * 4;      // p of the current block per pair
+    static constexpr size_t RED = (size_t)NPW * 8 * D * 4;      // per-pair outputs (after the loop)
+    static constexpr size_t WT = (size_t)NPW * 8 * kAttmMaxSplit * 4;  // merge weights
     static constexpr size_t BYTES = (LOOP + SP > RED + WT ? LOOP + SP : RED + WT);
 };
 
-// G2 = rows of a query pair: the model's G heads of each of its 2 queries
-template <int D, int G2, int NW>
+// G2 = rows of a query pair: the model's G heads of each of its 2 queries.
+// NW waves, RP query pairs per wave (each staged K / V fragment read from LDS
+// once per wave feeds the RP pairs' MFMAs).
+template <int D, int G2, int NW, int RP>
 __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
-    constexpr int DT = D / 32, NT = D / 16, NTH = NW * 64, GH = G2 / 2;
-    using L = AttqLds<D, NW>;
+    constexpr int DT = D / 32, NT = D / 16, NTH = NW * 64, GH = G2 / 2, NPW = NW * RP;
+    using L = AttqLds<D, NPW>;
     constexpr int KS = L::KS, VS = L::VS;
     static_assert(G2 <= 8 && G2 % 2 == 0, "2G rows of a query pair (hi / lo) fill at most one MFMA tile");
     __shared__ __align__(16) char smem[L::BYTES];
     __shared__ int is_last;
     _Float16 *lk = (_Float16 *)smem;             // [2][32][KS]
     _Float16 *lv = lk + 2 * L::KH;               // [2][D][VS]
-    float *sp = (float *)(smem + L::LOOP);       // [NW][8][32]
-    float *red = (float *)smem;                  // [NW][8][D], after the loop
-    float *wt = (float *)(smem + L::RED);        // [NW][8][kAttmMaxSplit]
+    float *sp = (float *)(smem + L::LOOP);       // [NPW][8][32]
+    float *red = (float *)smem;                  // [NPW][8][D], after the loop
+    float *wt = (float *)(smem + L::RED);        // [NPW][8][kAttmMaxSplit]
 
     const int kvh = blockIdx.y, s = blockIdx.x, zg = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
-    const int npairs = a.nq / 2, p = zg * NW + wave;
-    const bool live = p < npairs;  // wave-uniform
-    const int q0 = 2 * min(p, npairs - 1), q1 = q0 + 1;
-    const int glast = 2 * min(npairs, (zg + 1) * NW) - 1;  // last query of the group
+    const int npairs = a.nq / 2, pw0 = zg * NPW + wave * RP;  // the wave's first pair
+    const bool live = pw0 < npairs;                           // wave-uniform
+    const int glast = 2 * min(npairs, (zg + 1) * NPW) - 1;    // last query of the group
+    int q0[RP];
+#pragma unroll
+    for (int i = 0; i < RP; i++) q0[i] = 2 * min(pw0 + i, npairs - 1);
 
     // query rows first (independent of the position)
-    v4f_t qv[DT][2];
+    v4f_t qv[RP][DT][2];
     {
         const int g = min(r >> 1, G2 - 1);
-        const size_t qo = (size_t)(g >= GH ? q1 : q0) * a.qstride + (size_t)(kvh * GH + g % GH) * D;
-        const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            qv[dt][0] = qp[8 * dt];
-            qv[dt][1] = qp[8 * dt + 1];
+        for (int i = 0; i < RP; i++) {
+            const size_t qo = (size_t)(q0[i] + (g >= GH ? 1 : 0)) * a.qstride + (size_t)(kvh * GH + g % GH) * D;
+            const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                qv[i][dt][0] = qp[8 * dt];
+                qv[i][dt][1] = qp[8 * dt + 1];
+            }
         }
     }
     const int base = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -83,10 +90,12 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
     const int t1 = min(Tg, t0 + CH), nact = (Tg + CH - 1) / CH;
     const int nblk = (t1 - t0 + kAttmBlock - 1) / kAttmBlock;
     // rows of lane group kg: head rows 2kg + e; their query's last slot
-    int lim[2];
+    int lim[RP][2];
 #pragma unroll
-    for (int e = 0; e < 2; e++) lim[e] = base + ((2 * kg + e) >= GH ? q1 : q0);
-    const int wlim = base + q1;  // last slot any row of this wave sees
+    for (int i = 0; i < RP; i++)
+#pragma unroll
+        for (int e = 0; e < 2; e++) lim[i][e] = base + q0[i] + ((2 * kg + e) >= GH ? 1 : 0);
+    const int wlim = base + 2 * min(pw0 + RP - 1, npairs - 1) + 1;  // last slot any row of the wave sees
 
     // block staging: K rows tb..tb+31 (contiguous [slot][D]) and the transposed
     // V block ([D][32], contiguous), 16 B per thread and piece
@@ -119,29 +128,32 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
     gload(kr[0], vr[0], t0);
     if (nblk > 1) gload(kr[1], vr[1], t0 + kAttmBlock);
 
-    // A operand of S: row m = 2g + (hi / lo) of head row g (rows >= 2 G2 zero)
-    v8h_t aq[DT];
-    {
-        const int m = r;
+    // A operands of S: row m = 2g + (hi / lo) of head row g (rows >= 2 G2 zero)
+    v8h_t aq[RP][DT];
+#pragma unroll
+    for (int i = 0; i < RP; i++)
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            const v4f_t x0 = qv[dt][0], x1 = qv[dt][1];
+            const v4f_t x0 = qv[i][dt][0], x1 = qv[i][dt][1];
             float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            if ((m >> 1) >= G2) {
+            if ((r >> 1) >= G2) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) x[i] = 0.0f;
+                for (int j = 0; j < 8; j++) x[j] = 0.0f;
             }
             v8h_t hi, lo;
             split8(x, hi, lo);
-            aq[dt] = (m & 1) ? lo : hi;
+            aq[i][dt] = (r & 1) ? lo : hi;
         }
-    }
     const float scale = 1.0f / sqrtf((float)D);
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
-    v4f32_t oacc[NT];
+    float m_run[RP][2], l_run[RP][2];
+    v4f32_t oacc[RP][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) oacc[nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
-    float *spw = sp + wave * 8 * 32;
+    for (int i = 0; i < RP; i++) {
+        m_run[i][0] = m_run[i][1] = -INFINITY;
+        l_run[i][0] = l_run[i][1] = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) oacc[i][nt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     lstore(kr[0], vr[0], 0);
     if (nblk > 2) gload(kr[0], vr[0], t0 + 2 * kAttmBlock);
@@ -152,53 +164,70 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
         const int cur = bi & 1, tb = t0 + bi * kAttmBlock;
         if (live && tb <= wlim) {  // wave-uniform: some row sees the block
             const _Float16 *bk = lk + cur * L::KH, *bv = lv + cur * L::VH;
-            float sc[2][2];  // [half][head row parity] for slot tb + 16h + r
+            v4f32_t acc[RP][2];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                v4f32_t acc = v4f32_t{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < RP; i++) acc[i][0] = acc[i][1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++)
-                    acc = mfma16(aq[dt], *(const v8h_t *)(bk + (16 * h + r) * KS + 32 * dt + 8 * kg), acc);
-                const int t = tb + 16 * h + r;
-                sc[h][0] = t < t1 && t <= lim[0] ? (acc[0] + acc[1]) * scale : -INFINITY;
-                sc[h][1] = t < t1 && t <= lim[1] ? (acc[2] + acc[3]) * scale : -INFINITY;
-            }
-            float alpha[2];
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const float bm = row_max<16>(fmaxf(sc[0][e], sc[1][e]));
-                const float mn = fmaxf(m_run[e], bm);
-                // a row that has seen nothing yet keeps m = -inf (and p = 0)
-                alpha[e] = (m_run[e] == -INFINITY) ? 0.0f : __expf(m_run[e] - mn);
-                const float p0 = sc[0][e] == -INFINITY ? 0.0f : __expf(sc[0][e] - mn);
-                const float p1 = sc[1][e] == -INFINITY ? 0.0f : __expf(sc[1][e] - mn);
-                l_run[e] = l_run[e] * alpha[e] + row_sum<16>(p0 + p1);
-                m_run[e] = mn;
-                const int g = 2 * kg + e;
-                if (g < G2) {
-                    spw[g * 32 + r] = p0;
-                    spw[g * 32 + 16 + r] = p1;
+                for (int dt = 0; dt < DT; dt++) {
+                    const v8h_t kb = *(const v8h_t *)(bk + (16 * h + r) * KS + 32 * dt + 8 * kg);
+#pragma unroll
+                    for (int i = 0; i < RP; i++) acc[i][h] = mfma16(aq[i][dt], kb, acc[i][h]);
+                }
+            v8h_t ap[RP];
+#pragma unroll
+            for (int i = 0; i < RP; i++) {
+                float *spw = sp + (wave * RP + i) * 8 * 32;
+                float sc[2][2];  // [half][head row parity] for slot tb + 16h + r
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int t = tb + 16 * h + r;
+                    sc[h][0] = t < t1 && t <= lim[i][0] ? (acc[i][h][0] + acc[i][h][1]) * scale : -INFINITY;
+                    sc[h][1] = t < t1 && t <= lim[i][1] ? (acc[i][h][2] + acc[i][h][3]) * scale : -INFINITY;
+                }
+                float alpha[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const float bm = row_max<16>(fmaxf(sc[0][e], sc[1][e]));
+                    const float mn = fmaxf(m_run[i][e], bm);
+                    // a row that has seen nothing yet keeps m = -inf (and p = 0)
+                    alpha[e] = (m_run[i][e] == -INFINITY) ? 0.0f : __expf(m_run[i][e] - mn);
+                    const float p0 = sc[0][e] == -INFINITY ? 0.0f : __expf(sc[0][e] - mn);
+                    const float p1 = sc[1][e] == -INFINITY ? 0.0f : __expf(sc[1][e] - mn);
+                    l_run[i][e] = l_run[i][e] * alpha[e] + row_sum<16>(p0 + p1);
+                    m_run[i][e] = mn;
+                    const int g = 2 * kg + e;
+                    if (g < G2) {
+                        spw[g * 32 + r] = p0;
+                        spw[g * 32 + 16 + r] = p1;
+                    }
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    oacc[i][nt][0] *= alpha[0];
+                    oacc[i][nt][1] *= alpha[0];
+                    oacc[i][nt][2] *= alpha[1];
+                    oacc[i][nt][3] *= alpha[1];
                 }
             }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                oacc[nt][0] *= alpha[0];
-                oacc[nt][1] *= alpha[0];
-                oacc[nt][2] *= alpha[1];
-                oacc[nt][3] *= alpha[1];
-            }
-            {
-                const int m = r, g = m >> 1;
+            for (int i = 0; i < RP; i++) {
+                const float *spw = sp + (wave * RP + i) * 8 * 32;
+                const int g = r >> 1;
                 float pv[8];
 #pragma unroll
-                for (int i = 0; i < 8; i++) pv[i] = g < G2 ? spw[g * 32 + 8 * kg + i] : 0.0f;
+                for (int j = 0; j < 8; j++) pv[j] = g < G2 ? spw[g * 32 + 8 * kg + j] : 0.0f;
                 v8h_t hi, lo;
                 split8(pv, hi, lo);
-                const v8h_t ap = (m & 1) ? lo : hi;
+                ap[i] = (r & 1) ? lo : hi;
+            }
 #pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    oacc[nt] = mfma16(ap, *(const v8h_t *)(bv + (16 * nt + r) * VS + 8 * kg), oacc[nt]);
+            for (int nt = 0; nt < NT; nt++) {
+                const v8h_t vb = *(const v8h_t *)(bv + (16 * nt + r) * VS + 8 * kg);
+#pragma unroll
+                for (int i = 0; i < RP; i++) oacc[i][nt] = mfma16(ap[i], vb, oacc[i][nt]);
             }
             __builtin_amdgcn_wave_barrier();
         }
@@ -213,44 +242,45 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
         if (bi + 1 < nblk) block(bi + 1, kr[0], vr[0]);
     }
 
-    // per-wave result: head row g = 2kg + e, channel 16nt + r
+    // per-pair result: head row g = 2kg + e, channel 16nt + r
     // (rows 4kg + 2e / + 1 of oacc: high / residual parts of P)
-    float *mypart = nullptr;
     constexpr int P = G2 * (D + 2);
-    if (nact > 1)
-        mypart = a.part + ((((size_t)zg * a.nkv + kvh) * a.nsplit + s) * NW + wave) * P;
-    float *rw = red + wave * 8 * D;
-    if (live) {
+    float *gpart = a.part + ((size_t)zg * a.nkv + kvh) * a.nsplit * NPW * P;  // this (group, kv head)
+#pragma unroll
+    for (int i = 0; i < RP; i++) {
+        const int slot = wave * RP + i;
+        if (pw0 + i >= npairs) continue;  // wave-uniform
+        float *mypart = gpart + ((size_t)s * NPW + slot) * P;
+        float *rw = red + slot * 8 * D;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int g = 2 * kg + e;
             if (g < G2) {
-                const float il = nact == 1 ? 1.0f / l_run[e] : 1.0f;
+                const float il = nact == 1 ? 1.0f / l_run[i][e] : 1.0f;
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
-                    const float o = oacc[nt][2 * e] + oacc[nt][2 * e + 1];
+                    const float o = oacc[i][nt][2 * e] + oacc[i][nt][2 * e + 1];
                     if (nact == 1) rw[g * D + 16 * nt + r] = o * il;
                     else st_agent(mypart + g * D + 16 * nt + r, o);
                 }
                 if (nact > 1 && r == 0) {
-                    st_agent(mypart + G2 * D + 2 * g, m_run[e]);
-                    st_agent(mypart + G2 * D + 2 * g + 1, l_run[e]);
+                    st_agent(mypart + G2 * D + 2 * g, m_run[i][e]);
+                    st_agent(mypart + G2 * D + 2 * g + 1, l_run[i][e]);
                 }
             }
         }
     }
     if (nact > 1) {
         if (!split_arrive_last<true>(&a.counters[(size_t)zg * a.nkv + kvh], nact, &is_last)) return;
-        // last workgroup: merge weights per (wave, head row), then each
+        // last workgroup: merge weights per (pair, head row), then each
         // output over the nact partials (all loads of an output independent)
-        const float *pb = a.part + (((size_t)zg * a.nkv + kvh) * a.nsplit) * NW * P;
-        for (int i = tid; i < NW * G2; i += NTH) {
+        for (int i = tid; i < NPW * G2; i += NTH) {
             const int w = i / G2, g = i % G2;
             float M = -INFINITY;
-            for (int j = 0; j < nact; j++) M = fmaxf(M, ld_agent(pb + ((size_t)j * NW + w) * P + G2 * D + 2 * g));
+            for (int j = 0; j < nact; j++) M = fmaxf(M, ld_agent(gpart + ((size_t)j * NPW + w) * P + G2 * D + 2 * g));
             float Ls = 0.0f;
             for (int j = 0; j < nact; j++) {
-                const float *pj = pb + ((size_t)j * NW + w) * P + G2 * D + 2 * g;
+                const float *pj = gpart + ((size_t)j * NPW + w) * P + G2 * D + 2 * g;
                 const float mj = ld_agent(pj);
                 const float wj = mj == -INFINITY ? 0.0f : __expf(mj - M);
                 Ls += ld_agent(pj + 1) * wj;
@@ -260,31 +290,32 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
             for (int j = 0; j < nact; j++) wt[(w * 8 + g) * kAttmMaxSplit + j] *= il;
         }
         __syncthreads();
-        for (int i = tid; i < NW * G2 * D; i += NTH) {
+        for (int i = tid; i < NPW * G2 * D; i += NTH) {
             const int w = i / (G2 * D), gd = i % (G2 * D), g = gd / D;
-            if (zg * NW + w >= npairs) continue;
+            if (zg * NPW + w >= npairs) continue;
             const float *wr = wt + (w * 8 + g) * kAttmMaxSplit;
             float O = 0.0f;
             int j = 0;
             for (; j + 8 <= nact; j += 8) {
                 float ov[8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) ov[k] = ld_agent(pb + ((size_t)(j + k) * NW + w) * P + gd);
+                for (int k = 0; k < 8; k++) ov[k] = ld_agent(gpart + ((size_t)(j + k) * NPW + w) * P + gd);
 #pragma unroll
                 for (int k = 0; k < 8; k++) O += ov[k] * wr[j + k];
             }
-            for (; j < nact; j++) O += ld_agent(pb + ((size_t)j * NW + w) * P + gd) * wr[j];
+            for (; j < nact; j++) O += ld_agent(gpart + ((size_t)j * NPW + w) * P + gd) * wr[j];
             red[w * 8 * D + gd] = O;
         }
         __syncthreads();
     } else {
         __syncthreads();
     }
-    // outputs of head row g of wave w: query (g >= GH ? q1 : q0), model head
-    // kvh * GH + g % GH; the f32 rows and / or their Q8_0 blocks (32 lanes each)
-    for (int b = tid >> 5; b < NW * G2 * D / 32; b += NTH / 32) {
+    // outputs of head row g of pair slot w: query 2 (group base + w) + (g >= GH),
+    // model head kvh * GH + g % GH; the f32 rows and / or their Q8_0 blocks
+    // (32 lanes each)
+    for (int b = tid >> 5; b < NPW * G2 * D / 32; b += NTH / 32) {
         const int w = b / (G2 * D / 32), gd = (b % (G2 * D / 32)) * 32, g = gd / D, c = gd % D;
-        const int pw = zg * NW + w;
+        const int pw = zg * NPW + w;
         if (pw >= npairs) continue;  // 32-lane groups: uniform
         const int q = 2 * pw + (g >= GH ? 1 : 0);
         const size_t e0 = (size_t)q * a.ostride + (size_t)(kvh * GH + g % GH) * D + c;

@@ -1984,7 +1984,8 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         if (!no_attq && a.qpair && M > kVerifyMaxTokens && ctx->kv_format == FL_KV_F16 && (D == 64 || D == 128)) {
             // splits: about one workgroup per CU over (kv heads x pair groups)
             static const int attq_ns = getenv("FLARE_ATTQ_NSPLIT") ? atoi(getenv("FLARE_ATTQ_NSPLIT")) : 0;
-            const int groups = (M / 2 + (M / 2 <= 4 ? 4 : 8) - 1) / (M / 2 <= 4 ? 4 : 8);
+            const int per_wg = M / 2 <= 4 ? 4 : 8;  // pairs per workgroup (launch_attq)
+            const int groups = (M / 2 + per_wg - 1) / per_wg;
             int ns = attq_ns > 0 ? attq_ns : ctx->ncu / (c.num_kv_heads * groups);
             a.nsplit = std::max(1, std::min(kAttmMaxSplit, ns));
             a.nq = M;
