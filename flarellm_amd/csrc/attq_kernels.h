@@ -272,39 +272,71 @@ __global__ __launch_bounds__(NW * 64) void k_attq(AttnArgs a) {
     }
     if (nact > 1) {
         if (!split_arrive_last<true>(&a.counters[(size_t)zg * a.nkv + kvh], nact, &is_last)) return;
-        // last workgroup: merge weights per (pair, head row), then each
-        // output over the nact partials (all loads of an output independent)
+        // last workgroup: merge weights per (pair, head row) from the (m, l)
+        // of every split (loads in batches of 8 splits, all in flight), then
+        // each thread's outputs in chunks of 8, all loads of a batch of 8
+        // splits in flight (a handful of round trips in all, not one per output)
+        float *mw = wt;  // [NPW * 8][kAttmMaxSplit]: m, then the weights
+        float *lw = red; // [NPW * 8][kAttmMaxSplit]: l (red is rewritten after)
         for (int i = tid; i < NPW * G2; i += NTH) {
             const int w = i / G2, g = i % G2;
+            for (int j0 = 0; j0 < nact; j0 += 8) {
+                float mv[8], lv[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float *pj = gpart + ((size_t)min(j0 + k, nact - 1) * NPW + w) * P + G2 * D + 2 * g;
+                    mv[k] = ld_agent(pj);
+                    lv[k] = ld_agent(pj + 1);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (j0 + k < nact) {
+                        mw[(w * 8 + g) * kAttmMaxSplit + j0 + k] = mv[k];
+                        lw[(w * 8 + g) * kAttmMaxSplit + j0 + k] = lv[k];
+                    }
+            }
             float M = -INFINITY;
-            for (int j = 0; j < nact; j++) M = fmaxf(M, ld_agent(gpart + ((size_t)j * NPW + w) * P + G2 * D + 2 * g));
+            for (int j = 0; j < nact; j++) M = fmaxf(M, mw[(w * 8 + g) * kAttmMaxSplit + j]);
             float Ls = 0.0f;
             for (int j = 0; j < nact; j++) {
-                const float *pj = gpart + ((size_t)j * NPW + w) * P + G2 * D + 2 * g;
-                const float mj = ld_agent(pj);
+                const float mj = mw[(w * 8 + g) * kAttmMaxSplit + j];
                 const float wj = mj == -INFINITY ? 0.0f : __expf(mj - M);
-                Ls += ld_agent(pj + 1) * wj;
-                wt[(w * 8 + g) * kAttmMaxSplit + j] = wj;
+                Ls += lw[(w * 8 + g) * kAttmMaxSplit + j] * wj;
+                mw[(w * 8 + g) * kAttmMaxSplit + j] = wj;
             }
             const float il = 1.0f / Ls;
-            for (int j = 0; j < nact; j++) wt[(w * 8 + g) * kAttmMaxSplit + j] *= il;
+            for (int j = 0; j < nact; j++) mw[(w * 8 + g) * kAttmMaxSplit + j] *= il;
         }
         __syncthreads();
-        for (int i = tid; i < NPW * G2 * D; i += NTH) {
-            const int w = i / (G2 * D), gd = i % (G2 * D), g = gd / D;
-            if (zg * NPW + w >= npairs) continue;
-            const float *wr = wt + (w * 8 + g) * kAttmMaxSplit;
-            float O = 0.0f;
-            int j = 0;
-            for (; j + 8 <= nact; j += 8) {
-                float ov[8];
+        constexpr int NO = NPW * G2 * D, CK = NO / NTH < 8 ? NO / NTH : 8;  // outputs; per chunk and thread
+        static_assert(NO % (NTH * CK) == 0, "whole chunks of outputs per thread");
+        for (int c0 = 0; c0 < NO; c0 += NTH * CK) {
+            float O[CK];
 #pragma unroll
-                for (int k = 0; k < 8; k++) ov[k] = ld_agent(gpart + ((size_t)(j + k) * NPW + w) * P + gd);
+            for (int k = 0; k < CK; k++) O[k] = 0.0f;
+            for (int j0 = 0; j0 < nact; j0 += 8) {
+                float ov[CK][8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) O += ov[k] * wr[j + k];
+                for (int k = 0; k < CK; k++) {
+                    const int i = c0 + k * NTH + tid, w = i / (G2 * D), gd = i % (G2 * D);
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        ov[k][u] = ld_agent(gpart + ((size_t)min(j0 + u, nact - 1) * NPW + w) * P + gd);
+                }
+#pragma unroll
+                for (int k = 0; k < CK; k++) {
+                    const int i = c0 + k * NTH + tid, w = i / (G2 * D), g = (i % (G2 * D)) / D;
+                    const float *wr = wt + (w * 8 + g) * kAttmMaxSplit;
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        if (j0 + u < nact) O[k] += ov[k][u] * wr[j0 + u];
+                }
             }
-            for (; j < nact; j++) O += ld_agent(gpart + ((size_t)j * NPW + w) * P + gd) * wr[j];
-            red[w * 8 * D + gd] = O;
+#pragma unroll
+            for (int k = 0; k < CK; k++) {
+                const int i = c0 + k * NTH + tid, w = i / (G2 * D), gd = i % (G2 * D);
+                if (zg * NPW + w < npairs) red[w * 8 * D + gd] = O[k];
+            }
         }
         __syncthreads();
     } else {

@@ -1981,7 +1981,9 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         static const int attq_chmin = getenv("FLARE_ATTQ_CHMIN") ? std::max(32, atoi(getenv("FLARE_ATTQ_CHMIN"))) : 64;
         // (prefill passes; the verify batches of up to 8 tokens keep k_attm's
         // query pairs, which measured faster at 8 tokens)
-        if (!no_attq && a.qpair && M > kVerifyMaxTokens && ctx->kv_format == FL_KV_F16 && (D == 64 || D == 128)) {
+        static const bool attq_verify = getenv("FLARE_ATTQ_VERIFY") != nullptr;  // measurement switch
+        if (!no_attq && a.qpair && (M > kVerifyMaxTokens || attq_verify) && ctx->kv_format == FL_KV_F16 &&
+            (D == 64 || D == 128)) {
             // splits: about one workgroup per CU over (kv heads x pair groups)
             static const int attq_ns = getenv("FLARE_ATTQ_NSPLIT") ? atoi(getenv("FLARE_ATTQ_NSPLIT")) : 0;
             const int per_wg = M / 2 <= 4 ? 4 : 8;  // pairs per workgroup (launch_attq)
