@@ -11,7 +11,14 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     const int nt = (a.M + 15) / 16;  // token tiles of the M > 8 kernels
     if (a.M > kVerifyMaxTokens && a.W.cols % 256 == 0 && !a.post) {
         // prefill batches: activations staged per 256-value step (chunk = steps)
-        if (fmt == F_Q4K) hipLaunchKernelGGL(k_pgemm<F_Q4K>, grid, dim3(256), 0, st, a);
+        // Q4_K: the f16-MFMA form (FLARE_PGEMM_I8: the int8 one, a measurement switch)
+        static const bool i8 = getenv("FLARE_PGEMM_I8") != nullptr;
+        if (fmt == F_Q4K && !i8) {
+            const dim3 gh((tiles + 7) / 8, a.ksplit);
+            static const bool db = getenv("FLARE_PGEMM_DB") != nullptr;  // measurement switch
+            if (db) hipLaunchKernelGGL((k_pgemm_h<8, 2>), gh, dim3(512), 0, st, a);
+            else hipLaunchKernelGGL((k_pgemm_h<8, 1>), gh, dim3(512), 0, st, a);
+        } else if (fmt == F_Q4K) hipLaunchKernelGGL(k_pgemm<F_Q4K>, grid, dim3(256), 0, st, a);
         else if (fmt == F_Q8_0) hipLaunchKernelGGL(k_pgemm<F_Q8_0>, grid, dim3(256), 0, st, a);
         else return hipErrorNotSupported;
         return hipGetLastError();

@@ -13,6 +13,7 @@
 #pragma once
 
 #include "verify_args.h"
+#include "attm_kernels.h"  // split8, mfma16 (f16 MFMA helpers)
 
 namespace fl {
 
@@ -409,6 +410,207 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * tt + 4 * kg + i;
                 if (t < a.M) a.part[((size_t)blockIdx.y * a.M + t) * W.rows + n] = acc[tt][i];
+            }
+    }
+}
+
+// Prefill GEMM for Q4_K weights on f16 MFMA (v_mfma_f32_16x16x32_f16), 17..64
+// tokens.  The int8 form above pays fp32 block terms per output and 32-block;
+// here the MFMA applies them:
+//  * B = sc * q of the lane's row: a 4-bit code times its 6-bit sub-block
+//    scale is an integer below 1024, exact in f16 (nibble -> 1024 + q by a
+//    byte permute under 0x64, then one packed f16 fma: (1024 + q) * sc -
+//    1024 * sc, exact);
+//  * A = the token's dequantized Q8 activation s * q in f16 high part +
+//    f16 residual (~22 bits), staged once per workgroup and step in LDS;
+//  * so one super-block's MFMAs accumulate sum_j s_j * sc_j * dot_j in fp32
+//    and the step ends with acc += d * C - d_min * Cmin, where Cmin =
+//    sum_j mn_j * (s * sum q)_j is a K = 8 f32 MFMA as in k_pgemm.
+// Each wave owns 16 weight rows and the four 16-token tiles (NW waves: NW x
+// 16 rows per workgroup share the staged activations); the next step's
+// activation codes and weights are in flight while the current one is consumed.
+constexpr int kPhStride = 256 + 8;  // halves per staged activation row
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// 8 nibbles (low or high half of the bytes of w) of a row times the
+// sub-block scale, as 8 exact binary16 values
+__device__ __forceinline__ h8_t q4_scaled_h8(const i64x1_t w, bool high, h2_t sc2, h2_t bias2) {
+    const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)((uint64_t)w >> 32);
+    const uint32_t n0 = (high ? w0 >> 4 : w0) & 0x0F0F0F0Fu, n1 = (high ? w1 >> 4 : w1) & 0x0F0F0F0Fu;
+    constexpr uint32_t m = 0x64646464u;
+    uint32_t d[4];
+    d[0] = __builtin_amdgcn_perm(m, n0, 0x04010400u);  // bytes: n0.b0, 0x64, n0.b1, 0x64
+    d[1] = __builtin_amdgcn_perm(m, n0, 0x04030402u);
+    d[2] = __builtin_amdgcn_perm(m, n1, 0x04010400u);
+    d[3] = __builtin_amdgcn_perm(m, n1, 0x04030402u);
+    h8_t r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        h2_t v;
+        __builtin_memcpy(&v, &d[k], 4);
+        v = __builtin_elementwise_fma(v, sc2, bias2);  // (1024 + q) * sc - 1024 * sc = q * sc, one rounding: exact
+        r[2 * k] = v[0];
+        r[2 * k + 1] = v[1];
+    }
+    return r;
+}
+
+// NB: activation buffers in LDS (2: the next step is staged while this one is
+// consumed, one barrier per step; 1: two barriers per step, half the LDS, so
+// two workgroups fit a CU)
+template <int NW, int NB>
+__global__ __launch_bounds__(NW * 64) void k_pgemm_h(VgArgs a) {
+    constexpr int NTH = NW * 64, NPC = 1024 / NTH;  // 16-code pieces per thread and step
+    __shared__ __align__(16) _Float16 lxh[NB][64 * kPhStride];  // high parts [token][k]
+    __shared__ __align__(16) _Float16 lxl[NB][64 * kPhStride];  // residuals
+    __shared__ __align__(16) float lsq[NB][8 * 64];             // [block][token] s * sum q
+    const WDesc &W = a.W;
+    const int K = W.cols, nst = K >> 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
+    const int s0 = blockIdx.y * a.chunk, s1 = min(nst, s0 + a.chunk);
+    if (s0 >= s1) return;
+    const int tile = blockIdx.x * NW + wave;
+    const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
+    const int row = min(n, W.rows - 1);
+    const bool live = tile * 16 < W.rows;  // wave-uniform
+    // activation staging: pieces of 16 codes (token i / 16, bytes 16 (i % 16))
+    v4i_t xc[NPC];
+    float xsc[NPC];
+    float usq = 0.0f;  // (token t / 8, block t % 8): s * sum q (t < 512)
+    auto xload = [&](int st) {
+        const int k0 = st * 256;
+#pragma unroll
+        for (int u = 0; u < NPC; u++) {
+            const int i = t + NTH * u, tok = min(i >> 4, a.M - 1);
+            xc[u] = *(const v4i_t *)(a.xq + (size_t)tok * K + k0 + 16 * (i & 15));
+            // token rows >= M stay zero in the MFMA: their scale is taken as 0
+            xsc[u] = (i >> 4) < a.M ? a.xs[(size_t)tok * (K >> 5) + (k0 >> 5) + ((i & 15) >> 1)] : 0.0f;
+        }
+        if (t < 512) {
+            const int tok = min(t >> 3, a.M - 1);
+            const size_t o = (size_t)tok * (K >> 5) + (k0 >> 5) + (t & 7);
+            usq = a.xs[o] * (float)a.xsum[o];
+        }
+    };
+    auto xstore = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < NPC; u++) {
+            const int i = t + NTH * u, tok = i >> 4;
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t wd = (uint32_t)xc[u][k];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[4 * k + e] = (float)(int8_t)(wd >> (8 * e));
+            }
+            h8_t hi[2], lo[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float x[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) x[k] = v[8 * h + k] * xsc[u];
+                v8h_t a8, b8;
+                split8(x, a8, b8);
+                hi[h] = a8;
+                lo[h] = b8;
+            }
+            _Float16 *ph = &lxh[buf][tok * kPhStride + 16 * (i & 15)];
+            _Float16 *pl = &lxl[buf][tok * kPhStride + 16 * (i & 15)];
+            *(h8_t *)ph = hi[0];
+            *(h8_t *)(ph + 8) = hi[1];
+            *(h8_t *)pl = lo[0];
+            *(h8_t *)(pl + 8) = lo[1];
+        }
+        if (t < 512) lsq[buf][(t & 7) * 64 + (t >> 3)] = (t >> 3) < a.M ? usq : 0.0f;
+    };
+    // weights of one step for this lane: qs 4 x 8 B + the 16-B header; two
+    // steps in flight (sets alternate by step parity)
+    i64x1_t wn[2][4];
+    v4i_t hn[2];
+    auto wload = [&](int st, int set) {
+        const int sc = min(st, s1 - 1);
+        const uint8_t *qs = W.q + ((size_t)row * nst + sc) * 128 + 8 * kg;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) wn[set][jj] = *(const i64x1_t *)(qs + 32 * jj);
+        hn[set] = *(const v4i_t *)(W.h + ((size_t)row * nst + sc) * 16);
+    };
+    float acc[4][4];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[tt][i] = 0.f;
+    wload(s0, 0);
+    wload(s0 + 1, 1);
+    xload(s0);
+    xstore(0);
+    if (s0 + 1 < s1) xload(s0 + 1);
+    __syncthreads();
+    auto step = [&](int st, int cur) {
+        i64x1_t w[4];
+        const v4i_t h = hn[cur];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) w[jj] = wn[cur][jj];
+        if (st + 2 < s1) wload(st + 2, cur);
+        if (live) {
+            const uint32_t h0 = (uint32_t)h.x;
+            const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+            v4f32_t cm[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) cm[tt] = v4f32_t{0.f, 0.f, 0.f, 0.f};
+            const _Float16 *bh = lxh[NB == 2 ? cur : 0], *bl = lxl[NB == 2 ? cur : 0];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int jj = j & 3;
+                // unpack_q4k_scales (model.rs:8709-8719), flare packing
+                const uint32_t sa = byte_of((uint32_t)h.y, jj), scc = byte_of((uint32_t)h.w, jj);
+                const uint32_t sc = j < 4 ? (sa & 63) : ((sa >> 6) | ((scc & 0xF) << 2));
+                const _Float16 scf = (_Float16)(float)sc;
+                const h2_t sc2 = {scf, scf}, bias2 = {(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
+                const h8_t b = q4_scaled_h8(w[jj], j >= 4, sc2, bias2);
+                v8h_t bv;
+                __builtin_memcpy(&bv, &b, 16);
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const int o = (tA + 16 * tt) * kPhStride + 32 * j + 8 * kg;
+                    cm[tt] = mfma16(*(const v8h_t *)(bh + o), bv, cm[tt]);
+                    cm[tt] = mfma16(*(const v8h_t *)(bl + o), bv, cm[tt]);
+                }
+            }
+            // min terms: K = 8 f32 MFMA per tile (A = s * sum q, B = mn of
+            // sub-blocks kg and 4 + kg of this lane's row)
+            const uint32_t sbb = byte_of((uint32_t)h.z, kg), scc = byte_of((uint32_t)h.w, kg);
+            const float mn0 = (float)(sbb & 63), mn1 = (float)((sbb >> 6) | ((scc >> 4) << 2));
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) {
+                v4f32_t c = {0.f, 0.f, 0.f, 0.f};
+                const float *lq = lsq[NB == 2 ? cur : 0];
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(lq[kg * 64 + tA + 16 * tt], mn0, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(lq[(4 + kg) * 64 + tA + 16 * tt], mn1, c, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(d, cm[tt][i], __builtin_fmaf(-dmin, c[i], acc[tt][i]));
+            }
+        }
+        if (st + 1 < s1) {
+            if constexpr (NB == 1) __syncthreads();  // every wave is done with the buffer
+            xstore(NB == 2 ? cur ^ 1 : 0);
+            if (st + 2 < s1) xload(st + 2);
+        }
+        __syncthreads();
+    };
+    // the register set and LDS buffer of step st are (st - s0) & 1
+    for (int st = s0; st < s1; st += 2) {
+        step(st, 0);
+        if (st + 1 < s1) step(st + 1, 1);
+    }
+    if (n < W.rows) {
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tk = 16 * tt + 4 * kg + i;
+                if (tk < a.M) a.part[((size_t)blockIdx.y * a.M + tk) * W.rows + n] = acc[tt][i];
             }
     }
 }
