@@ -425,6 +425,58 @@ struct RegX8L {
     __device__ __forceinline__ void finish(const MvsArgs &, int) {}
 };
 
+// PRO_LOADQ variant for Q4_K weights: lane l's 16 qs bytes of a step hold
+// half `h` of sub-blocks c (low nibbles) and c+4 (high nibbles) of one
+// super-block, so the lane loads those two 16-code runs of the pre-quantized
+// activation and its own sub-block's (scale, code sum): c on the even lane,
+// c+4 on the odd one (the pair add of pc_dot_q8 gives each its full block).
+template <int SX>
+struct RegX4L {
+    v4i_t ql[SX], qh[SX];
+    float sc[SX];
+    int sm[SX];
+    __device__ __forceinline__ void issue(const MvsArgs &a, int lane) {
+        const int span = (a.W.cols >> 8) * 128;
+#pragma unroll
+        for (int s = 0; s < SX; s++) {
+            const int off = min(s * 1024 + 16 * lane, span - 16);
+            const int sb = off >> 7, c = (off >> 5) & 3, h = (off >> 4) & 1;
+            const int blo = sb * 8 + c, bhi = blo + 4, own = h ? bhi : blo;
+            ql[s] = *(const v4i_t *)(a.gq + blo * 32 + h * 16);
+            qh[s] = *(const v4i_t *)(a.gq + bhi * 32 + h * 16);
+            sc[s] = a.gs[own];
+            sm[s] = a.gsum[own];
+        }
+    }
+    __device__ __forceinline__ void finish(const MvsArgs &, int) {}
+};
+
+// dot_q4k_q8_0_scalar per-sub-block term (as pc_dot_q8) with the activation
+// runs in registers
+template <int SX>
+__device__ __forceinline__ float pc_dot_q4x(const Pc<F_Q4K> &P, const WDesc &W, const RegX4L<SX> &X, int s,
+                                            int lane) {
+    const int span = (W.cols >> 8) * 128, off0 = s * 1024 + 16 * lane;
+    const int off = min(off0, span - 16);
+    const int c = (off >> 5) & 3, half = (off >> 4) & 1;
+    const v4i_t lo = P.q & 0x0F0F0F0F, hi = (P.q >> 4) & 0x0F0F0F0F;
+    int dl = dot16(lo, X.ql[s], 0), dh = dot16(hi, X.qh[s], 0);
+    dl += xpair(dl);
+    dh += xpair(dh);
+    const uint32_t h0 = (uint32_t)P.h.x;
+    const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
+    // unpack_q4k_scales (model.rs:8709-8719), flare packing
+    const uint32_t s_a = byte_of((uint32_t)P.h.y, c), s_b = byte_of((uint32_t)P.h.z, c),
+                   s_c = byte_of((uint32_t)P.h.w, c);
+    const bool own_hi = half;
+    const uint32_t sc = own_hi ? ((s_a >> 6) | ((s_c & 0xF) << 2)) : (s_a & 63);
+    const uint32_t mn = own_hi ? ((s_b >> 6) | ((s_c >> 4) << 2)) : (s_b & 63);
+    const int dot = own_hi ? dh : dl;
+    const float d_sc = d * (float)sc, dmin_mn = dmin * (float)mn;
+    const float t = X.sc[s] * (d_sc * (float)dot - dmin_mn * (float)X.sm[s]);
+    return off0 < span ? t : 0.0f;
+}
+
 // matvec_q8_0_preq_into per-block term with the activation codes in registers
 __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W, const v4i_t &xq, float xs, int step,
                                             int lane) {
@@ -494,7 +546,8 @@ constexpr int kMvsThreads = 256;
 // order (SeqFold, seq_sumsq); LDS grows by seq_lds_bytes(4, R, SU)
 template <int FMT, bool F32IN, int R, int SU, int RX = 0, bool SEQ = false>
 __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
-    static_assert(!RX || (FMT == F_Q8_0 && !F32IN), "register activation: Q8_0 weights, Q8 input");
+    static_assert(!RX || ((FMT == F_Q8_0 || (FMT == F_Q4K && RX == 2)) && !F32IN),
+                  "register activation: Q8_0 weights (or pre-quantized Q4_K input), Q8 input");
     static_assert(!SEQ || !F32IN, "reference-order sums: Q8 input");
     extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
@@ -518,7 +571,8 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     MV_TS(0);
     MV_TSB(0);
     Stage<F32IN, kMvsThreads, SEQ> stg;
-    typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1, SEQ>>::type rx;
+    typename std::conditional<RX == 2, typename std::conditional<FMT == F_Q4K, RegX4L<SU>, RegX8L<SU>>::type,
+                              RegX8<RX ? SU : 1, SEQ>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);             // 1. activation loads
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
@@ -587,7 +641,10 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 #pragma unroll
             for (int r = 0; r < R; r++)
 #pragma unroll
-                for (int s = 0; s < SU; s++) acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                for (int s = 0; s < SU; s++) {
+                    if constexpr (FMT == F_Q4K) acc[r] += pc_dot_q4x(T[r][s], W, rx, s, lane);
+                    else acc[r] += pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
+                }
         } else {
 #pragma unroll
             for (int r = 0; r < R; r++)

@@ -26,6 +26,20 @@ hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
         SX(4, 1) SX(2, 1) SX(1, 2)
         return hipErrorNotSupported;
     }
+    // pre-quantized input whose row fits one unit: the lane's activation runs
+    // in registers (RegX4L, no LDS staging or workgroup barrier)
+    static const bool noregx = getenv("FLARE_NO_REGX") != nullptr;
+    if (!noregx && a.pro == PRO_LOADQ && mvs_steps(F_Q4K, a.W.cols) <= p.su) {
+#define CR(RR, SS)                                                                                        \
+    if (p.r == RR && p.su == SS) {                                                                        \
+        hipLaunchKernelGGL((k_mvs<F_Q4K, false, RR, SS, 2>),                                               \
+                           dim3(resident_grid(k_mvs<F_Q4K, false, RR, SS, 2>, kMvsThreads, p.lds, p.grid)), \
+                           dim3(kMvsThreads), p.lds, st, a);                                            \
+        return hipSuccess;                                                                                \
+    }
+        CR(1, 2) CR(2, 2) CR(4, 2)
+#undef CR
+    }
     C(F_Q4K, false, 4, 1) C(F_Q4K, false, 2, 1) C(F_Q4K, false, 2, 2) C(F_Q4K, false, 1, 2) C(F_Q4K, false, 1, 4)
     return hipErrorNotSupported;
 }
