@@ -64,15 +64,22 @@ hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a) {
     const int npairs = a.nq / 2;
     if (a.nq < 2 || a.nq % 2 || !a.v_tblk || a.nsplit < 1 || a.nsplit > kAttmMaxSplit || a.S % 32 || a.chmin < 1)
         return hipErrorInvalidValue;
-    // 8 waves with one query pair each (two pairs per wave, sharing each LDS
-    // fragment read, measured slower at the Llama-3-8B prefill shape: C3
-    // 4096-token prefill 452 against 515 ms)
-    const int NW = npairs <= 4 ? 4 : 8, RP = 1;
-    const dim3 grid(a.nsplit, a.nkv, (npairs + NW * RP - 1) / (NW * RP));
+    // pairs per workgroup x block lanes (waves per pair, each walking every
+    // BW-th block): 8 x 2 for prefill passes (C3 4096-token prefill 380 ms
+    // against 388 with 8 x 1; two pairs per wave sharing each LDS fragment
+    // read measured slower, 452 against 515 ms before other changes), 4 x 2 for
+    // up to 8 queries (the verify batches keep k_attm, which measured faster).
+    // FLARE_ATTQ_BW / FLARE_ATTQ_PBW: 1 or 2 (measurement switches)
+    static const int bwe = getenv("FLARE_ATTQ_BW") ? atoi(getenv("FLARE_ATTQ_BW")) : 2;
+    static const int pbw = getenv("FLARE_ATTQ_PBW") ? atoi(getenv("FLARE_ATTQ_PBW")) : 2;
+    const int NPW = npairs <= 4 ? 4 : 8, BW = npairs <= 4 ? (bwe == 1 ? 1 : 2) : (pbw == 1 ? 1 : 2);
+    const dim3 grid(a.nsplit, a.nkv, (npairs + NPW - 1) / NPW);
 #define C(DD, GG)                                                                                     \
     if (D == DD && G == GG) {                                                                         \
-        if (NW == 4) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4, RP>), grid, dim3(256), 0, st, a);      \
-        else hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8, RP>), grid, dim3(512), 0, st, a);               \
+        if (NPW == 8 && BW == 2) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8, 2>), grid, dim3(1024), 0, st, a); \
+        else if (NPW == 8) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 8, 1>), grid, dim3(512), 0, st, a); \
+        else if (BW == 1) hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4, 1>), grid, dim3(256), 0, st, a);  \
+        else hipLaunchKernelGGL((k_attq<DD, 2 * GG, 4, 2>), grid, dim3(512), 0, st, a);               \
         return hipGetLastError();                                                                     \
     }
     C(64, 1) C(64, 2) C(64, 4) C(128, 1) C(128, 2) C(128, 4)
