@@ -822,7 +822,14 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
     const int tc = min(t, a.M - 1);
     auto psum = [&](int row) {
         float v = 0.0f;
-        for (int k = 0; k < a.ksplit; k++) v += ld_agent(a.part + ((size_t)k * a.M + tc) * W.rows + row);
+        for (int k0 = 0; k0 < a.ksplit; k0 += 8) {  // 8 loads in flight, added in split order
+            float pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) pv[u] = ld_agent(a.part + ((size_t)min(k0 + u, a.ksplit - 1) * a.M + tc) * W.rows + row);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (k0 + u < a.ksplit) v += pv[u];
+        }
         return v;
     };
     if (a.post == 1) {
@@ -848,10 +855,36 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
 
 // ---- per-token glue ------------------------------------------------------
 
+// Sum of the K-split partials of one output, in split order (loads issued 8
+// at a time, all in flight, then added in order: the same sum as a loop).
 __device__ __forceinline__ float vsum_part(const float *part, int ksplit, int M, int rows, int t, int n) {
     float v = 0.0f;
-    for (int k = 0; k < ksplit; k++) v += part[((size_t)k * M + t) * rows + n];
+    for (int k0 = 0; k0 < ksplit; k0 += 8) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = part[((size_t)min(k0 + u, ksplit - 1) * M + t) * rows + n];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (k0 + u < ksplit) v += pv[u];
+    }
     return v;
+}
+__device__ __forceinline__ float4 vsum_part4(const float *part, int ksplit, int M, int rows, int t, int e) {
+    float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k0 = 0; k0 < ksplit; k0 += 8) {
+        float4 pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = *(const float4 *)(part + ((size_t)min(k0 + u, ksplit - 1) * M + t) * rows + e);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (k0 + u < ksplit) {
+                p.x += pv[u].x;
+                p.y += pv[u].y;
+                p.z += pv[u].z;
+                p.w += pv[u].w;
+            }
+    }
+    return p;
 }
 
 // Embedding rows of the M tokens (token_embedding lookup, model.rs:1964).
@@ -953,14 +986,7 @@ __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part
             v[c] = *(const float4 *)(xt + e);
             wv[c] = *(const float4 *)(w + e);
             if (part) {
-                float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                for (int k = 0; k < ksplit; k++) {
-                    const float4 pk = *(const float4 *)(part + ((size_t)k * M + t) * H + e);
-                    p.x += pk.x;
-                    p.y += pk.y;
-                    p.z += pk.z;
-                    p.w += pk.w;
-                }
+                const float4 p = vsum_part4(part, ksplit, M, H, t, e);
                 v[c].x += p.x;
                 v[c].y += p.y;
                 v[c].z += p.z;
