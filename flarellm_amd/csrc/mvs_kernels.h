@@ -126,35 +126,66 @@ __device__ __forceinline__ float pc_dot_q8(const Pc<F_Q8_0> &P, const WDesc &W, 
     return (off0 < K && !(lane & 1)) ? t : 0.0f;
 }
 
-// dot_q4k_q8_0_scalar per-sub-block term (model.rs:8969-9025):
+// Q4_K (scale, min) of the sub-block a lane owns after the pair add: c (even
+// lane, low nibbles) or c+4 (odd lane, high nibbles), with c = (lane / 2) % 4
+// (unpack_q4k_scales model.rs:8709-8719, flare packing).  Low half: sc =
+// y.byte(c) & 63, mn = z.byte(c) & 63; high half: sc = y.byte(c) >> 6 |
+// (w.byte(c) & 15) << 2, mn = z.byte(c) >> 6 | (w.byte(c) >> 4) << 2.  Both
+// cases are bit-field extracts at lane-constant offsets and widths (a zero
+// width extracts 0), so a lane spends 6 integer ops per (row, step) on them.
+struct Q4Lane {
+    uint32_t oa, wa, oc, wc;
+    __device__ __forceinline__ explicit Q4Lane(int lane) {
+        const uint32_t c = (lane >> 1) & 3, h = lane & 1;
+        oa = 8 * c + 6 * h;
+        wa = h ? 2 : 6;
+        oc = 8 * c;
+        wc = h ? 4 : 0;
+    }
+    __device__ __forceinline__ void scmn(const v4i_t &hd, uint32_t &sc, uint32_t &mn) const {
+        const uint32_t y = (uint32_t)hd.y, z = (uint32_t)hd.z, w = (uint32_t)hd.w;
+        sc = __builtin_amdgcn_ubfe(y, oa, wa) | (__builtin_amdgcn_ubfe(w, oc, wc) << 2);
+        mn = __builtin_amdgcn_ubfe(z, oa, wa) | (__builtin_amdgcn_ubfe(w, oc + 4, wc) << 2);
+    }
+};
+
+// dot_q4k_q8_0_scalar per-sub-block term (model.rs:8969-9025) of one lane:
 // s_x * (d*sc*dot - dmin*mn*sum(q_x)).  The 16 qs bytes of a lane hold half of
-// sub-block c (low nibbles) and half of sub-block c+4 (high nibbles); after
-// the pair add the even lane owns sub c, the odd lane sub c+4.
-__device__ __forceinline__ float pc_dot_q8(const Pc<F_Q4K> &P, const WDesc &W, const int8_t *lq, const float *ls,
-                                           const int *lsum, int step, int lane) {
-    const int span = (W.cols >> 8) * 128, off0 = step * 1024 + 16 * lane;
-    const int off = min(off0, span - 16);
-    const int sb = off >> 7, c = (off >> 5) & 3, half = (off >> 4) & 1;
-    const int blo = sb * 8 + c, bhi = blo + 4;
-    const v4i_t xl = *(const v4i_t *)(lq + blo * 32 + half * 16);
-    const v4i_t xh = *(const v4i_t *)(lq + bhi * 32 + half * 16);
+// sub-block c (low nibbles, activation run xl) and half of sub-block c+4 (high
+// nibbles, run xh); the pair add gives the even lane sub-block c's full dot
+// and the odd lane c+4's (each lane keeps its own half-dot and passes the
+// other one to its partner).  xs is the lane's block scale (0 for a lane past
+// the row's end), xsum its block code sum.
+__device__ __forceinline__ float q4_term(const Pc<F_Q4K> &P, const v4i_t &xl, const v4i_t &xh, float xs, float xsum,
+                                         const Q4Lane &L) {
     const v4i_t lo = P.q & 0x0F0F0F0F, hi = (P.q >> 4) & 0x0F0F0F0F;
-    int dl = dot16(lo, xl, 0), dh = dot16(hi, xh, 0);
-    dl += xpair(dl);
-    dh += xpair(dh);
+    const int dl = dot16(lo, xl, 0), dh = dot16(hi, xh, 0);
+    const bool odd = L.wc != 0;
+    const int dot = (odd ? dh : dl) + xpair(odd ? dl : dh);
     const uint32_t h0 = (uint32_t)P.h.x;
     const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
-    // unpack_q4k_scales (model.rs:8709-8719), flare packing
-    const uint32_t s_a = byte_of((uint32_t)P.h.y, c), s_b = byte_of((uint32_t)P.h.z, c),
-                   s_c = byte_of((uint32_t)P.h.w, c);
-    const bool own_hi = half;  // odd lane: sub-block c+4
-    const uint32_t sc = own_hi ? ((s_a >> 6) | ((s_c & 0xF) << 2)) : (s_a & 63);
-    const uint32_t mn = own_hi ? ((s_b >> 6) | ((s_c >> 4) << 2)) : (s_b & 63);
-    const int b = own_hi ? bhi : blo;
-    const int dot = own_hi ? dh : dl;
+    uint32_t sc, mn;
+    L.scmn(P.h, sc, mn);
     const float d_sc = d * (float)sc, dmin_mn = dmin * (float)mn;
-    const float t = ls[b] * (d_sc * (float)dot - dmin_mn * (float)lsum[b]);
-    return off0 < span ? t : 0.0f;
+    return xs * (d_sc * (float)dot - dmin_mn * xsum);
+}
+
+// the same term with the activation codes, scales and sums in LDS
+__device__ __forceinline__ float pc_dot_q8(const Pc<F_Q4K> &P, const WDesc &W, const int8_t *lq, const float *ls,
+                                           const int *lsum, int step, int lane) {
+    const int K = W.cols, span = (K >> 8) * 128, off0 = step * 1024 + 16 * lane;
+    // lane-constant parts of the activation offsets: the lane's low run is
+    // sub-block c of super-block off0/128 (bytes blo*32 + half*16), its high
+    // run 128 bytes on, its own block blo (+4 on the odd lane); the step adds
+    // 2048 bytes / 64 blocks.  Lanes past the row's end read a clamped, valid
+    // offset and contribute 0 through a zero activation scale.
+    const Q4Lane L(lane);
+    const int lo_b = min(step * 2048 + (lane >> 3) * 256 + ((lane >> 1) & 3) * 32 + (lane & 1) * 16, K - 144);
+    const int own = min(step * 64 + (lane >> 3) * 8 + ((lane >> 1) & 3) + 4 * (lane & 1), (K >> 5) - 1);
+    const v4i_t xl = *(const v4i_t *)(lq + lo_b);
+    const v4i_t xh = *(const v4i_t *)(lq + lo_b + 128);
+    const float xs = off0 < span ? ls[own] : 0.0f;
+    return q4_term(P, xl, xh, xs, (float)lsum[own], L);
 }
 
 // ---- f32 input (activations in LDS as floats) ------------------------------
@@ -457,24 +488,7 @@ template <int SX>
 __device__ __forceinline__ float pc_dot_q4x(const Pc<F_Q4K> &P, const WDesc &W, const RegX4L<SX> &X, int s,
                                             int lane) {
     const int span = (W.cols >> 8) * 128, off0 = s * 1024 + 16 * lane;
-    const int off = min(off0, span - 16);
-    const int c = (off >> 5) & 3, half = (off >> 4) & 1;
-    const v4i_t lo = P.q & 0x0F0F0F0F, hi = (P.q >> 4) & 0x0F0F0F0F;
-    int dl = dot16(lo, X.ql[s], 0), dh = dot16(hi, X.qh[s], 0);
-    dl += xpair(dl);
-    dh += xpair(dh);
-    const uint32_t h0 = (uint32_t)P.h.x;
-    const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
-    // unpack_q4k_scales (model.rs:8709-8719), flare packing
-    const uint32_t s_a = byte_of((uint32_t)P.h.y, c), s_b = byte_of((uint32_t)P.h.z, c),
-                   s_c = byte_of((uint32_t)P.h.w, c);
-    const bool own_hi = half;
-    const uint32_t sc = own_hi ? ((s_a >> 6) | ((s_c & 0xF) << 2)) : (s_a & 63);
-    const uint32_t mn = own_hi ? ((s_b >> 6) | ((s_c >> 4) << 2)) : (s_b & 63);
-    const int dot = own_hi ? dh : dl;
-    const float d_sc = d * (float)sc, dmin_mn = dmin * (float)mn;
-    const float t = X.sc[s] * (d_sc * (float)dot - dmin_mn * (float)X.sm[s]);
-    return off0 < span ? t : 0.0f;
+    return q4_term(P, X.ql[s], X.qh[s], off0 < span ? X.sc[s] : 0.0f, (float)X.sm[s], Q4Lane(lane));
 }
 
 // matvec_q8_0_preq_into per-block term with the activation codes in registers
