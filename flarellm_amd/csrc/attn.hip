@@ -142,10 +142,10 @@ __global__ __launch_bounds__(256) void k_kv_q8_write(AttnArgs a, const float *kr
     const int t = p0 + r;
     if (isv) {  // V codes into the 32-slot transposed blocks
         int8_t *q = (int8_t *)a.vc + (size_t)kvh * a.head_stride;
-        for (int e = 0; e < 32; e++) q[vt_off(t, 32 * b + e, D)] = sat_i8(roundf(x[e] * id));
+        for (int e = 0; e < 32; e++) q[vt_off(t, 32 * b + e, D)] = q8_code(x[e] * id);
     } else {
         int8_t *q = (int8_t *)a.kc + (size_t)kvh * a.head_stride + (size_t)t * D + 32 * b;
-        for (int e = 0; e < 32; e++) q[e] = sat_i8(roundf(x[e] * id));
+        for (int e = 0; e < 32; e++) q[e] = q8_code(x[e] * id);
     }
     (isv ? a.vs : a.ks)[((size_t)kvh * a.S + t) * nb + b] = f2h(d);
 }

@@ -195,7 +195,7 @@ __device__ __forceinline__ void q8_block8(const float *x, v2i_t &q, uint16_t &s)
     const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)sat_i8(roundf(x[i] * id)) << (8 * (i & 3));
+    for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q8_code(x[i] * id) << (8 * (i & 3));
     q = v2i_t{(int)w[0], (int)w[1]};
     s = f2h(d);
 }

@@ -35,8 +35,17 @@ typedef int v2i_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half(f)); }
 
+// v_dot4_i32_i8 with an inline-constant zero accumulator: the builtin's
+// v_dot4c form accumulates in place and first needs a v_mov of 0
+__device__ __forceinline__ int dot4_z(int a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ int dot16(const v4i_t &a, const v4i_t &b, int c) {
-    c = __builtin_amdgcn_sdot4(a.x, b.x, c, false);
+    if (__builtin_constant_p(c) && c == 0) c = dot4_z(a.x, b.x);
+    else c = __builtin_amdgcn_sdot4(a.x, b.x, c, false);
     c = __builtin_amdgcn_sdot4(a.y, b.y, c, false);
     c = __builtin_amdgcn_sdot4(a.z, b.z, c, false);
     c = __builtin_amdgcn_sdot4(a.w, b.w, c, false);
@@ -232,6 +241,19 @@ __device__ __forceinline__ int8_t sat_i8(float v) {
     return (int8_t)(int)v;
 }
 
+// quantize_input_q8_0_into's code (y).round() as i8 (model.rs:5557-5570):
+// round half away from zero, then saturate to [-128, 127] (a NaN gives -128,
+// as sat_i8 does).  Adding the largest float below 0.5 with y's sign and
+// truncating rounds exactly as roundf for every float: the sum reaches the
+// next integer only when y's fraction is at least 0.5 (at a fraction just
+// below 0.5 it stays at least an ulp short), and a y of 2^23 or more is
+// already an integer that the addition rounds back to.  Clamping before the
+// truncation does not change the result.  4 ops against roundf's 8.
+__device__ __forceinline__ int8_t q8_code(float y) {
+    const float s = y + __builtin_copysignf(0.49999997f, y);
+    return (int8_t)(int)fminf(fmaxf(s, -128.0f), 127.0f);
+}
+
 // quantize_input_q8_0_into for one 32-block (model.rs:5557-5570).
 __device__ __forceinline__ void quant_block32(const float *v, int8_t *q, float *s, int *sum) {
     float amax = 0.0f;
@@ -246,7 +268,7 @@ __device__ __forceinline__ void quant_block32(const float *v, int8_t *q, float *
         uint32_t p = 0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            int8_t qq = sat_i8(roundf(v[4 * j + k] * id));
+            int8_t qq = q8_code(v[4 * j + k] * id);
             acc += qq;
             p |= (uint32_t)(uint8_t)qq << (8 * k);
         }
@@ -269,7 +291,7 @@ __device__ __forceinline__ void quant_block32_lanes(float v, int8_t *q, float *s
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const float d = amax / 127.0f;
     const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
-    const int8_t qq = sat_i8(roundf(v * id));
+    const int8_t qq = q8_code(v * id);
     q[lane] = qq;
     int t = qq;
 #pragma unroll

@@ -146,17 +146,20 @@ struct StageQ8 {
         const float rms = sqrtf(ss / (float)n + eps);
         const float inv = 1.0f / rms;
         float v[16];
+        // rmsnorm_quantize_q8_0_scalar (x*w)*inv (model.rs:5615) or
+        // rmsnorm_scalar_into (x*inv)*w (model.rs:7474): one branch on the
+        // uniform prologue kind
+        if (pro == PRO_NORMQ0) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = j < E ? xs[j] * ws[j] * inv : 0.0f;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = j < E ? (xs[j] * inv) * ws[j] : 0.0f;
+        }
         float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            v[j] = 0.0f;
-            if (j < E) {
-                // rmsnorm_quantize_q8_0_scalar (x*w)*inv (model.rs:5615) or
-                // rmsnorm_scalar_into (x*inv)*w (model.rs:7474)
-                v[j] = (pro == PRO_NORMQ0) ? xs[j] * ws[j] * inv : (xs[j] * inv) * ws[j];
-                amax = fmaxf(amax, fabsf(v[j]));
-            }
-        }
+        for (int j = 0; j < 16; j++)
+            if (j < E) amax = fmaxf(amax, fabsf(v[j]));
         // a 32-block spans 32/E consecutive lanes of one row
         if (E == 8) amax = row_max<4>(amax);
         else amax = row_max<2>(amax);
@@ -167,7 +170,7 @@ struct StageQ8 {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             if (j < E) {
-                const int8_t qq = sat_i8(roundf(v[j] * id));
+                const int8_t qq = q8_code(v[j] * id);
                 qsum += qq;
                 packed[j >> 2] |= (uint32_t)(uint8_t)qq << (8 * (j & 3));
             }

@@ -416,21 +416,23 @@ struct RegX8 {
 #pragma unroll
         for (int s = 0; s < SX; s++) {
             float v[16];
+            // (x*w)*inv or (x*inv)*w: one branch on the uniform prologue kind
+            if (a.pro == PRO_NORMQ0) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = xv[s][i >> 2][i & 3] * wv[s][i >> 2][i & 3] * inv;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = (xv[s][i >> 2][i & 3] * inv) * wv[s][i >> 2][i & 3];
+            }
             float amax = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float x = xv[s][j][k], w = wv[s][j][k];
-                    v[4 * j + k] = a.pro == PRO_NORMQ0 ? x * w * inv : (x * inv) * w;
-                    amax = fmaxf(amax, fabsf(v[4 * j + k]));
-                }
+            for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
             amax = fmaxf(amax, __int_as_float(xpair(__float_as_int(amax))));  // the block's other half
             const float d = amax / 127.0f;
             const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
             uint32_t pk[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 16; i++) pk[i >> 2] |= (uint32_t)(uint8_t)sat_i8(roundf(v[i] * id)) << (8 * (i & 3));
+            for (int i = 0; i < 16; i++) pk[i >> 2] |= (uint32_t)(uint8_t)q8_code(v[i] * id) << (8 * (i & 3));
             q[s] = v4i_t{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
             sc[s] = d;
         }

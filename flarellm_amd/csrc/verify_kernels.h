@@ -1023,7 +1023,7 @@ __global__ __launch_bounds__(kResnormThreads) void k_v_resnorm(const float *part
         int8_t qq[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            qq[j] = sat_i8(roundf(y[j] * id));
+            qq[j] = q8_code(y[j] * id);
             cs += qq[j];
         }
         char4 cq;
