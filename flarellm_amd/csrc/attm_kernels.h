@@ -834,8 +834,16 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
 #pragma unroll
                     for (int k2 = 0; k2 < MB; k2++) {
                         const float *pj = pb + (size_t)min(j0 + k2, nact - 1) * P;
-                        mv[k2] = ld_agent(pj + G * D + 2 * g);
-                        lv[k2] = ld_agent(pj + G * D + 2 * g + 1);
+                        if constexpr (D == 64) {
+                            // (m, l) in one load: measured faster at D = 64
+                            // (Llama-3.2-1B), slower at D = 128 (Llama-3-8B)
+                            const float2 ml = ld_agent2(pj + G * D + 2 * g);
+                            mv[k2] = ml.x;
+                            lv[k2] = ml.y;
+                        } else {
+                            mv[k2] = ld_agent(pj + G * D + 2 * g);
+                            lv[k2] = ld_agent(pj + G * D + 2 * g + 1);
+                        }
                         ov[k2] = ld_agent(pj + i);
                     }
                     float Mb = M[k];
@@ -864,6 +872,21 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         ATTN_TSL(7);
 #pragma unroll
         for (int k = 0; k < OPT; k++) O[k] *= 1.0f / L[k];
+        if constexpr (OPT == 1) {
+            // one output per thread, a 32-block in 32 consecutive lanes: the
+            // Q8_0 copy straight from registers (no LDS round trip)
+            if (tid == 0) __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid < G * D) {
+                if (a.out) a.out[oix(tid)] = O[0];
+                if (a.oq) {
+                    const size_t e0 = oix(tid & ~31);
+                    quant_block32_lanes(O[0], a.oq + e0, a.os + e0 / 32, a.osum + e0 / 32);
+                }
+            }
+            ATTN_TSL(8);
+            ATTN_TSL(9);
+            return;
+        }
         __syncthreads();  // red (mo) is rewritten below
 #pragma unroll
         for (int k = 0; k < OPT; k++) {

@@ -109,6 +109,12 @@ __device__ __forceinline__ void st_agent(float *p, float v) {
 __device__ __forceinline__ float ld_agent(const float *p) {
     return __uint_as_float(__hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
+// two adjacent floats (8-byte aligned) in one agent-scope load
+__device__ __forceinline__ float2 ld_agent2(const float *p) {
+    const unsigned long long u =
+        __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((unsigned)u), __uint_as_float((unsigned)(u >> 32)));
+}
 
 __device__ __forceinline__ void h8_to_f32(const v4i_t &v, float *o) {
     const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
