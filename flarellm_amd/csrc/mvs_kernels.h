@@ -46,7 +46,22 @@ __device__ __forceinline__ void i8x4_to_f32(int w, float *q) {
 #endif
 
 // lanes l and l^1 exchange a value (quad_perm [1,0,3,2])
-__device__ __forceinline__ int xpair(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int xpair(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true); }
+
+// f32 product of the f16 in the low (high) half of w and b, rounded once as a
+// plain multiply: v_fma_mix_f32 with the f16 operand selected by op_sel and a
+// -0 addend (x + -0 = x for every x, signed zeros included), one op instead of
+// a conversion and a multiply
+__device__ __forceinline__ float mul_h16lo(uint32_t w, float b) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
+    return r;
+}
+__device__ __forceinline__ float mul_h16hi(uint32_t w, float b) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
+    return r;
+}
 
 // bytes of one row in the streamed plane
 __host__ __device__ inline int mvs_span(int fmt, int K) {
@@ -122,7 +137,7 @@ __device__ __forceinline__ float pc_dot_q8(const Pc<F_Q8_0> &P, const WDesc &W, 
     const v4i_t x = *(const v4i_t *)(lq + off);
     int d = dot16(P.q, x, 0);
     d += xpair(d);
-    const float t = (h2f((uint16_t)P.sc) * ls[off >> 5]) * (float)d;
+    const float t = mul_h16lo(P.sc, ls[off >> 5]) * (float)d;
     return (off0 < K && !(lane & 1)) ? t : 0.0f;
 }
 
@@ -163,10 +178,9 @@ __device__ __forceinline__ float q4_term(const Pc<F_Q4K> &P, const v4i_t &xl, co
     const bool odd = L.wc != 0;
     const int dot = (odd ? dh : dl) + xpair(odd ? dl : dh);
     const uint32_t h0 = (uint32_t)P.h.x;
-    const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
     uint32_t sc, mn;
     L.scmn(P.h, sc, mn);
-    const float d_sc = d * (float)sc, dmin_mn = dmin * (float)mn;
+    const float d_sc = mul_h16lo(h0, (float)sc), dmin_mn = mul_h16hi(h0, (float)mn);
     return xs * (d_sc * (float)dot - dmin_mn * xsum);
 }
 
@@ -498,7 +512,7 @@ __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W,
                                             int lane) {
     int d = dot16(P.q, xq, 0);
     d += xpair(d);
-    const float t = (h2f((uint16_t)P.sc) * xs) * (float)d;
+    const float t = mul_h16lo(P.sc, xs) * (float)d;
     return (step * 1024 + 16 * lane < W.cols && !(lane & 1)) ? t : 0.0f;
 }
 
