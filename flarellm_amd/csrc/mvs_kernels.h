@@ -173,7 +173,12 @@ struct Q4Lane {
 // the row's end), xsum its block code sum.
 __device__ __forceinline__ float q4_term(const Pc<F_Q4K> &P, const v4i_t &xl, const v4i_t &xh, float xs, float xsum,
                                          const Q4Lane &L) {
-    const v4i_t lo = P.q & 0x0F0F0F0F, hi = (P.q >> 4) & 0x0F0F0F0F;
+    const v4i_t lo = P.q & 0x0F0F0F0F;
+    // high nibbles: one 64-bit shift per two words
+    const uint64_t w01 = ((uint64_t)(uint32_t)P.q.y << 32) | (uint32_t)P.q.x;
+    const uint64_t w23 = ((uint64_t)(uint32_t)P.q.w << 32) | (uint32_t)P.q.z;
+    const uint64_t h01 = (w01 >> 4) & 0x0F0F0F0F0F0F0F0Full, h23 = (w23 >> 4) & 0x0F0F0F0F0F0F0F0Full;
+    const v4i_t hi = {(int)(uint32_t)h01, (int)(uint32_t)(h01 >> 32), (int)(uint32_t)h23, (int)(uint32_t)(h23 >> 32)};
     const int dl = dot16(lo, xl, 0), dh = dot16(hi, xh, 0);
     const bool odd = L.wc != 0;
     const int dot = (odd ? dh : dl) + xpair(odd ? dl : dh);
