@@ -243,8 +243,7 @@ __device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q8_0> &P, const XIn<F_Q8
 #pragma unroll
         for (int k = 0; k < 4; k++) a = __builtin_fmaf((float)((u >> (8 * k)) & 0xFFu), X.x[j][k], a);
     }
-    const float scale = h2f((uint16_t)P.sc);
-    return X.ok ? scale * (a - 128.0f * X.g) : 0.0f;
+    return X.ok ? mul_h16lo(P.sc, a - 128.0f * X.g) : 0.0f;
 }
 
 // dequant_q6k_block (quantize.rs:343-384, llama.cpp layout): w = d*sc*q.
@@ -279,16 +278,17 @@ __device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q6K> &P, const XIn<F_Q6K
     for (int j = 0; j < 4; j++) {
         // four 6-bit codes per word, assembled byte-wise: nibble | 2 qh bits << 4
         const uint32_t lw = (uint32_t)P.ql[j], hw = (uint32_t)P.qh[j];
-        const uint32_t clo = (lw & 0x0F0F0F0Fu) | (((hw >> X.sh) & 0x03030303u) << 4);
-        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (X.sh + 4)) & 0x03030303u) << 4);
+        // (the 2 bits at sh / sh + 4 of each qh byte land on bits 4-5 by one
+        // shift within the byte, sh <= 2)
+        const uint32_t clo = (lw & 0x0F0F0F0Fu) | ((hw << (4 - X.sh)) & 0x30303030u);
+        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> X.sh) & 0x30303030u);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             slo = __builtin_fmaf((float)((clo >> (8 * k)) & 0xFFu), X.xl[j][k], slo);
             shi = __builtin_fmaf((float)((chi >> (8 * k)) & 0xFFu), X.xh[j][k], shi);
         }
     }
-    const float d = h2f((uint16_t)P.d);
-    const float ds_lo = d * (float)(int8_t)(P.sc & 0xFF), ds_hi = d * (float)(int8_t)(P.sc >> 8);
+    const float ds_lo = mul_h16lo(P.d, (float)(int8_t)(P.sc & 0xFF)), ds_hi = mul_h16lo(P.d, (float)(int8_t)(P.sc >> 8));
     return X.ok ? ds_lo * (slo - 32.0f * X.glo) + ds_hi * (shi - 32.0f * X.ghi) : 0.0f;
 }
 
