@@ -14,6 +14,7 @@
 #include <unistd.h>
 
 #include <cctype>
+#include <climits>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -238,24 +239,37 @@ bool meta_f32(const fl_gguf *g, const std::string &key, float *out) {
     return true;
 }
 
+// Element count (numel().max(1)); 0 when the product of the dimensions does
+// not fit in 63 bits (a crafted header), which every caller rejects.
 uint64_t numel(const TensorInfo &t) {
     uint64_t n = 1;
-    for (uint64_t d : t.dims) n *= d;
-    return n ? n : 1;  // numel().max(1)
+    for (uint64_t d : t.dims) {
+        if (d != 0 && n > (UINT64_C(1) << 63) / d) return 0;
+        n *= d;
+    }
+    return n ? n : 1;
 }
 
 int tensor_bytes(const TensorInfo &t, uint64_t *bytes) {
     uint64_t e, b;
     if (!ggml_block(t.type, &e, &b)) return FL_E_UNSUPPORTED;
-    *bytes = (numel(t) + e - 1) / e * b;  // bytes_for_elements (quantize.rs:139-147)
+    const uint64_t n = numel(t);
+    if (n == 0) return FL_E_INVALID;
+    const uint64_t blocks = n / e + (n % e != 0);
+    if (blocks > UINT64_MAX / b) return FL_E_INVALID;
+    *bytes = blocks * b;  // bytes_for_elements (quantize.rs:139-147)
     return 0;
 }
 
 int tensor_span(const fl_gguf *g, const TensorInfo &t, const uint8_t **p, uint64_t *bytes) {
     int rc = tensor_bytes(t, bytes);
-    if (rc) return gg_fail(rc, "unsupported quantization format of tensor " + t.name);
+    if (rc == FL_E_UNSUPPORTED) return gg_fail(rc, "unsupported quantization format of tensor " + t.name);
+    if (rc) return gg_fail(rc, "tensor " + t.name + " has dimensions whose product overflows");
+    // offset checked before the addition, so a huge offset cannot wrap
+    if (g->data_offset > g->len || t.offset > g->len - g->data_offset)
+        return gg_fail(FL_E_INVALID, "tensor " + t.name + " starts past the end of the file");
     const uint64_t start = g->data_offset + t.offset;
-    if (start > g->len || *bytes > g->len - start)
+    if (*bytes > g->len - start)
         return gg_fail(FL_E_INVALID, "tensor " + t.name + " extends past the end of the file");
     *p = g->data + start;
     return 0;
@@ -427,7 +441,9 @@ int fl_gguf_raw_weight(const fl_gguf *g, const char *name, fl_raw_weight *out) {
     // dimensions are [cols, rows]: the last one is the output rows
     const uint64_t rows = t->dims.empty() ? 1 : t->dims.back();
     uint64_t cols = 1;
-    for (size_t d = 0; d + 1 < t->dims.size(); d++) cols *= t->dims[d];
+    for (size_t d = 0; d + 1 < t->dims.size(); d++) cols *= t->dims[d];  // bounded: numel() did not overflow
+    if (rows > (uint64_t)INT_MAX || (cols + wpb - 1) / wpb > (uint64_t)INT_MAX)
+        return gg_fail(FL_E_INVALID, std::string("tensor ") + name + " has more rows or blocks than an int holds");
     out->data = p;
     out->nbytes = (size_t)bytes;
     out->format = fmt;

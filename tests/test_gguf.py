@@ -199,3 +199,29 @@ def test_f16_tensor_dequant(tmp_path):
     got = g.tensor_f32("w", n)
     want = bits.view(np.float16).astype(np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _one_tensor(dims, typ, offset, payload=b""):
+    buf = header(1, 0) + gstr("w") + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims) + \
+        struct.pack("<IQ", typ, offset)
+    buf += b"\0" * (-len(buf) % 32)
+    return GgufFile(data=buf + payload)
+
+
+def test_crafted_offset_does_not_wrap():
+    """A tensor offset near 2**64 must be rejected, not wrapped to a small
+    start inside the file."""
+    payload = bytes(34 * 4)
+    g = _one_tensor([32, 4], 8, (1 << 64) - 64, payload)
+    with pytest.raises(FlareError):
+        g.raw_weight("w")
+    # the same tensor at offset 0 reads back
+    data, fmt, rows, bpr = _one_tensor([32, 4], 8, 0, payload).raw_weight("w")
+    assert (fmt, rows, bpr) == (FL_Q8_0, 4, 1) and data.size == 34 * 4
+
+
+def test_dims_overflow_rejected():
+    """Dimensions whose product overflows 64 bits are rejected."""
+    g = _one_tensor([1 << 40, 1 << 40], 8, 0, bytes(64))
+    with pytest.raises(FlareError):
+        g.raw_weight("w")
