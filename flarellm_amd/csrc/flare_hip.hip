@@ -53,7 +53,8 @@ template <int PRO, bool SEQ>
 __global__ __launch_bounds__(kThreads) void k_norm_quant(const float *x, const float *w, int n,
                                                          float eps, int8_t *q, float *s, int *sums) {
     __shared__ float red[8];
-    stage_q8<PRO, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, q, s, sums, red);
+    __shared__ float ess[SEQ ? kEssLdsWords + 1 : 1];
+    stage_q8<PRO, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, q, s, sums, red, SEQ ? ess : nullptr);
 }
 
 __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const float *w, int n,

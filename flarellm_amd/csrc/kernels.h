@@ -309,12 +309,17 @@ __device__ __forceinline__ void quant_block32_lanes(float v, int8_t *q, float *s
 // ------------------------------------------------------------------------
 enum Pro { PRO_LOADQ = 0, PRO_NORMQ0 = 1, PRO_NORMQ1 = 2 };
 
-// SEQ: the sum of squares in the reference's sequential order (seq_sumsq).
+}  // namespace fl
+#include "ess.h"
+namespace fl {
+
+// SEQ: the sum of squares in the reference's sequential order (ess_sumsq_wg
+// with `ess` = kEssLdsWords + 1 floats of LDS, else the plain loop).
 template <bool SEQ = false>
-__device__ __forceinline__ float wg_inv_rms(const float *x, int n, float eps, float *red) {
+__device__ __forceinline__ float wg_inv_rms(const float *x, int n, float eps, float *red, float *ess = nullptr) {
     float ss = 0.0f;
     if (SEQ) {
-        ss = seq_sumsq(x, n);
+        ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
     } else {
         for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
         ss = wg_sum(ss, red);
@@ -326,7 +331,7 @@ __device__ __forceinline__ float wg_inv_rms(const float *x, int n, float eps, fl
 template <int PRO, bool SEQ = false>
 __device__ __forceinline__ void stage_q8(const float *x, const float *w, float eps, int n,
                                          const int8_t *gq, const float *gs, const int *gsum,
-                                         int8_t *lq, float *ls, int *lsum, float *red) {
+                                         int8_t *lq, float *ls, int *lsum, float *red, float *ess = nullptr) {
     const int nb = n >> 5;
     if (PRO == PRO_LOADQ) {
         const v4i_t *src = (const v4i_t *)gq;
@@ -339,7 +344,7 @@ __device__ __forceinline__ void stage_q8(const float *x, const float *w, float e
     } else {
         // one element per lane; the 32 lanes of a half-wave form one block
         // (blockDim and n are multiples of 32), quantized by the lane quantizer
-        const float inv = wg_inv_rms<SEQ>(x, n, eps, red);
+        const float inv = wg_inv_rms<SEQ>(x, n, eps, red, ess);
         for (int i = threadIdx.x; i < n; i += blockDim.x) {
             const float v = (PRO == PRO_NORMQ0) ? x[i] * w[i] * inv : (x[i] * inv) * w[i];
             quant_block32_lanes(v, lq + (i & ~31), ls + (i >> 5), lsum + (i >> 5));

@@ -101,7 +101,8 @@ struct StageQ8 {
     }
 
     __device__ __forceinline__ void finish(int pro, int n, float eps, const float *x, const float *w,
-                                           int8_t *lq, float *ls, int *lsum, float *red, long long *tr = nullptr) {
+                                           int8_t *lq, float *ls, int *lsum, float *red, long long *tr = nullptr,
+                                           float *ess = nullptr) {
         const int t = threadIdx.x;
         ST_TS(7);
         if (pro == PRO_LOADQ) {
@@ -124,8 +125,8 @@ struct StageQ8 {
         }
         const int E = n / NT;
         if (!(n == NT * E && (E == 8 || E == 16))) {
-            if (pro == PRO_NORMQ0) stage_q8<PRO_NORMQ0, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
-            else stage_q8<PRO_NORMQ1, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red);
+            if (pro == PRO_NORMQ0) stage_q8<PRO_NORMQ0, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red, ess);
+            else stage_q8<PRO_NORMQ1, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red, ess);
             return;
         }
         float xs[16], ws[16];
@@ -140,7 +141,7 @@ struct StageQ8 {
         for (int j = 0; j < 16; j++)
             if (j < E) ss += xs[j] * xs[j];
         ST_TS(8);
-        if (SEQ) ss = seq_sumsq(x, n);
+        if (SEQ) ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
         else ss = wg_sum(ss, red);
         ST_TS(9);
         const float rms = sqrtf(ss / (float)n + eps);

@@ -345,20 +345,20 @@ template <int NT, bool SEQ>
 struct Stage<false, NT, SEQ> {
     StageQ8<NT, SEQ> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw, a.gq, a.gs, a.gsum); }
-    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
+    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem, float *ess = nullptr) {
         const int K = a.W.cols;
         int8_t *lq = (int8_t *)smem;
         float *ls = (float *)(smem + K);
         int *lsum = (int *)(ls + (K >> 5));
         float *red = (float *)(lsum + (K >> 5));
-        s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red, a.trace);
+        s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red, a.trace, ess);
     }
 };
 template <int NT, bool SEQ>
 struct Stage<true, NT, SEQ> {
     StageF32<NT> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw); }
-    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem) {
+    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem, float * = nullptr) {
         const int K = a.W.cols;
         float *lx = (float *)smem;
         s.finish(a.pro, K, a.eps, a.x, a.nw, lx, lx + K + K / 16);
@@ -416,20 +416,32 @@ struct RegX8 {
             }
         }
     }
-    __device__ __forceinline__ void finish(const MvsArgs &a, int lane) {
+    // ess: this wave's kEssLdsWords floats of LDS (SEQ)
+    __device__ __forceinline__ void finish(const MvsArgs &a, int lane, float *ess = nullptr) {
         const int K = a.W.cols;
         float ss = 0.0f;
+        if constexpr (SEQ) {
+            // the reference's sequential order, reproduced exactly (ess.h)
+            float t[SX][16];
 #pragma unroll
-        for (int s = 0; s < SX; s++) {
-            if (s * 1024 + 16 * lane < K) {
+            for (int s = 0; s < SX; s++) {
+                const bool ok = s * 1024 + 16 * lane < K;
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-#pragma unroll
-                    for (int k = 0; k < 4; k++) ss += xv[s][j][k] * xv[s][j][k];
+                for (int i = 0; i < 16; i++) t[s][i] = ok ? xv[s][i >> 2][i & 3] * xv[s][i >> 2][i & 3] : 0.0f;
             }
+            ss = ess_sumsq<SX>(t, K, lane, ess, a.x);
+        } else {
+#pragma unroll
+            for (int s = 0; s < SX; s++) {
+                if (s * 1024 + 16 * lane < K) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) ss += xv[s][j][k] * xv[s][j][k];
+                }
+            }
+            ss = wave_sum(ss);
         }
-        if (SEQ) ss = seq_sumsq(a.x, K);  // the reference's sequential order
-        else ss = wave_sum(ss);
         const float rms = sqrtf(ss / (float)K + a.eps);
         const float inv = 1.0f / rms;
 #pragma unroll
@@ -474,7 +486,7 @@ struct RegX8L {
             sc[s] = a.gs[off >> 5];
         }
     }
-    __device__ __forceinline__ void finish(const MvsArgs &, int) {}
+    __device__ __forceinline__ void finish(const MvsArgs &, int, float * = nullptr) {}
 };
 
 // PRO_LOADQ variant for Q4_K weights: lane l's 16 qs bytes of a step hold
@@ -500,7 +512,7 @@ struct RegX4L {
             sm[s] = a.gsum[own];
         }
     }
-    __device__ __forceinline__ void finish(const MvsArgs &, int) {}
+    __device__ __forceinline__ void finish(const MvsArgs &, int, float * = nullptr) {}
 };
 
 // dot_q4k_q8_0_scalar per-sub-block term (as pc_dot_q8) with the activation
@@ -536,7 +548,7 @@ __device__ __forceinline__ float pc_dot_q8x(const Pc<F_Q8_0> &P, const WDesc &W,
 template <int FMT, int R, int SU>
 struct SeqFold {
     float run = 0.0f;  // lane r: running sum of row r
-    __device__ __forceinline__ void add(const float (&t)[R][SU], float *fs, int rr, int span, int lane) {
+    __device__ __forceinline__ void add(const float (&t)[R][SU], float *fs, int rr, int lane) {
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -546,13 +558,26 @@ struct SeqFold {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (rr == 0) run = 0.0f;
         if (lane < R) {
+            // all 64 terms of a step are read before the dependent adds; the
+            // terms past the row's end are +-0 and leave the sum unchanged
+            // (the running sum starts at +0 and never becomes -0)
+#pragma unroll
             for (int s = 0; s < SU; s++) {
-                const int nl = min(64, max(0, (span - (rr * SU + s) * 1024 + 15) >> 4));
-                const float *p = fs + (lane * SU + s) * 64;
-                if (FMT == F_Q8_0) {
-                    for (int l = 0; l < nl; l += 2) run += p[l];
-                } else {
-                    for (int l = 0; l < nl; l++) run += p[l];
+                const v4f_t *p = (const v4f_t *)(fs + (lane * SU + s) * 64);
+                v4f_t v[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = p[i];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    if (FMT == F_Q8_0) {  // one term per lane pair (the even lane)
+                        run += v[i].x;
+                        run += v[i].z;
+                    } else {
+                        run += v[i].x;
+                        run += v[i].y;
+                        run += v[i].z;
+                        run += v[i].w;
+                    }
                 }
             }
         }
@@ -567,8 +592,13 @@ struct SeqFold {
 };
 
 __host__ __device__ inline size_t align16(size_t b) { return (b + 15) & ~(size_t)15; }
-// LDS of the SEQ fold areas: waves x R x SU x 64 floats
-__host__ __device__ inline size_t seq_lds_bytes(int waves, int r, int su) { return (size_t)waves * r * su * 64 * 4; }
+// LDS of the SEQ areas, per wave: the fold terms (R x SU x 64 floats) or the
+// exact sum of squares' scratch (wave 0's area also serves the workgroup form)
+__host__ __device__ inline int seq_wave_words(int r, int su) {
+    const int f = r * su * 64, e = (kEssLdsWords + 1 + 3) & ~3;
+    return f > e ? f : e;
+}
+__host__ __device__ inline size_t seq_lds_bytes(int waves, int r, int su) { return (size_t)waves * seq_wave_words(r, su) * 4; }
 
 // ---------------------------------------------------------------------------
 // k_mvs: generic persistent streaming matvec
@@ -638,8 +668,10 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         pre1 = *p1;
     }
     MV_TS(1);
-    if constexpr (RX) rx.finish(a, lane);
-    else stg.finish(a, smem);      // 3. prologue arithmetic (ends with a barrier)
+    float *seqa = (float *)(smem + align16(mvs_lds_bytes(F32IN, K)));  // SEQ areas
+    float *fs = seqa + wave * seq_wave_words(R, SU);
+    if constexpr (RX) rx.finish(a, lane, fs);
+    else stg.finish(a, smem, seqa);  // 3. prologue arithmetic (ends with a barrier)
     MV_TS(2);
 
     float acc[R];
@@ -647,7 +679,6 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     unsigned long long best = 0;
     SeqFold<FMT, R, SU> fold;
-    float *fs = (float *)(smem + align16(mvs_lds_bytes(F32IN, K))) + wave * (R * SU * 64);
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
         const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
         if constexpr (SEQ) {
@@ -659,7 +690,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
                     if constexpr (RX) t[r][s] = pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
                     else t[r][s] = pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
                 }
-            fold.add(t, fs, rr, mvs_span(FMT, K), lane);
+            fold.add(t, fs, rr, lane);
         } else if constexpr (F32IN) {
             // one step at a time: the lane's activation floats are loaded
             // once and shared by the R rows (not hoisted for the whole tile)
@@ -774,15 +805,16 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     FLARE_STAGE_BARRIER();
     load(ta, 0);  // unconditional, so the prologue waits for the activation loads only
     MV_TS(1);
-    if constexpr (RX) rx.finish(a, lane);
-    else stg.finish(a, smem);
+    float *seqa = (float *)(smem + align16(mvs_lds_bytes(false, K) + 32 * 4));  // SEQ areas
+    float *fs = seqa + wave * seq_wave_words(R, SU);
+    if constexpr (RX) rx.finish(a, lane, fs);
+    else stg.finish(a, smem, seqa);
     MV_TS(2);
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     SeqFold<FMT, R, SU> fold;
-    float *fs = (float *)(smem + align16(mvs_lds_bytes(false, K) + 32 * 4)) + wave * (R * SU * 64);
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
         int blk, item, rr;
         rows_of(u, blk, item, rr);
@@ -795,7 +827,7 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
                     if constexpr (RX) t[r][s] = pc_dot_q8x(T[r][s], W, rx.q[s], rx.sc[s], s, lane);
                     else t[r][s] = pc_dot<FMT, false>(T[r][s], W, smem, rr * SU + s, lane);
                 }
-            fold.add(t, fs, rr, mvs_span(FMT, K), lane);
+            fold.add(t, fs, rr, lane);
         } else {
 #pragma unroll
             for (int r = 0; r < R; r++)

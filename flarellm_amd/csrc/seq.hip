@@ -59,7 +59,8 @@ __global__ __launch_bounds__(256) void k_attn_seq(SeqAttnArgs a) {
 // rmsnorm_into (model.rs:7456-7477): (x * inv_rms) * w with the sequential
 // sum of squares.  One workgroup.
 __global__ __launch_bounds__(256) void k_rmsnorm_seq(const float *x, const float *w, int n, float eps, float *out) {
-    const float inv = wg_inv_rms<true>(x, n, eps, nullptr);
+    __shared__ float ess[kEssLdsWords + 1];
+    const float inv = wg_inv_rms<true>(x, n, eps, nullptr, ess);
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] * inv) * w[i];
 }
 

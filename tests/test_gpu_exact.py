@@ -95,6 +95,38 @@ def test_exact_rmsnorm_quantize_bit_exact(exact, oracle, n, order):
     assert np.array_equal(_bits(s.cpu().numpy()), _bits(so))
 
 
+def _ess_vectors(n, seed):
+    """Vectors that stress the exact sum of squares: scales over 80 decades,
+    zero runs, heavy tails, integer values (frequent ties), a constant, a
+    tiny leading element, growing magnitudes."""
+    rng = np.random.default_rng(seed)
+    out = [rng.standard_normal(n) * 10.0 ** rng.uniform(-18, 18) for _ in range(6)]
+    v = rng.standard_normal(n)
+    v[: n // 3] = 0.0
+    out.append(v)
+    out.append(np.where(rng.random(n) < 0.01, rng.standard_normal(n) * 1e5, rng.standard_normal(n)))
+    out.append(np.round(rng.standard_normal(n) * 8.0))
+    out.append(np.ldexp(1.0, rng.integers(-10, 10, n)).astype(np.float64))
+    out.append(np.full(n, 1.0 + 2.0 ** -20))
+    v = rng.standard_normal(n)
+    v[0] = 1e-30
+    out.append(v)
+    out.append(rng.standard_normal(n) * np.arange(1, n + 1))
+    return [np.ascontiguousarray(v, np.float32) for v in out]
+
+
+@pytest.mark.parametrize("n", [576, 1024, 2048, 3072, 4096])
+def test_exact_sum_of_squares_stress(exact, oracle, n):
+    """rmsnorm_into in reference order (the exact sum of squares of ess.h,
+    workgroup form) over adversarial vectors: every output bit-identical to
+    the oracle's sequential fold."""
+    w = np.ones(n, np.float32)
+    for i, x in enumerate(_ess_vectors(n, 100 + n)):
+        got = exact.rmsnorm(_t(x), _t(w), 1e-5).cpu().numpy()
+        want = oracle.rmsnorm(x, w, 1e-5)
+        assert np.array_equal(_bits(got), _bits(want)), f"vector {i}: {(_bits(got) != _bits(want)).sum()} differ"
+
+
 TINY = {
     "q8_tied": S.tiny_spec(FL_Q8_0),
     "q4k_q6k_out": S.tiny_spec(FL_Q4K, embed_fmt=FL_Q6K, output_fmt=FL_Q6K),
