@@ -296,6 +296,11 @@ struct fl_ctx {
     float *scratch = nullptr;     // device address of `scratch` on this context's GPU
     float *seq_scores = nullptr;  // [num_heads][kv_slots] attention scores (exact mode)
     float *seq_xn = nullptr;      // [hidden] final-normed vector (exact mode)
+    // layer probe (fl_probe_layer): intermediates of one layer of the step
+    int probe_layer = -1;
+    char *probe_dev = nullptr;
+    void *probe_host = nullptr;
+    size_t probe_bytes = 0;
     // device sampler (allocated on first use, for rows of up to sample_cap)
     int sample_cap = 0, sample_prev_cap = 0;
     float *sp = nullptr;
@@ -712,6 +717,11 @@ static void model_release(fl_ctx *c) {
     c->attn = c->logits = c->bench_out = nullptr; c->bench_trace = nullptr; c->rope_cur = nullptr; c->aq = c->hq = nullptr; c->as = c->hs = nullptr;
     c->asum = c->hsum = nullptr; c->st = nullptr; c->tokens = nullptr;
     c->seq_scores = c->seq_xn = nullptr;
+    if (c->probe_dev) (void)hipFree(c->probe_dev);
+    c->probe_dev = nullptr;
+    c->probe_bytes = 0;
+    c->probe_layer = -1;
+    c->probe_host = nullptr;
     void *vp[] = {c->vx, c->vx2, c->vq, c->vk, c->vv, c->vpart, c->vxq, c->vaq, c->vxs, c->vas, c->vxsum, c->vasum,
                   c->vtok, c->vpos, c->vslots, c->vhq, c->vhs, c->vhsum, c->vcnt};
     for (void *p : vp)
@@ -1309,6 +1319,49 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
     return e;
 }
 
+// ---- layer probe ------------------------------------------------------------
+// Byte offsets of the probe regions (PR_*), each 256-byte aligned; returns the
+// total size.
+enum { PR_XIN, PR_Q, PR_K, PR_V, PR_ATTN, PR_AS, PR_XMID, PR_HS, PR_XOUT, PR_XFIN, PR_AQ, PR_HQ, PR_N };
+static size_t probe_layout(const fl_model_config &c, size_t off[PR_N]) {
+    const size_t H = c.hidden_dim, nq = (size_t)c.num_heads * c.head_dim, nk = (size_t)c.num_kv_heads * c.head_dim,
+                 F = c.intermediate_dim;
+    const size_t sz[PR_N] = {H * 4, nq * 4, nk * 4, nk * 4, nq * 4, nq / 32 * 4, H * 4, F / 32 * 4, H * 4, H * 4, nq, F};
+    size_t o = 0;
+    for (int i = 0; i < PR_N; i++) {
+        off[i] = o;
+        o += (sz[i] + 255) / 256 * 256;
+    }
+    return o;
+}
+
+}  // extern "C"
+// K / V rows of the step's slot (cache layout of kv_layer_args) as f32
+template <bool F16>
+__global__ void k_probe_kv(const void *kc, const void *vc, long long head_stride, int D, int nkv, bool vt,
+                           const DevState *st, float *k, float *v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nkv * D) return;
+    const int h = i / D, d = i % D, t = st->pos;
+    const size_t kb = (size_t)h * head_stride;
+    const size_t ko = kb + (size_t)t * D + d, vo = kb + (vt ? vt_off(t, d, D) : (size_t)t * D + d);
+    if (F16) {
+        k[i] = __half2float(((const __half *)kc)[ko]);
+        v[i] = __half2float(((const __half *)vc)[vo]);
+    } else {
+        k[i] = ((const float *)kc)[ko];
+        v[i] = ((const float *)vc)[vo];
+    }
+}
+extern "C" {
+
+static int probe_copy(fl_ctx *ctx, int region, const void *src, size_t bytes) {
+    size_t off[PR_N];
+    probe_layout(ctx->cfg, off);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->probe_dev + off[region], src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return 0;
+}
+
 // x_given: the caller has put the step's f32 embedding row into ctx->x.
 static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
     const fl_model_config &c = ctx->cfg;
@@ -1325,12 +1378,39 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
     default: hipLaunchKernelGGL(k_embed<F_F32>, dim3(1), dim3(kEmbedThreads), 0, ctx->stream, ctx->embed.desc(), ctx->st, ctx->tokens, x_given ? nullptr : ctx->x, ctx->rope, sin_off, c.head_dim / 2, ctx->rope_cur); break;
     }
     HIPCHK(ctx, hipGetLastError());
+    const size_t H = c.hidden_dim, nq = (size_t)c.num_heads * hd, nk = (size_t)c.num_kv_heads * hd;
+    const size_t F = c.intermediate_dim;
+    size_t poff[PR_N];
+    probe_layout(c, poff);
     for (int l = 0; l < c.num_layers; l++) {
         Layer &L = ctx->layers[l];
+        const bool probe = l == ctx->probe_layer && ctx->probe_dev;
+        int rc;
+        if (probe && (rc = probe_copy(ctx, PR_XIN, ctx->x, H * 4))) return rc;
         const QkvEpi qe = layer_qkv_epi(ctx, l);
-        int rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
-                             ctx->qkv, nullptr, &qe);
+        rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
+                         ctx->qkv, nullptr, &qe);
         if (rc) return rc;
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_Q, ctx->qkv, nq * 4))) return rc;
+            float *pk = (float *)(ctx->probe_dev + poff[PR_K]), *pv = (float *)(ctx->probe_dev + poff[PR_V]);
+            if (ctx->kv_format == FL_KV_F32 || ctx->kv_format == FL_KV_F16) {
+                AttnArgs ka{};
+                kv_layer_args(ctx, l, ka);
+                const int n = (int)nk;
+                if (ctx->kv_format == FL_KV_F16)
+                    hipLaunchKernelGGL(k_probe_kv<true>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc,
+                                       ka.vc, ka.head_stride, hd, c.num_kv_heads, true, ctx->st, pk, pv);
+                else
+                    hipLaunchKernelGGL(k_probe_kv<false>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc,
+                                       ka.vc, ka.head_stride, hd, c.num_kv_heads, false, ctx->st, pk, pv);
+                HIPCHK(ctx, hipGetLastError());
+            } else {
+                // Q8 / KIVI: the f32 rows the attention kernel quantizes
+                if ((rc = probe_copy(ctx, PR_K, ctx->qkv + nq, nk * 4))) return rc;
+                if ((rc = probe_copy(ctx, PR_V, ctx->qkv + nq + nk, nk * 4))) return rc;
+            }
+        }
         if (ctx->exact) {
             // reference-order attention, then quantize_input_q8_0_into of its output
             AttnArgs a = layer_attn_args(ctx, l);
@@ -1350,19 +1430,35 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
             hipLaunchKernelGGL(k_quantize, dim3((nblk + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream,
                                ctx->attn, nblk, ctx->aq, ctx->as, ctx->asum);
             HIPCHK(ctx, hipGetLastError());
+            if (probe && (rc = probe_copy(ctx, PR_ATTN, ctx->attn, nq * 4))) return rc;
         } else {
             AttnArgs a = layer_attn_args(ctx, l);
+            if (probe) a.out = (float *)(ctx->probe_dev + poff[PR_ATTN]);  // also the f32 output
             rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
             if (rc) return rc;
+        }
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_AQ, ctx->aq, nq))) return rc;
+            if ((rc = probe_copy(ctx, PR_AS, ctx->as, nq / 32 * 4))) return rc;
         }
         rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
                          nullptr);
         if (rc) return rc;
+        if (probe && (rc = probe_copy(ctx, PR_XMID, ctx->x, H * 4))) return rc;
         rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs,
                            ctx->hsum, nullptr);
         if (rc) return rc;
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_HQ, ctx->hq, F))) return rc;
+            if ((rc = probe_copy(ctx, PR_HS, ctx->hs, F / 32 * 4))) return rc;
+        }
         rc = launch_q8in(ctx, L.down, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum, ctx->x,
                          nullptr);
+        if (rc) return rc;
+        if (probe && (rc = probe_copy(ctx, PR_XOUT, ctx->x, H * 4))) return rc;
+    }
+    if (ctx->probe_dev && ctx->probe_layer >= 0) {
+        int rc = probe_copy(ctx, PR_XFIN, ctx->x, H * 4);
         if (rc) return rc;
     }
     // output projection (forward_greedy, model.rs:1898-1932)
@@ -1440,8 +1536,9 @@ static int decode_step(fl_ctx *ctx, uint32_t token, const float *embedding, int 
     HIPCHK(ctx, hipMemcpyAsync(ctx->st, &hs, sizeof hs, hipMemcpyHostToDevice, ctx->stream));
     if (embedding)
         HIPCHK(ctx, hipMemcpyAsync(ctx->x, embedding, (size_t)c.hidden_dim * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (out_logits || embedding) {
+    if (out_logits || embedding || ctx->probe_layer >= 0) {
         // enqueued directly: the captured step dequantizes the token's row
+        // (and carries no probe copies)
         int rc = enqueue_step(ctx, out_logits != nullptr, embedding != nullptr);
         if (rc) return rc;
     } else {
@@ -1453,6 +1550,9 @@ static int decode_step(fl_ctx *ctx, uint32_t token, const float *embedding, int 
     HIPCHK(ctx, hipMemcpyAsync(&out, ctx->st, sizeof out, hipMemcpyDeviceToHost, ctx->stream));
     if (out_logits)
         HIPCHK(ctx, hipMemcpyAsync(out_logits, ctx->logits, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    if (ctx->probe_layer >= 0 && ctx->probe_host)
+        HIPCHK(ctx, hipMemcpyAsync(ctx->probe_host, ctx->probe_dev, ctx->probe_bytes, hipMemcpyDeviceToHost,
                                    ctx->stream));
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
     if (out_logits) {
@@ -1471,6 +1571,31 @@ static int decode_step(fl_ctx *ctx, uint32_t token, const float *embedding, int 
         std::memcpy(&v, &u, 4);
         if (out_val) *out_val = v;
     }
+    return 0;
+}
+
+int fl_probe_layout(const fl_ctx *ctx, size_t *offsets, int n) {
+    if (!ctx || !ctx->have_cfg || !offsets || n < PR_N) return -1;
+    return (int)probe_layout(ctx->cfg, offsets);
+}
+
+int fl_probe_layer(fl_ctx *ctx, int layer, void *host_buf) {
+    if (!ctx || !ctx->have_cfg) return fail(ctx, FL_E_STATE, "no model");
+    if (layer < 0) {
+        ctx->probe_layer = -1;
+        ctx->probe_host = nullptr;
+        return 0;
+    }
+    if (layer >= ctx->cfg.num_layers || !host_buf) return fail(ctx, FL_E_INVALID, "layer %d / null buffer", layer);
+    size_t off[PR_N];
+    const size_t bytes = probe_layout(ctx->cfg, off);
+    if (!ctx->probe_dev) {
+        ALLOC(ctx, ctx->probe_dev, bytes);
+        HIPCHK(ctx, hipMemset(ctx->probe_dev, 0, bytes));
+        ctx->probe_bytes = bytes;
+    }
+    ctx->probe_layer = layer;
+    ctx->probe_host = host_buf;
     return 0;
 }
 
