@@ -356,36 +356,42 @@ class HipBackend:
                   self.ctx)
         return out
 
-    PROBE_FIELDS = ("x_in", "q", "k", "v", "attn", "attn_s", "x_mid", "h_s", "x_out", "x_final", "attn_q", "h_q")
+    PROBE_FIELDS = ("x_in", "q", "k", "v", "attn", "attn_s", "x_mid", "h_s", "x_out", "x_final", "attn_q", "h_q",
+                    "x_q", "x_s", "f_q", "f_s")
+    PROBE_TOKENS = 16
 
     def probe_layer(self, layer: int):
-        """Layer probe (fl_probe_layer): the following decode steps record
-        layer `layer`'s intermediates; read them with probe_read().  None turns
-        it off."""
+        """Layer probe (fl_probe_layer): the following decode steps and
+        verify passes record layer `layer`'s intermediates; read them with
+        probe_read().  None turns it off."""
         if layer is None or layer < 0:
             check(self.lib.fl_probe_layer(self.ctx, -1, None), self.ctx)
             self._probe = None
             return
-        off = (C.c_size_t * 12)()
-        total = self.lib.fl_probe_layout(self.ctx, off, 12)
+        off = (C.c_size_t * 16)()
+        total = self.lib.fl_probe_layout(self.ctx, off, 16)
         assert total > 0
         self._probe = (np.zeros(total, np.uint8), list(off))
         check(self.lib.fl_probe_layer(self.ctx, layer, self._probe[0].ctypes.data), self.ctx)
 
-    def probe_read(self) -> dict:
-        """The last probed step's intermediates (copies)."""
+    def probe_read(self, n_tokens: int = 1) -> dict:
+        """The last probed step's (or verify pass's) intermediates, [n_tokens, n]
+        arrays (copies); n_tokens = 1 for a decode step, squeezed."""
         buf, off = self._probe
         sp = self.spec
         nq, nk, H, F = sp.heads * sp.head_dim, sp.kv_heads * sp.head_dim, sp.hidden, sp.inter
         sizes = {"x_in": H, "q": nq, "k": nk, "v": nk, "attn": nq, "attn_s": nq // 32, "x_mid": H, "h_s": F // 32,
-                 "x_out": H, "x_final": H, "attn_q": nq, "h_q": F}
+                 "x_out": H, "x_final": H, "attn_q": nq, "h_q": F, "x_q": H, "x_s": H // 32, "f_q": H,
+                 "f_s": H // 32}
         out = {}
         for i, name in enumerate(self.PROBE_FIELDS):
-            n = sizes[name]
-            if name in ("attn_q", "h_q"):
-                out[name] = buf[off[i]:off[i] + n].view(np.int8).copy()
+            n = sizes[name] * n_tokens
+            if name in ("attn_q", "h_q", "x_q", "f_q"):
+                a = buf[off[i]:off[i] + n].view(np.int8).copy()
             else:
-                out[name] = buf[off[i]:off[i] + 4 * n].view(np.float32).copy()
+                a = buf[off[i]:off[i] + 4 * n].view(np.float32).copy()
+            a = a.reshape(n_tokens, -1)
+            out[name] = a[0] if n_tokens == 1 else a
         return out
 
     def generate(self, prompt, n_gen: int) -> np.ndarray:

@@ -1320,29 +1320,37 @@ static QkvEpi layer_qkv_epi(fl_ctx *ctx, int l) {
 }
 
 // ---- layer probe ------------------------------------------------------------
-// Byte offsets of the probe regions (PR_*), each 256-byte aligned; returns the
-// total size.
-enum { PR_XIN, PR_Q, PR_K, PR_V, PR_ATTN, PR_AS, PR_XMID, PR_HS, PR_XOUT, PR_XFIN, PR_AQ, PR_HQ, PR_N };
+// Regions (PR_*), each [kProbeTokens][per-token size], 256-byte aligned;
+// byte offsets into off[], total size returned.  The decode step fills token
+// 0; a verify pass its M tokens.  The norm codes (PR_XQ .. PR_FS) exist only
+// in the verify pass, whose GEMMs read them from memory.
+constexpr int kProbeTokens = 16;
+enum {
+    PR_XIN, PR_Q, PR_K, PR_V, PR_ATTN, PR_AS, PR_XMID, PR_HS, PR_XOUT, PR_XFIN, PR_AQ, PR_HQ,
+    PR_XQ, PR_XS, PR_FQ, PR_FS, PR_N
+};
 static size_t probe_layout(const fl_model_config &c, size_t off[PR_N]) {
     const size_t H = c.hidden_dim, nq = (size_t)c.num_heads * c.head_dim, nk = (size_t)c.num_kv_heads * c.head_dim,
                  F = c.intermediate_dim;
-    const size_t sz[PR_N] = {H * 4, nq * 4, nk * 4, nk * 4, nq * 4, nq / 32 * 4, H * 4, F / 32 * 4, H * 4, H * 4, nq, F};
+    const size_t sz[PR_N] = {H * 4, nq * 4, nk * 4, nk * 4, nq * 4, nq / 32 * 4, H * 4, F / 32 * 4, H * 4, H * 4,
+                             nq, F, H, H / 32 * 4, H, H / 32 * 4};
     size_t o = 0;
     for (int i = 0; i < PR_N; i++) {
         off[i] = o;
-        o += (sz[i] + 255) / 256 * 256;
+        o += (sz[i] * kProbeTokens + 255) / 256 * 256;
     }
     return o;
 }
 
 }  // extern "C"
-// K / V rows of the step's slot (cache layout of kv_layer_args) as f32
+// K / V rows of slots *posp .. *posp + M - 1 (cache layout of kv_layer_args)
+// as f32, [M][nkv*D]
 template <bool F16>
 __global__ void k_probe_kv(const void *kc, const void *vc, long long head_stride, int D, int nkv, bool vt,
-                           const DevState *st, float *k, float *v) {
+                           const int *posp, int M, float *k, float *v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nkv * D) return;
-    const int h = i / D, d = i % D, t = st->pos;
+    if (i >= M * nkv * D) return;
+    const int m = i / (nkv * D), r = i % (nkv * D), h = r / D, d = r % D, t = *posp + m;
     const size_t kb = (size_t)h * head_stride;
     const size_t ko = kb + (size_t)t * D + d, vo = kb + (vt ? vt_off(t, d, D) : (size_t)t * D + d);
     if (F16) {
@@ -1360,6 +1368,30 @@ static int probe_copy(fl_ctx *ctx, int region, const void *src, size_t bytes) {
     probe_layout(ctx->cfg, off);
     HIPCHK(ctx, hipMemcpyAsync(ctx->probe_dev + off[region], src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
     return 0;
+}
+
+// the layer's K / V rows at *posp .. + M - 1 (F32 / F16 caches), or the f32
+// staging rows the Q8 / KIVI writers quantize (`stage_k`, `stage_v`)
+static int probe_kv(fl_ctx *ctx, int l, const int *posp, int M, const float *stage_k, const float *stage_v) {
+    const fl_model_config &c = ctx->cfg;
+    size_t off[PR_N];
+    probe_layout(c, off);
+    float *pk = (float *)(ctx->probe_dev + off[PR_K]), *pv = (float *)(ctx->probe_dev + off[PR_V]);
+    const int n = M * c.num_kv_heads * c.head_dim;
+    if (ctx->kv_format == FL_KV_F32 || ctx->kv_format == FL_KV_F16) {
+        AttnArgs ka{};
+        kv_layer_args(ctx, l, ka);
+        if (ctx->kv_format == FL_KV_F16)
+            hipLaunchKernelGGL(k_probe_kv<true>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc, ka.vc,
+                               ka.head_stride, c.head_dim, c.num_kv_heads, true, posp, M, pk, pv);
+        else
+            hipLaunchKernelGGL(k_probe_kv<false>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc, ka.vc,
+                               ka.head_stride, c.head_dim, c.num_kv_heads, false, posp, M, pk, pv);
+        HIPCHK(ctx, hipGetLastError());
+        return 0;
+    }
+    int rc = probe_copy(ctx, PR_K, stage_k, (size_t)n * 4);
+    return rc ? rc : probe_copy(ctx, PR_V, stage_v, (size_t)n * 4);
 }
 
 // x_given: the caller has put the step's f32 embedding row into ctx->x.
@@ -1393,23 +1425,8 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
         if (rc) return rc;
         if (probe) {
             if ((rc = probe_copy(ctx, PR_Q, ctx->qkv, nq * 4))) return rc;
-            float *pk = (float *)(ctx->probe_dev + poff[PR_K]), *pv = (float *)(ctx->probe_dev + poff[PR_V]);
-            if (ctx->kv_format == FL_KV_F32 || ctx->kv_format == FL_KV_F16) {
-                AttnArgs ka{};
-                kv_layer_args(ctx, l, ka);
-                const int n = (int)nk;
-                if (ctx->kv_format == FL_KV_F16)
-                    hipLaunchKernelGGL(k_probe_kv<true>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc,
-                                       ka.vc, ka.head_stride, hd, c.num_kv_heads, true, ctx->st, pk, pv);
-                else
-                    hipLaunchKernelGGL(k_probe_kv<false>, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, ka.kc,
-                                       ka.vc, ka.head_stride, hd, c.num_kv_heads, false, ctx->st, pk, pv);
-                HIPCHK(ctx, hipGetLastError());
-            } else {
-                // Q8 / KIVI: the f32 rows the attention kernel quantizes
-                if ((rc = probe_copy(ctx, PR_K, ctx->qkv + nq, nk * 4))) return rc;
-                if ((rc = probe_copy(ctx, PR_V, ctx->qkv + nq + nk, nk * 4))) return rc;
-            }
+            // Q8 / KIVI: the f32 rows after q that the attention kernel quantizes
+            if ((rc = probe_kv(ctx, l, &ctx->st->pos, 1, ctx->qkv + nq, ctx->qkv + nq + nk))) return rc;
         }
         if (ctx->exact) {
             // reference-order attention, then quantize_input_q8_0_into of its output
@@ -2046,6 +2063,12 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         // norm only), one workgroup per token
         HIPCHK(ctx, launch_v_resnorm(pro, st, l ? ctx->vpart : nullptr, ks_down, M, H, xa, L.attn_norm, eps, ctx->vxq,
                                      ctx->vxs, ctx->vxsum));
+        const bool probe = l == ctx->probe_layer && ctx->probe_dev && M <= kProbeTokens;
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_XIN, xa, (size_t)M * H * 4))) return rc;
+            if ((rc = probe_copy(ctx, PR_XQ, ctx->vxq, (size_t)M * H))) return rc;
+            if ((rc = probe_copy(ctx, PR_XS, ctx->vxs, (size_t)M * (H / 32) * 4))) return rc;
+        }
         AttnArgs a{};
         kv_layer_args(ctx, l, a);
         // RoPE'd q; K and V straight into F16 / F32 cache slots, else staged
@@ -2076,6 +2099,10 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
             if (rc) return rc;
             HIPCHK(ctx, launch_v_qkv_post(st, ctx->vpart, ks, M, L.qkv.rows, pq.qp));
         }
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_Q, ctx->vq, (size_t)M * qd * 4))) return rc;
+            if ((rc = probe_kv(ctx, l, ctx->vpos, M, ctx->vk, ctx->vv))) return rc;
+        }
         if (!plain)
             HIPCHK(ctx, launch_kv_write(ctx->kv_format, st, a, ctx->vk, ctx->vv, pos0, M, D,
                                         dev_pos ? ctx->vpos : nullptr));
@@ -2095,7 +2122,9 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         a.waves = ctx->attn_waves;
         a.part = ctx->d_part;
         a.counters = ctx->d_counters;
-        a.out = nullptr;
+        size_t poff[PR_N];
+        probe_layout(c, poff);
+        a.out = probe ? (float *)(ctx->probe_dev + poff[PR_ATTN]) : nullptr;  // the f32 output, when probed
         a.oq = ctx->vaq;
         a.os = ctx->vas;
         a.osum = ctx->vasum;
@@ -2126,11 +2155,20 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
             if (e == hipErrorNotSupported) return fail(ctx, FL_E_UNSUPPORTED, "attention shape");
             HIPCHK(ctx, e);
         }
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_AQ, ctx->vaq, (size_t)M * qd))) return rc;
+            if ((rc = probe_copy(ctx, PR_AS, ctx->vas, (size_t)M * (qd / 32) * 4))) return rc;
+        }
         rc = verify_gemm(ctx, L.wo, M, ctx->vaq, ctx->vas, ctx->vasum, ks);
         if (rc) return rc;
         // FFN block (model.rs:2376-2543): wo residual + FFN norm in one kernel
         HIPCHK(ctx, launch_v_resnorm(pro, st, ctx->vpart, ks, M, H, xa, L.ffn_norm, eps, ctx->vxq, ctx->vxs,
                                      ctx->vxsum));
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_XMID, xa, (size_t)M * H * 4))) return rc;
+            if ((rc = probe_copy(ctx, PR_FQ, ctx->vxq, (size_t)M * H))) return rc;
+            if ((rc = probe_copy(ctx, PR_FS, ctx->vxs, (size_t)M * (H / 32) * 4))) return rc;
+        }
         if (fuse && L.gu.rows == 2 * F && F % 32 == 0) {
             // SiLU(gate)*up + Q8_0 in the GEMM's last-arriving K split
             VgArgs pg{};
@@ -2146,10 +2184,18 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
             if (!rc) HIPCHK(ctx, launch_v_silu_quant(st, ctx->vpart, ks, M, F, ctx->vhq, ctx->vhs, ctx->vhsum));
         }
         if (rc) return rc;
+        if (probe) {
+            if ((rc = probe_copy(ctx, PR_HQ, ctx->vhq, (size_t)M * F))) return rc;
+            if ((rc = probe_copy(ctx, PR_HS, ctx->vhs, (size_t)M * (F / 32) * 4))) return rc;
+        }
         rc = verify_gemm(ctx, L.down, M, ctx->vhq, ctx->vhs, ctx->vhsum, ks_down);
         if (rc) return rc;
     }
     HIPCHK(ctx, launch_v_residual(st, ctx->vpart, ks_down, M, H, xa));
+    if (ctx->probe_dev && ctx->probe_layer >= 0 && M <= kProbeTokens) {
+        rc = probe_copy(ctx, PR_XFIN, xa, (size_t)M * H * 4);
+        if (rc) return rc;
+    }
     if (out_mode == VOUT_NONE) return 0;
     // output projection + fused argmax per token (forward_greedy, model.rs:1898-1932)
     const fl_weight &O = ctx->tied ? ctx->embed : ctx->output;
@@ -2226,7 +2272,8 @@ static int run_verify_pass(fl_ctx *ctx, int M, const int *pos_host, int out_mode
     // mode) (the positions are read from the device); KIVI plans its group
     // work from the host.  FLARE_NO_VERIFY_GRAPH (read per call): enqueue the
     // kernels directly
-    const bool graph = use_graph() && ctx->verify_graph && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr;
+    const bool graph = use_graph() && ctx->verify_graph && getenv("FLARE_NO_VERIFY_GRAPH") == nullptr &&
+                       ctx->probe_layer < 0;
     if (graph && ctx->kv_format != FL_KV_KIVI2) {
         const int key = M + 256 * out_mode;
         auto it = ctx->vgraphs.find(key);
@@ -2274,6 +2321,8 @@ int fl_verify(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, int32
     if (rc) return rc;
     std::vector<unsigned long long> keys(M);
     HIPCHK(ctx, hipMemcpyAsync(keys.data(), ctx->vslots, (size_t)M * 8, hipMemcpyDeviceToHost, st));
+    if (ctx->probe_layer >= 0 && ctx->probe_host)
+        HIPCHK(ctx, hipMemcpyAsync(ctx->probe_host, ctx->probe_dev, ctx->probe_bytes, hipMemcpyDeviceToHost, st));
     HIPCHK(ctx, hipStreamSynchronize(st));
     for (int t = 0; t < M; t++) unpack_key(keys[t], &out_tokens[t], out_vals ? &out_vals[t] : nullptr);
     return 0;

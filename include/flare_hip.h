@@ -130,17 +130,21 @@ const char *fl_backend_name(void);
 int fl_set_option(fl_ctx *ctx, int option, int value);
 
 /* Layer probe (testing surface; no reference counterpart).  With layer >= 0,
- * every following fl_decode_step / fl_decode_step_embed runs the step's
- * kernels without its captured graph and copies, as the step computes them,
- * the intermediates of that layer into host_buf (fl_probe_layout bytes,
- * kept alive by the caller): x_in, q (after RoPE), the slot's K and V rows,
- * the attention output and its Q8_0 codes / scales, x after wo, the hidden
- * vector's Q8_0 codes / scales, x after down, and the final residual.  So a
- * test can check each operation of the production step against the CPU
- * reference applied to the step's own inputs.  layer = -1 turns it off.
- * fl_probe_layout fills offsets[0..11] (byte offsets of x_in, q, k, v, attn,
- * attn scales, x_mid, h scales, x_out, x_final, attn codes, h codes) and
- * returns the total size (-1 without a model). */
+ * every following fl_decode_step / fl_decode_step_embed / fl_verify runs its
+ * kernels without a captured graph and copies, as the production kernels
+ * compute them, the intermediates of that layer into host_buf
+ * (fl_probe_layout bytes, kept alive by the caller), for up to 16 tokens:
+ * x_in, q (after RoPE), the slots' K and V rows, the attention output and
+ * its Q8_0 codes / scales, x after wo, the hidden vector's Q8_0 codes /
+ * scales, x after down (decode step), the final residual, and (verify pass)
+ * the Q8_0 codes / scales of both RMSNorm outputs the GEMMs read.  So a test
+ * can check each operation of the production path against the CPU reference
+ * applied to the path's own inputs.  layer = -1 turns it off.
+ * fl_probe_layout fills offsets[0..15] (byte offsets of the regions x_in, q,
+ * k, v, attn, attn scales, x_mid, h scales, x_out, x_final, attn codes,
+ * h codes, norm codes, norm scales, FFN-norm codes, FFN-norm scales; each
+ * region [16 tokens][size]) and returns the total size (-1 without a
+ * model). */
 int fl_probe_layer(fl_ctx *ctx, int layer, void *host_buf);
 int fl_probe_layout(const fl_ctx *ctx, size_t *offsets, int n);
 

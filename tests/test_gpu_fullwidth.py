@@ -149,3 +149,95 @@ def test_production_step_per_operation(backend, oracle, models, name, n_pos):
         assert worst[key] <= TOL, (key, worst[key])
     assert worst["h scales"] <= 2e-3
     assert asserted * 2 >= n_pos, f"only {asserted}/{n_pos} positions had a clear greedy token"
+
+
+def _codes_close(got_q, got_s, want_q, want_s, what):
+    """Q8_0 codes / scales of an RMSNorm output formed in tree order: the
+    scales within 1e-5 (one ulp of the inverse RMS), at most 0.1 % of the
+    codes one step off (values at a rounding tie), none further."""
+    assert _rel(got_s / np.where(want_s == 0, 1, want_s), np.ones_like(want_s)) <= 1e-5, what
+    d = np.abs(got_q.astype(np.int32) - want_q.astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() <= 1e-3, (what, int(d.max()), float((d > 0).mean()))
+    return int((d > 0).sum())
+
+
+@pytest.mark.timeout(900)
+def test_verify_c5_context_4096_per_operation(backend, oracle, models):
+    """C5: an 8-token speculative-verify pass (int8-MFMA GEMMs, multi-query
+    attention) at context 4096 on the Llama-3-8B width (2 layers, Q4_K, Q6_K
+    output).  Both layers' caches hold 4096 seeded rows (fl_kv_write_batch);
+    layer 1 of the pass is probed and every operation checked against the
+    oracle on the pass's own inputs; then each draft's greedy token and its
+    logit against the oracle's output projection of the pass's final
+    residual (generate.rs:244-312 verifies drafts by these tokens)."""
+    spec, model = _model(models, "c3")
+    ctx_len, M = 4096, 8
+    spec = S.replace(spec, max_seq=ctx_len + 64)
+    backend.init_gpu_kv_cache(spec, FL_KV_F16)
+    backend.upload_weights_to_gpu(model)
+    backend.reset()
+    rng = np.random.default_rng(404)
+    nkvd = spec.kv_heads * spec.head_dim
+    seeded = []
+    for layer in range(spec.layers):
+        K = (rng.standard_normal((ctx_len, nkvd)) * 0.3).astype(np.float32)
+        V = (rng.standard_normal((ctx_len, nkvd)) * 0.3).astype(np.float32)
+        backend.gpu_kv_write_batch(layer, 0, K, V)
+        seeded.append((_f16(K), _f16(V)))
+    drafts = S.random_tokens(405, M, spec.vocab)
+    print(f"[c5 verify] context {ctx_len}, {M} drafts {drafts.tolist()}", flush=True)
+    backend.probe_layer(1)
+    try:
+        got, vals = backend.verify(drafts, ctx_len)
+        P = backend.probe_read(M)
+    finally:
+        backend.probe_layer(None)
+    W = _out_matrix(oracle, model)
+    wq, wk, wv, wo, wg, wu, wd = model.layers[1]
+    D, nh, nkv, eps = spec.head_dim, spec.heads, spec.kv_heads, spec.eps
+    Kc, Vc = seeded[1]
+
+    def mv(w, q, s):
+        return oracle.matvec(w.data, w.fmt, w.rows, w.cols, np.ascontiguousarray(q), np.ascontiguousarray(s))
+
+    def norm_quant(x, nw):
+        return oracle.quantize_q8(oracle.rmsnorm(x, nw, eps))  # Q4_K layers: rmsnorm_into, then quantize
+
+    worst, flips, asserted = {}, 0, 0
+    for m in range(M):
+        pos = ctx_len + m
+        nq_, ns_ = norm_quant(P["x_in"][m], model.attn_norms[1])
+        flips += _codes_close(P["x_q"][m], P["x_s"][m], nq_, ns_, f"attention-norm codes, token {m}")
+        q = oracle.apply_rope(mv(wq, P["x_q"][m], P["x_s"][m]), nh, D, pos, spec.theta)
+        k = oracle.apply_rope(mv(wk, P["x_q"][m], P["x_s"][m]), nkv, D, pos, spec.theta)
+        v = mv(wv, P["x_q"][m], P["x_s"][m])
+        for key, g, w in (("q", P["q"][m], q), ("k", P["k"][m], _f16(k)), ("v", P["v"][m], _f16(v))):
+            worst[key] = max(worst.get(key, 0.0), _rel(g, w))
+        Kall = np.concatenate([Kc, P["k"][:m + 1]])
+        Vall = np.concatenate([Vc, P["v"][:m + 1]])
+        att = oracle.gqa_attention(P["q"][m], Kall, Vall, nh, nkv, D, pos + 1)
+        worst["attention"] = max(worst.get("attention", 0.0), _rel(P["attn"][m], att))
+        aq, as_ = oracle.quantize_q8(P["attn"][m])
+        assert np.array_equal(aq, P["attn_q"][m]) and np.array_equal(as_, P["attn_s"][m]), f"attention codes {m}"
+        worst["wo"] = max(worst.get("wo", 0.0), _rel(P["x_mid"][m], P["x_in"][m] + mv(wo, P["attn_q"][m],
+                                                                                     P["attn_s"][m])))
+        fq, fs = norm_quant(P["x_mid"][m], model.ffn_norms[1])
+        flips += _codes_close(P["f_q"][m], P["f_s"][m], fq, fs, f"FFN-norm codes, token {m}")
+        h = oracle.silu_mul(mv(wg, P["f_q"][m], P["f_s"][m]), mv(wu, P["f_q"][m], P["f_s"][m]))
+        hq, hs = oracle.quantize_q8(h)
+        flips += _codes_close(P["h_q"][m], P["h_s"][m], hq, hs, f"hidden-vector codes, token {m}")
+        worst["down"] = max(worst.get("down", 0.0), _rel(P["x_final"][m], P["x_mid"][m] + mv(wd, P["h_q"][m],
+                                                                                            P["h_s"][m])))
+        want = oracle.matvec_f32(W, oracle.rmsnorm(P["x_final"][m], model.output_norm, eps))
+        top2 = np.sort(want)[-2:]
+        worst["logit"] = max(worst.get("logit", 0.0), abs(vals[m] - want[got[m]]) / abs(top2[1]))
+        if top2[1] - top2[0] > 2e-3 * abs(top2[1]):
+            assert int(got[m]) == int(np.argmax(want)), f"draft {m}: greedy token"
+            asserted += 1
+    print(f"[c5 verify] worst relative deviation per operation: "
+          + ", ".join(f"{k} {v:.2e}" for k, v in worst.items())
+          + f"; norm / hidden codes one step off: {flips}; greedy token asserted at {asserted}/{M} drafts",
+          flush=True)
+    for key, v in worst.items():
+        assert v <= TOL, (key, v)
+    assert asserted * 2 >= M
