@@ -413,11 +413,137 @@ def run_decode(args, config: str, with_cpu: bool) -> dict:
             f"({cpu['parallel']['cores']} threads)")
     return {
         "value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4), "spec": spec, "n_prompt": n_prompt,
-        "wl": wl, "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "prefill": prefill,
+        "wl": wl, "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "prefill": prefill, "model": model,
         "decode_weight_roofline": {"bytes_per_token": bytes_per_token,
                                    "achieved_GB_s": round(bytes_per_token * tok_s / 1e9, 1),
                                    "frac": round(bytes_per_token * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
     }
+
+
+def run_exact(args, config: str, model=None) -> dict:
+    """The same decode workload in the reference-order mode (FL_OPT_EXACT:
+    logits bit-identical to the CPU reference's): the prompt through exact
+    decode steps (untimed), then args.steps steps timed with HIP events."""
+    import torch
+
+    from flarellm_amd import FL_KV_F16
+    from flarellm_amd import _lib as L
+    from flarellm_amd import synth as S
+    from flarellm_amd.backend import HipBackend
+
+    wl = WORKLOADS[config]
+    spec = S.CONFIGS[wl["spec"]]
+    n_prompt = wl["prompt"] if args.prompt is None else max(1, args.prompt)
+    need = n_prompt + args.warmup + args.steps
+    if need > spec.max_seq:
+        spec = S.replace(spec, max_seq=need)
+    if model is None or model.spec != spec:
+        model = S.make_model(spec, seed=1)
+    b = HipBackend(0)
+    b.init_gpu_kv_cache(spec, FL_KV_F16)
+    b.upload_weights_to_gpu(model)
+    b.set_option(L.FL_OPT_EXACT, 1)
+    stream = torch.cuda.ExternalStream(b.stream)
+    t0 = time.time()
+    b.generate(S.random_tokens(7, n_prompt, spec.vocab), 1)
+    b.decode_continue(args.warmup)
+    b.sync()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    b.decode_continue(args.steps)
+    ev1.record(stream)
+    b.sync()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    toks = b.read_tokens(n_prompt, 8)
+    b.close()
+    log(f"[bench {config} exact] {args.steps} steps: {1000.0 / ms:.1f} tok/s ({ms:.4f} ms/token; prompt "
+        f"{time.time() - t0:.1f}s); first tokens {toks.tolist()}")
+    return {"value": round(1000.0 / ms, 2), "unit": "tok/s", "ms_per_step": round(ms, 4), "steps": args.steps,
+            "context": n_prompt,
+            "mode": "FL_OPT_EXACT: logits bit-identical to the x86 reference's (reference summation order)"}
+
+
+def c4_128k(args) -> dict:
+    """BASELINE configs[3] at its longest context only (the default line's
+    extra_configs): the decode attention kernel over 128k cached tokens in the
+    three cache forms, from HBM (>= 1 GB of K+V rotated across layers)."""
+    import numpy as np
+    import torch
+
+    from flarellm_amd import FL_KV_F16, FL_KV_KIVI2, FL_KV_Q8
+    from flarellm_amd import synth as S
+    from flarellm_amd.backend import HipBackend
+
+    base = S.CONFIGS["Llama-3-8B"]
+    nh, nkv, hd = base.heads, base.kv_heads, base.head_dim
+    T = 131072
+    rng = np.random.default_rng(3)
+    rows_k = rng.standard_normal((T, nkv * hd), dtype=np.float32)
+    rows_v = rng.standard_normal((T, nkv * hd), dtype=np.float32)
+    q = rng.standard_normal(nh * hd, dtype=np.float32)
+    b = HipBackend(0)
+    stream = torch.cuda.ExternalStream(b.stream)
+    out = {}
+    for name, fmt in (("f16", FL_KV_F16), ("q8", FL_KV_Q8), ("kivi2", FL_KV_KIVI2)):
+        spec = S.replace(base, layers=1, max_seq=T)
+        b.init_gpu_kv_cache(spec, fmt)
+        nbytes = b.bench_attention(T, 0)
+        L = int(min(256, max(2, -(-1.0e9 // nbytes))))
+        b.init_gpu_kv_cache(S.replace(base, layers=L, max_seq=T), fmt)
+        for layer in range(L):
+            b.gpu_kv_write_batch(layer, 0, rows_k, rows_v)
+        b.grouped_query_attention_from_gpu_cache(q, 0, T)
+        b.bench_attention(T, 3)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        nbytes = b.bench_attention(T, args.kernel_iters)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / args.kernel_iters
+        out[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"[bench c4 128k] {name:6s} {us:8.2f} us  {nbytes / 1e6:8.2f} MB  {nbytes / us / 1e3:7.1f} GB/s")
+    b.close()
+    return {"workload": "decode attention alone, Llama-3-8B heads, 131072 cached tokens", "unit": "us per launch",
+            "cases": out}
+
+
+def c5_verify(args, model) -> dict:
+    """one 8-draft verify pass at context 4096 on the
+    Llama-3-8B model (the prompt through fl_prefill, untimed); ms per pass
+    timed with HIP events over repeated passes at the same positions."""
+    import torch
+
+    from flarellm_amd import FL_KV_F16
+    from flarellm_amd import synth as S
+    from flarellm_amd.backend import HipBackend
+
+    spec = model.spec
+    n_prompt, k = 4096, 8
+    b = HipBackend(0)
+    b.init_gpu_kv_cache(spec, FL_KV_F16)
+    b.upload_weights_to_gpu(model)
+    b.forward_prefill(S.random_tokens(7, n_prompt, spec.vocab), logits=False)
+    drafts = S.random_tokens(9, k, spec.vocab)
+    for _ in range(3):
+        b.verify(drafts, n_prompt)
+    stream = torch.cuda.ExternalStream(b.stream)
+    torch.cuda.synchronize()
+    n = 16
+    t1 = time.perf_counter()
+    for _ in range(n):
+        b.verify(drafts, n_prompt)
+    ms = (time.perf_counter() - t1) * 1000.0 / n
+    b.close()
+    log(f"[bench c5] verify pass of {k} drafts at context {n_prompt}: {ms:.3f} ms ({k * 1000.0 / ms:.0f} drafts/s)")
+    return {"workload": WORKLOADS["c5"]["desc"], "ms_per_pass": round(ms, 4), "unit": "drafts/s",
+            "value": round(k * 1000.0 / ms, 1), "passes": n,
+            "weight_roofline_frac": round(spec.weight_bytes_per_token() / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "timing": "host wall clock per fl_verify call (each call synchronizes for the 8 tokens)"}
 
 
 def main() -> int:
@@ -429,6 +555,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-c3", action="store_true",
                     help="default run: skip the Llama-3-8B (C3) decode line reported under extra_configs")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="default run: skip the exact-mode, C4 128k and C5 lines under extra_configs")
     ap.add_argument("--cpu-tokens", type=int, default=40)
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--prompt", type=int, default=None,
@@ -469,12 +597,19 @@ def main() -> int:
         "kernels": r["kernels"],
     }
     if args.config == "c2" and not args.no_c3 and args.prompt is None:
-        # the north-star shape, driver-timed in the same run
+        # the north-star shape and the other BASELINE configs, driver-timed in
+        # the same run
         c3 = run_decode(args, "c3", False)
-        out["extra_configs"] = {"c3": {
+        extra = {"c3": {
             "workload": c3["wl"]["desc"], "value": c3["value"], "unit": "tok/s", "ms_per_step": c3["ms_per_step"],
             "steps": args.steps, "decode_weight_roofline": c3["decode_weight_roofline"],
             "roofline": c3["roofline"], "prefill": c3["prefill"], "kernels": c3["kernels"]}}
+        if not args.no_extra:
+            extra["c2_exact"] = run_exact(args, "c2")
+            extra["c3_exact"] = run_exact(args, "c3", c3["model"])
+            extra["c4_128k"] = c4_128k(args)
+            extra["c5"] = c5_verify(args, c3["model"])
+        out["extra_configs"] = extra
     print(json.dumps(out), flush=True)
     return 0
 

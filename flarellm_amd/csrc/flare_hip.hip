@@ -1502,8 +1502,11 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
 
 // FLARE_NO_GRAPH=1: enqueue the step's kernels directly instead of replaying a
 // HIP graph (identical kernels; for profilers that cannot follow graphs).
+// Graphs are also off under rocprofv3 counter collection (it sets
+// ROCPROF_COUNTER_COLLECTION): the one counter run that replayed graphs
+// died with a SIGSEGV in a profiler-side thread at the first capture.
 static bool use_graph() {
-    static const bool g = getenv("FLARE_NO_GRAPH") == nullptr;
+    static const bool g = getenv("FLARE_NO_GRAPH") == nullptr && getenv("ROCPROF_COUNTER_COLLECTION") == nullptr;
     return g;
 }
 
