@@ -70,8 +70,8 @@ hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a) {
     // read measured slower, 452 against 515 ms before other changes), 4 x 2 for
     // up to 8 queries (the verify batches keep k_attm, which measured faster).
     // FLARE_ATTQ_BW / FLARE_ATTQ_PBW: 1 or 2 (measurement switches)
-    static const int bwe = getenv("FLARE_ATTQ_BW") ? atoi(getenv("FLARE_ATTQ_BW")) : 2;
-    static const int pbw = getenv("FLARE_ATTQ_PBW") ? atoi(getenv("FLARE_ATTQ_PBW")) : 2;
+    static const int bwe = measure_env("FLARE_ATTQ_BW") ? atoi(measure_env("FLARE_ATTQ_BW")) : 2;
+    static const int pbw = measure_env("FLARE_ATTQ_PBW") ? atoi(measure_env("FLARE_ATTQ_PBW")) : 2;
     const int NPW = npairs <= 4 ? 4 : 8, BW = npairs <= 4 ? (bwe == 1 ? 1 : 2) : (pbw == 1 ? 1 : 2);
     const dim3 grid(a.nsplit, a.nkv, (npairs + NPW - 1) / NPW);
 #define C(DD, GG)                                                                                     \

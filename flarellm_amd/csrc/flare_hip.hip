@@ -535,7 +535,7 @@ static int launch_q8in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const 
 // streaming kernel keeps more bytes in flight per wave).
 static int launch_f32in(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x,
                         const float *nw, float eps, float *out, unsigned long long *slot, int M = 1) {
-    if ((w.format == FL_Q6K || w.format == FL_Q8_0) && (M > 1 || getenv("FLARE_MVO_SINGLE"))) {
+    if ((w.format == FL_Q6K || w.format == FL_Q8_0) && (M > 1 || measure_env("FLARE_MVO_SINGLE"))) {
         MvoArgs a{};
         a.W = w.desc();
         a.x = x;
@@ -676,7 +676,7 @@ int fl_ctx_create(int device, fl_ctx **out) {
         fl_ctx_destroy(c);
         return fail(nullptr, FL_E_HIP, "scratch array address: %s", hipGetErrorString(e));
     }
-    c->verify_fuse = getenv("FLARE_NO_VFUSE") == nullptr;  // initial value of FL_OPT_VERIFY_FUSE
+    c->verify_fuse = measure_env("FLARE_NO_VFUSE") == nullptr;  // initial value of FL_OPT_VERIFY_FUSE
     *out = c;
     return 0;
 }
@@ -1025,11 +1025,11 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         // fp16 44 -> 32 / 109 -> 99 us, Q8 49 -> 32 / 100 -> 88 us).
         ctx->attn_waves = c.head_dim <= 64 ? 4 : 8;
         ctx->single = 0;
-        if (const char *ev = getenv("FLARE_ATTN_WAVES")) ctx->attn_waves = atoi(ev) == 4 ? 4 : 8;  // tuning override
+        if (const char *ev = measure_env("FLARE_ATTN_WAVES")) ctx->attn_waves = atoi(ev) == 4 ? 4 : 8;  // tuning override
         const int pass = kAttmBlock * ctx->attn_waves;  // tokens of one block per wave
         ctx->chmin = pass;
-        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(pass, atoi(ev) / pass * pass);
-        if (const char *ev = getenv("FLARE_ATTN_SINGLE")) ctx->single = std::max(0, atoi(ev));  // tuning override
+        if (const char *ev = measure_env("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(pass, atoi(ev) / pass * pass);
+        if (const char *ev = measure_env("FLARE_ATTN_SINGLE")) ctx->single = std::max(0, atoi(ev));  // tuning override
         int ncu = 0, dev = 0;
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
@@ -1039,9 +1039,9 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
         ctx->nsplit = std::max(1, std::min({kAttmMaxSplit, fit, (c.max_seq_len + ctx->chmin - 1) / ctx->chmin}));
     } else {
         choose_splits(c.max_seq_len, c.num_kv_heads, c.head_dim, ctx->nsplit, ctx->chmin);
-        if (const char *ev = getenv("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
+        if (const char *ev = measure_env("FLARE_ATTN_CHMIN")) ctx->chmin = std::max(1, atoi(ev));  // tuning override
     }
-    if (const char *ev = getenv("FLARE_ATTN_NSPLIT")) {  // tuning override
+    if (const char *ev = measure_env("FLARE_ATTN_NSPLIT")) {  // tuning override
         const int ns = atoi(ev);
         if (ns > 0 && ns <= (kv_format != FL_KV_F32 ? kAttmMaxSplit : kAttnMaxSplit))
             ctx->nsplit = ns;
@@ -1836,7 +1836,7 @@ static int verify_split(const fl_weight &w, int M, int &chunk) {
     const int units = w.format == FL_Q4K ? w.cols / 256 : w.cols / 32;
     const int ubytes = w.format == FL_Q4K ? 256 : 32;
     const int maxks = M > kVerifyMaxTokens ? kPrefillMaxKsplit : kVerifyMaxKsplit;
-    static const int target = getenv("FLARE_VG_WAVES") ? atoi(getenv("FLARE_VG_WAVES")) : 2048;  // tuning
+    static const int target = measure_env("FLARE_VG_WAVES") ? atoi(measure_env("FLARE_VG_WAVES")) : 2048;  // tuning
     const int want = std::max(1, std::min({units, maxks, (target + tiles - 1) / tiles}));
     if (M > kVerifyMaxTokens && w.cols % 256 == 0) {
         // the prefill kernel walks 256-value steps: chunk counts steps
@@ -2117,7 +2117,7 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         // 4k on MI355X, unpaired: 33 vs 40 us per layer, one split per query 47 us;
         // paired: M/2 measured best against 1, 2, 6 and 8)
         // query pairs share each K/V block (fp16 / Q8, G <= 4, even M)
-        static const bool no_pair = getenv("FLARE_NO_QPAIR") != nullptr;  // measurement switch
+        static const bool no_pair = measure_env("FLARE_NO_QPAIR") != nullptr;  // measurement switch
         a.qpair = !no_pair && M % 2 == 0 && (G == 1 || G == 2 || G == 4) &&
                   (ctx->kv_format == FL_KV_F16 || ctx->kv_format == FL_KV_Q8);
         a.chmin = ctx->chmin * (a.qpair ? M / 2 : M);
@@ -2135,15 +2135,15 @@ static int enqueue_verify(fl_ctx *ctx, int M, int pos0, bool dev_pos, int out_mo
         a.ostride = qd;
         // fp16 caches, even M: the query pairs of a group share each staged
         // K/V block (k_attq), so the pass reads the cache once per group
-        static const bool no_attq = getenv("FLARE_NO_ATTQ") != nullptr;  // measurement switch
-        static const int attq_chmin = getenv("FLARE_ATTQ_CHMIN") ? std::max(32, atoi(getenv("FLARE_ATTQ_CHMIN"))) : 64;
+        static const bool no_attq = measure_env("FLARE_NO_ATTQ") != nullptr;  // measurement switch
+        static const int attq_chmin = measure_env("FLARE_ATTQ_CHMIN") ? std::max(32, atoi(measure_env("FLARE_ATTQ_CHMIN"))) : 64;
         // (prefill passes; the verify batches of up to 8 tokens keep k_attm's
         // query pairs, which measured faster at 8 tokens)
-        static const bool attq_verify = getenv("FLARE_ATTQ_VERIFY") != nullptr;  // measurement switch
+        static const bool attq_verify = measure_env("FLARE_ATTQ_VERIFY") != nullptr;  // measurement switch
         if (!no_attq && a.qpair && (M > kVerifyMaxTokens || attq_verify) && ctx->kv_format == FL_KV_F16 &&
             (D == 64 || D == 128)) {
             // splits: about one workgroup per CU over (kv heads x pair groups)
-            static const int attq_ns = getenv("FLARE_ATTQ_NSPLIT") ? atoi(getenv("FLARE_ATTQ_NSPLIT")) : 0;
+            static const int attq_ns = measure_env("FLARE_ATTQ_NSPLIT") ? atoi(measure_env("FLARE_ATTQ_NSPLIT")) : 0;
             const int per_wg = M / 2 <= 4 ? 4 : 8;  // pairs per workgroup (launch_attq)
             const int groups = (M / 2 + per_wg - 1) / per_wg;
             int ns = attq_ns > 0 ? attq_ns : ctx->ncu / (c.num_kv_heads * groups);
@@ -2349,8 +2349,8 @@ int fl_prefill(fl_ctx *ctx, const uint32_t *tokens, int n_tokens, int pos0, floa
     }
     hipStream_t st = ctx->stream;
     // FLARE_PREFILL_TOKENS: pass size (measurement switch; 1..64)
-    static const int C = getenv("FLARE_PREFILL_TOKENS")
-                             ? std::max(1, std::min(kPrefillTokens, atoi(getenv("FLARE_PREFILL_TOKENS"))))
+    static const int C = measure_env("FLARE_PREFILL_TOKENS")
+                             ? std::max(1, std::min(kPrefillTokens, atoi(measure_env("FLARE_PREFILL_TOKENS"))))
                              : kPrefillTokens;
     const int nchunks = (n_tokens + C - 1) / C;
     // host copies stay alive until the final synchronisation
@@ -2549,7 +2549,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         }
         if (rc) return rc;
     }
-    if (which <= 4 && getenv("FLARE_MV_TRACE_PRINT")) {
+    if (which <= 4 && measure_env("FLARE_MV_TRACE_PRINT")) {
         // workgroup 0 phases, then the spread of workgroup start / end times
         std::vector<long long> tr(64 + 3072, 0);
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
@@ -2569,7 +2569,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         }
         if (n) fprintf(stderr, " | %d wgs: starts %lld..%lld ends %lld..%lld", n, s0 - tr[0], s1 - tr[0], e0 - tr[0], e1 - tr[0]);
         fprintf(stderr, "\n");
-        if (const char *dump = getenv("FLARE_MV_TRACE_DUMP")) {
+        if (const char *dump = measure_env("FLARE_MV_TRACE_DUMP")) {
             // raw per-workgroup (start, end) ticks, one line per launch
             if (FILE *f = fopen(dump, "a")) {
                 fprintf(f, "%d", which);
@@ -2581,7 +2581,7 @@ int fl_bench_layer_kernel(fl_ctx *ctx, int which, int first_layer, int iters, do
         }
         HIPCHK(ctx, hipMemset(ctx->bench_trace, 0, tr.size() * 8));
     }
-    if (which == 5 && getenv("FLARE_ATTN_TRACE_PRINT")) {
+    if (which == 5 && measure_env("FLARE_ATTN_TRACE_PRINT")) {
         long long tr[24] = {0};
         HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
         HIPCHK(ctx, hipMemcpy(tr, ctx->bench_trace, sizeof tr, hipMemcpyDeviceToHost));

@@ -15,8 +15,21 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace fl {
+
+// Measurement switches (tile shapes, split counts, rejected kernel variants,
+// trace dumps) are read from the environment in FLARE_MEASURE builds only; the
+// product library ignores them and runs the measured defaults.
+inline const char *measure_env(const char *name) {
+#ifdef FLARE_MEASURE
+    return getenv(name);
+#else
+    (void)name;
+    return nullptr;
+#endif
+}
 
 constexpr int kThreads = 256;  // 4 wave64 per workgroup
 
@@ -180,10 +193,28 @@ __device__ __forceinline__ float fl_expf(float x) {
 //     counts with an acq_rel RMW, the last workgroup's waves acquire at agent
 //     scope before loading (an L2 writeback + invalidate on gfx950).
 //   0: barrier, thread 0's acq_rel RMW only.
-// (2 and 0 are measurement builds.)
+// (2 and 0 exist in FLARE_MEASURE builds only.)
+// Why 1 is sufficient on gfx950.  The partials are written with agent-scope
+// atomic stores, which carry the device scope bits (sc1): they are written
+// through to the device's point of coherence (past the per-XCD L2s), and a
+// store is acknowledged -- vmcnt decremented -- only once it is there.  The
+// s_waitcnt 0 of every wave therefore means all its partials are visible
+// device-wide before the barrier, and thread 0's counting RMW is issued
+// after the barrier.  The last arriver issues its loads after that RMW has
+// returned (the flag passes through LDS and a barrier), and they are
+// agent-scope atomic loads, which read from the point of coherence rather
+// than a possibly stale L2 line.  A release fence would add an L2 writeback
+// of non-atomic data (there is none) and an acquire fence an L2 invalidate
+// for non-atomic loads (there are none): the measured 3.41 vs 4.83 ms per
+// C5 verify pass is that extra cache maintenance.  The split-merge tests
+// (bit-repeatable over 20 launches, forced splits, every verify test) run
+// on this form.
 // ------------------------------------------------------------------------
 #ifndef FLARE_SPLIT_SYNC
 #define FLARE_SPLIT_SYNC 1
+#endif
+#if FLARE_SPLIT_SYNC != 1 && !defined(FLARE_MEASURE)
+#error "FLARE_SPLIT_SYNC variants other than 1 are measurement builds (define FLARE_MEASURE)"
 #endif
 template <bool RESET>
 __device__ __forceinline__ bool split_arrive_last(int *counter, int n, int *flag) {

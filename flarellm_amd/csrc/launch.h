@@ -74,9 +74,9 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = fa
     // tuning overrides for the Q8-input kernels (experiments): FLARE_MVS_R /
     // FLARE_MVS_SU / FLARE_MVS_GRID
     // (FLARE_MVF_R / FLARE_MVF_SU for the f32-input kernels)
-    const char *er = getenv(f32in ? "FLARE_MVF_R" : pairs ? "FLARE_QKV_R" : "FLARE_MVS_R");
+    const char *er = measure_env(f32in ? "FLARE_MVF_R" : pairs ? "FLARE_QKV_R" : "FLARE_MVS_R");
     if (er) p.r = atoi(er);
-    if (const char *e = getenv(f32in ? "FLARE_MVF_SU" : pairs ? "FLARE_QKV_SU" : "FLARE_MVS_SU")) p.su = atoi(e);
+    if (const char *e = measure_env(f32in ? "FLARE_MVF_SU" : pairs ? "FLARE_QKV_SU" : "FLARE_MVS_SU")) p.su = atoi(e);
     // fill the chip: halve the rows per group while fewer than 256
     // workgroups (4 waves, one group each) would run; not for the fused QKV,
     // whose waves each normalise the activation (4 rows x 2 KiB measured
@@ -84,9 +84,9 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = fa
     while (p.r > 2 && (rows + p.r - 1) / p.r < 4 * 256 && !er && !pairs) p.r /= 2;
     const int ngrp = (rows + p.r - 1) / std::max(1, p.r);
     p.grid = std::max(1, std::min((ngrp + 3) / 4, 1024));
-    if (const char *e = getenv("FLARE_MVS_GRID")) p.grid = std::max(1, std::min(p.grid, atoi(e)));
+    if (const char *e = measure_env("FLARE_MVS_GRID")) p.grid = std::max(1, std::min(p.grid, atoi(e)));
     p.lds = mvs_lds_bytes(f32in, cols);
-    if (const char *e = getenv("FLARE_MVS_LDSPAD")) p.lds += (size_t)atoi(e);  // placement experiments
+    if (const char *e = measure_env("FLARE_MVS_LDSPAD")) p.lds += (size_t)atoi(e);  // placement experiments
     return p;
 }
 
@@ -101,8 +101,8 @@ inline MvsPlan mvs_gu_plan(int fmt, int F, int cols) {
     p.r = 8;
     p.su = (fmt == F_Q8_0 && mvs_steps(fmt, cols) >= 2) ? 2 : 1;
     // tuning overrides (experiments): FLARE_GU_NW / FLARE_GU_SU
-    if (const char *e = getenv("FLARE_GU_NW")) p.r = atoi(e);
-    if (const char *e = getenv("FLARE_GU_SU")) p.su = atoi(e);
+    if (const char *e = measure_env("FLARE_GU_NW")) p.r = atoi(e);
+    if (const char *e = measure_env("FLARE_GU_SU")) p.su = atoi(e);
     p.grid = std::max(1, std::min(nblk, 1024));
     p.lds = mvs_lds_bytes(false, cols) + 32 * 4;
     return p;

@@ -28,7 +28,7 @@ hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
     }
     // pre-quantized input whose row fits one unit: the lane's activation runs
     // in registers (RegX4L, no LDS staging or workgroup barrier)
-    static const bool noregx = getenv("FLARE_NO_REGX") != nullptr;
+    static const bool noregx = measure_env("FLARE_NO_REGX") != nullptr;
     if (!noregx && a.pro == PRO_LOADQ && mvs_steps(F_Q4K, a.W.cols) <= p.su) {
 #define CR(RR, SS)                                                                                        \
     if (p.r == RR && p.su == SS) {                                                                        \

@@ -17,7 +17,7 @@ namespace fl {
 // in registers (RegX8, no workgroup barrier).
 // 1: norm prologue (RegX8), 2: pre-quantized input (RegX8L), 0: LDS staging
 static int use_regx(const MvsPlan &p, const MvsArgs &a) {
-    static const bool off = getenv("FLARE_NO_REGX") != nullptr;
+    static const bool off = measure_env("FLARE_NO_REGX") != nullptr;
     if (off || mvs_steps(F_Q8_0, a.W.cols) > p.su) return 0;
     if (a.pro == PRO_NORMQ0 || a.pro == PRO_NORMQ1) return 1;
     return a.pro == PRO_LOADQ ? 2 : 0;

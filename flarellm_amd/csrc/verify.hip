@@ -12,10 +12,10 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     if (a.M > kVerifyMaxTokens && a.W.cols % 256 == 0 && !a.post) {
         // prefill batches: activations staged per 256-value step (chunk = steps)
         // Q4_K: the f16-MFMA form (FLARE_PGEMM_I8: the int8 one, a measurement switch)
-        static const bool i8 = getenv("FLARE_PGEMM_I8") != nullptr;
+        static const bool i8 = measure_env("FLARE_PGEMM_I8") != nullptr;
         if (fmt == F_Q4K && !i8) {
             const dim3 gh((tiles + 7) / 8, a.ksplit);
-            static const bool db = getenv("FLARE_PGEMM_DB") != nullptr;  // measurement switch
+            static const bool db = measure_env("FLARE_PGEMM_DB") != nullptr;  // measurement switch
             if (db) hipLaunchKernelGGL((k_pgemm_h<8, 2>), gh, dim3(512), 0, st, a);
             else hipLaunchKernelGGL((k_pgemm_h<8, 1>), gh, dim3(512), 0, st, a);
         } else if (fmt == F_Q4K) hipLaunchKernelGGL(k_pgemm<F_Q4K>, grid, dim3(256), 0, st, a);
