@@ -117,6 +117,7 @@ SIGNATURES = {
     "fl_kv_write_batch": (i32, [vp, i32, i32, i32, vp, vp]),
     "fl_gqa_from_cache": (i32, [vp, i32, vp, i32, vp]),
     "fl_probe_layer": (i32, [vp, i32, vp]),
+    "fl_op_batched_block_dots": (i32, [vp, vp, i32, vp, vp, vp, vp]),
     "fl_probe_layout": (i32, [vp, C.POINTER(C.c_size_t), i32]),
     "fl_bench_attention": (i32, [vp, i32, i32, C.POINTER(C.c_double)]),
     "fl_decode_step": (i32, [vp, C.c_uint32, i32, vp, C.POINTER(C.c_int32), C.POINTER(f32)]),

@@ -148,6 +148,19 @@ class HipBackend:
               self.ctx)
         return out
 
+    def batched_block_dots(self, w: Weight, q, s, su):
+        """Per-block integer dots of the batched GEMM (fl_op_batched_block_dots):
+        [n_tokens, rows, K/32] int32."""
+        import torch
+
+        M = q.shape[0]
+        out = torch.empty((M, w.rows, q.shape[1] // 32), dtype=torch.int32, device=q.device)
+        self._torch_sync()
+        check(self.lib.fl_op_batched_block_dots(self.ctx, w.handle, M, _ptr(q), _ptr(s), _ptr(su), _ptr(out)),
+              self.ctx)
+        self.sync()
+        return out
+
     def batched_matvec_f32in(self, w: Weight, x):
         """f32-input matvec for n rows x [n, cols] (Q6_K / Q8_0) -> [n, rows]."""
         import torch

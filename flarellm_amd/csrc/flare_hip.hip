@@ -1906,6 +1906,34 @@ int fl_op_batched_matvec_q8in(fl_ctx *ctx, const fl_weight *w, int n_tokens, con
     return 0;
 }
 
+int fl_op_batched_block_dots(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q, const float *scales,
+                             const int32_t *sums, int32_t *dots) {
+    if (!ctx || !w || !q || !scales || !sums || !dots) return fail(ctx, FL_E_INVALID, "null argument");
+    if (n_tokens < 1 || n_tokens > kPrefillTokens)
+        return fail(ctx, FL_E_INVALID, "batch of %d tokens (1..%d)", n_tokens, kPrefillTokens);
+    if (w->format != FL_Q8_0 && w->format != FL_Q4K) return fail(ctx, FL_E_UNSUPPORTED, "format %d", w->format);
+    int chunk = 0;
+    const int ks = verify_split(*w, n_tokens, chunk);
+    float *part = nullptr;
+    ALLOC(ctx, part, (size_t)ks * n_tokens * w->rows * 4);
+    VgArgs a{};
+    a.W = w->desc();
+    a.xq = q;
+    a.xs = scales;
+    a.xsum = sums;
+    a.M = n_tokens;
+    a.ksplit = ks;
+    a.chunk = chunk;
+    a.part = part;
+    a.dots = dots;
+    const hipError_t e = launch_vgemm(w->format, ctx->stream, a);
+    const hipError_t e2 = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(part);
+    HIPCHK(ctx, e);
+    HIPCHK(ctx, e2);
+    return 0;
+}
+
 int fl_op_batched_matvec_q8in_noalloc(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q,
                                       const float *scales, const int32_t *sums, float *out) {
     if (!ctx || !w || !q || !scales || !sums || !out) return fail(ctx, FL_E_INVALID, "null argument");

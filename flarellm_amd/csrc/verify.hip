@@ -11,9 +11,12 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     const int nt = (a.M + 15) / 16;  // token tiles of the M > 8 kernels
     if (a.M > kVerifyMaxTokens && a.W.cols % 256 == 0 && !a.post) {
         // prefill batches: activations staged per 256-value step (chunk = steps)
-        // Q4_K: the f16-MFMA form (FLARE_PGEMM_I8: the int8 one, a measurement switch)
-        static const bool i8 = measure_env("FLARE_PGEMM_I8") != nullptr;
-        if (fmt == F_Q4K && !i8) {
+        // Q4_K: the int8-MFMA form, whose MFMAs form the reference's exact
+        // per-block integer dots (FLARE_PGEMM_H: the f16-MFMA form, 3.5 %
+        // faster on the C3 prefill but with no integer dots; a measurement
+        // switch)
+        static const bool f16 = measure_env("FLARE_PGEMM_H") != nullptr;
+        if (fmt == F_Q4K && f16 && !a.dots) {
             const dim3 gh((tiles + 7) / 8, a.ksplit);
             static const bool db = measure_env("FLARE_PGEMM_DB") != nullptr;  // measurement switch
             if (db) hipLaunchKernelGGL((k_pgemm_h<8, 2>), gh, dim3(512), 0, st, a);

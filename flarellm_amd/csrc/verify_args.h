@@ -23,6 +23,8 @@ struct VgArgs {
     int ksplit;       // K chunks (grid y)
     int chunk;        // units (Q8_0 blocks / Q4_K super-blocks) per K chunk; ksplit = ceil(units / chunk)
     float *part;      // [ksplit][M][rows] fp32 partial sums
+    int *dots;        // testing (nullptr otherwise): the per-block integer dots the MFMAs form,
+                      // [M][rows][K/32] (Q4_K: block 8*sb + j = sub-block j of super-block sb)
     // k_vgemm_q4k8 only (rows % 64 == 0): the last-arriving K split of each
     // workgroup column sums the partials of its 64 rows and applies
     // post 1 = SiLU(gate)*up + Q8_0 (gate/up weight; a column holds 32 gate

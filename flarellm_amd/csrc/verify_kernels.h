@@ -73,6 +73,11 @@ __device__ __forceinline__ v4i32_t vg_mfma(i64x1_t a, i64x1_t b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
+// Testing readback of one per-block integer dot (VgArgs::dots).
+__device__ __forceinline__ void vg_dot_out(const VgArgs &a, int t, int n, int blk, int v) {
+    if (t < a.M && n < a.W.rows) a.dots[((size_t)t * a.W.rows + n) * (a.W.cols >> 5) + blk] = v;
+}
+
 // Q8_0 weights: unit = one 32-block.  Block term of matvec_q8_0_preq_into
 // (model.rs:8082-8099): (f16(w_scale) * x_scale) * (int dot as f32).
 // NT token tiles of 16 (M <= 16 NT): each weight fragment feeds NT MFMAs.
@@ -119,6 +124,9 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_0(VgArgs a) {
             const int tx = tA + 16 * tt;
             const i64x1_t x = tx < a.M ? *(const i64x1_t *)(lx + tx * xst + 32 * bl + 8 * kg) : 0;
             const v4i32_t d = vg_mfma(x, wcur);
+            if (a.dots)
+#pragma unroll
+                for (int i = 0; i < 4; i++) vg_dot_out(a, 16 * tt + 4 * kg + i, n, b, d[i]);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * tt + 4 * kg + i;
@@ -200,6 +208,9 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
                 const int tx = tA + 16 * tt;
                 const i64x1_t x = tx < a.M ? *(const i64x1_t *)(lx + tx * xst + sl * 256 + 32 * j + 8 * kg) : 0;
                 const v4i32_t dd = vg_mfma(x, wb);
+                if (a.dots)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) vg_dot_out(a, 16 * tt + 4 * kg + i, n, sb * 8 + j, dd[i]);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int t = 16 * tt + 4 * kg + i;
@@ -374,6 +385,11 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++)
                     dd[tt] = vg_mfma(*(const i64x1_t *)(bx + (tA + 16 * tt) * kPgStride + 32 * j + 8 * kg), wb);
+                if (a.dots)
+#pragma unroll
+                    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) vg_dot_out(a, 16 * tt + 4 * kg + i, n, st * 8 + j, dd[tt][i]);
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
                     const int t0 = 16 * tt + 4 * kg;  // tokens t0 .. t0+3 of this lane
@@ -677,6 +693,12 @@ __global__ __launch_bounds__(256) void k_vgemm_q8_08(VgArgs a) {
             const i64x1_t x2 = ((i64x1_t)(uint32_t)xv.w << 32) | (uint32_t)xv.z;
             dd[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x2, w2, vg_mfma(x1, w1), 0, 0, 0);
         }
+        if (a.dots)
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (g0 + 2 * p + hi < b1) vg_dot_out(a, 4 * h + e, n, g0 + 2 * p + hi, dd[p][e]);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int bb = g0 + 2 * p + hi;
@@ -778,6 +800,11 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k8(VgArgs a) {
             const i64x1_t x2 = ((i64x1_t)(uint32_t)xv.w << 32) | (uint32_t)xv.z;
             dd[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x2, w2, vg_mfma(x1, w1), 0, 0, 0);
         }
+        if (a.dots)
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) vg_dot_out(a, 4 * h + e, n, sb * 8 + p + 4 * hi, dd[p][e]);
         const uint32_t h0 = (uint32_t)hh.x;
         const float d = h2f((uint16_t)(h0 & 0xFFFF)), dmin = h2f((uint16_t)(h0 >> 16));
         // unpack_q4k_scales (model.rs:8709-8719), flare packing: the 6-bit

@@ -191,6 +191,16 @@ int fl_op_batched_dequant_matmul(fl_ctx *ctx, const fl_weight *w, const float *i
  * Synchronises. */
 int fl_op_prefill_attention(fl_ctx *ctx, const float *q, const float *k, const float *v, int seq_len,
                             int num_heads, int num_kv_heads, int head_dim, float *out);
+/* The per-block integer dot products of the batched quantized GEMMs above
+ * (the same kernels, K split and launches as fl_op_batched_matvec_q8in),
+ * read back from the MFMA results: dots[t][row][b] for token t and 32-value
+ * block b (Q4_K: b = 8 * super-block + sub-block, sub-blocks 4-7 the high
+ * nibbles).  The integer part of batched_dequant_matmul's per-token
+ * matvec_q8_0_preq_into / matvec_q4k_q8_into (model.rs:8082-8099, 8997-9014);
+ * the parity surface of the verify and prefill GEMMs.  dots: device memory,
+ * n_tokens * rows * K/32 int32. */
+int fl_op_batched_block_dots(fl_ctx *ctx, const fl_weight *w, int n_tokens, const int8_t *q, const float *scales,
+                             const int32_t *sums, int32_t *dots);
 /* fl_op_batched_matvec_q8in without any allocation: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same

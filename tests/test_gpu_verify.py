@@ -1,8 +1,11 @@
 """Speculative verify (BASELINE config 5's pass) on the GPU.
 
 * fl_op_batched_matvec_q8in: every token row of the int8-MFMA GEMM equals the
-  oracle's single-token quantized matvec within 1e-3 relative (the per-block
-  integer dots are exact; only the fp32 order of the block terms differs).
+  oracle's single-token quantized matvec within 1e-3 relative (only the fp32
+  order of the block terms differs);
+* fl_op_batched_block_dots: the per-block integer dots those GEMMs' MFMAs
+  form equal the oracle's bit for bit, at the C3 / C5 shapes for M = 8
+  (verify) and 64 (prefill).
 * fl_verify: the greedy token after each of M drafts equals what sequential
   decode gives -- the GPU's own fl_decode_step loop and the oracle -- wherever
   the oracle's top-2 logit gap is not a near-tie.
@@ -40,6 +43,40 @@ GEMM_SHAPES = [(FL_Q8_0, 96, 256, 1), (FL_Q8_0, 1001, 2048, 8), (FL_Q8_0, 64, 57
                # prefill batches (17..64 tokens): 256-value steps staged through LDS
                (FL_Q8_0, 3072, 2048, 64), (FL_Q8_0, 513, 8192, 37), (FL_Q4K, 6144, 4096, 64),
                (FL_Q4K, 4096, 14336, 50), (FL_Q4K, 130, 4096, 17)]
+
+
+# the BASELINE C5 / C3 GEMM shapes at M = 8 (verify) and 64 (prefill pass),
+# plus one shape per token-tile kernel (M 5, 16, 37)
+DOT_SHAPES = [(FL_Q4K, 6144, 4096, 8), (FL_Q4K, 28672, 4096, 8), (FL_Q4K, 4096, 14336, 8),
+              (FL_Q4K, 6144, 4096, 64), (FL_Q4K, 28672, 4096, 64), (FL_Q4K, 4096, 14336, 64),
+              (FL_Q4K, 1536, 4096, 16), (FL_Q4K, 130, 4096, 37),
+              (FL_Q8_0, 3072, 2048, 8), (FL_Q8_0, 16384, 2048, 64), (FL_Q8_0, 2048, 8192, 5),
+              (FL_Q8_0, 1001, 2048, 16)]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("fmt,rows,cols,M", DOT_SHAPES)
+def test_batched_block_dots_bit_exact(backend, oracle, fmt, rows, cols, M):
+    """The per-block integer dots the verify / prefill GEMMs form on the int8
+    MFMA, read back from the MFMA results (fl_op_batched_block_dots), equal
+    the oracle's block dots of every token bit for bit (model.rs:8082-8099,
+    8997-9014)."""
+    print(f"[block-dots] fmt={fmt} {rows}x{cols} M={M}", flush=True)
+    w = S.quantize(S.normal(rows + 7, 0, rows * cols, 0, 0.02).reshape(rows, cols), fmt)
+    W = backend.upload(S.QWeight(w, fmt, rows, cols))
+    qs, ss, sums = [], [], []
+    for m in range(M):
+        q, s = oracle.quantize_q8(S.normal(70 + m, 0, cols, 0.0, 1.0))
+        qs.append(q)
+        ss.append(s)
+        sums.append(q.reshape(-1, 32).astype(np.int32).sum(1, dtype=np.int32))
+    got = backend.batched_block_dots(W, _t(np.stack(qs)), _t(np.stack(ss)), _t(np.stack(sums))).cpu().numpy()
+    for m in range(M):
+        want = oracle.block_dots(w, fmt, rows, cols, qs[m])
+        if fmt == FL_Q4K:
+            # the oracle interleaves (sub-block j, sub-block j + 4); the readback is in sub-block order
+            want = want.reshape(rows, cols // 256, 4, 2).transpose(0, 1, 3, 2).reshape(rows, cols // 32)
+        assert np.array_equal(got[m], want), f"token {m}: {(got[m] != want).sum()} block dots differ"
 
 
 @pytest.mark.parametrize("fmt,rows,cols,M", GEMM_SHAPES)
