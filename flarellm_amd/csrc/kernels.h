@@ -120,16 +120,41 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Workgroup-wide sum with a fixed combination order (deterministic).
+// Sum over the 64 lanes, every lane with the same value: DPP sums inside the
+// 16-lane rows, then the four row sums read into scalars (v_readlane: no LDS
+// round trips) and added in a fixed order.  The whole wave must be active.
+__device__ __forceinline__ float wave_sum_rl(float v) {
+    v = row_sum<16>(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
+
+// Workgroup-wide sum with a fixed combination order (deterministic).  NT:
+// the workgroup's thread count when known at compile time (0: blockDim.x,
+// which is read from the dispatch packet).
+template <int NT = 0>
 __device__ __forceinline__ float wg_sum(float v, float *red) {
-    v = group_sum<64>(v);
+    v = wave_sum_rl(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     __syncthreads();
     if (lane == 0) red[w] = v;
     __syncthreads();
     float t = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += red[i];
+    const int nw = NT ? NT / 64 : (int)(blockDim.x >> 6);
+    for (int i = 0; i < nw; i++) t += red[i];
     return t;
+}
+
+// A uniform int read through the scalar data cache (s_load_dword): waiting
+// for it does not wait for the vector loads in flight, as the wait for a
+// vector load does (loads complete in order).  Only for data that no kernel
+// writes while the reading kernel runs (the scalar cache is invalidated at
+// each launch).
+__device__ __forceinline__ int ld_uniform(const int *p) {
+    return *(const __attribute__((address_space(4))) int *)p;
 }
 
 // ------------------------------------------------------------------------

@@ -85,7 +85,7 @@ inline MvsPlan mvs_plan(int fmt, int rows, int cols, bool f32in, bool pairs = fa
     const int ngrp = (rows + p.r - 1) / std::max(1, p.r);
     p.grid = std::max(1, std::min((ngrp + 3) / 4, 1024));
     if (const char *e = measure_env("FLARE_MVS_GRID")) p.grid = std::max(1, std::min(p.grid, atoi(e)));
-    p.lds = mvs_lds_bytes(f32in, cols);
+    p.lds = mvs_lds_fmt(fmt, f32in, cols);
     if (const char *e = measure_env("FLARE_MVS_LDSPAD")) p.lds += (size_t)atoi(e);  // placement experiments
     return p;
 }

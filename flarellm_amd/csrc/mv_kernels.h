@@ -142,7 +142,7 @@ struct StageQ8 {
             if (j < E) ss += xs[j] * xs[j];
         ST_TS(8);
         if (SEQ) ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
-        else ss = wg_sum(ss, red);
+        else ss = wg_sum<NT>(ss, red);
         ST_TS(9);
         const float rms = sqrtf(ss / (float)n + eps);
         const float inv = 1.0f / rms;
@@ -178,15 +178,15 @@ struct StageQ8 {
         }
         if (E == 8) {
             ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
-            qsum += __shfl_xor(qsum, 1, 64);
-            qsum += __shfl_xor(qsum, 2, 64);
+            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
             if ((t & 3) == 0) {
                 ls[t >> 2] = d;
                 lsum[t >> 2] = qsum;
             }
         } else {
             ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
-            qsum += __shfl_xor(qsum, 1, 64);
+            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
             if ((t & 1) == 0) {
                 ls[t >> 1] = d;
                 lsum[t >> 1] = qsum;
@@ -237,7 +237,7 @@ struct StageF32 {
 #pragma unroll
             for (int j = 0; j < 16; j++)
                 if (j < E) ss += xs[j] * xs[j];
-            ss = wg_sum(ss, red);
+            ss = wg_sum<NT>(ss, red);
             const float rms = sqrtf(ss / (float)n + eps);
             inv = 1.0f / rms;
         }

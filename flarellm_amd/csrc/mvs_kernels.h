@@ -207,96 +207,151 @@ __device__ __forceinline__ float pc_dot_q8(const Pc<F_Q4K> &P, const WDesc &W, c
     return q4_term(P, xl, xh, xs, (float)lsum[own], L);
 }
 
-// ---- f32 input (activations in LDS as floats) ------------------------------
+// ---- f32 input, quantized weights (logits): split activations -------------
 // dequant (quantize.rs) then matvec_argmax_f32's f32 dot (model.rs:8668-8689).
-// LDS holds x[K] and gx[K/16] = the sum of each 16-element group of x.  A
-// lane's 16 consecutive weights share one scale, so their dot is formed as
-// scale * (sum c_j x_j - bias * gx) with c_j the unsigned code (converted to
-// float by one instruction) and bias the code offset (Q8_0: 128 after the
-// sign bias, Q6_K: 32): the same value as sum (scale * q_j) * x_j up to fp32
-// rounding (the accumulation order differs from the reference's sequential
-// sum in any case; parity is 1e-3 relative).  The lane's x values are loaded
-// once per step and shared by the R rows of the tile.
+// The f32 activation is held in LDS as three int8 levels per 16-element
+// group, x ~= s1 a1 + s2 a2 + s3 a3: a1 quantizes x at s1 = max|x| / 127,
+// a2 the remainder x - s1 a1 at its own max / 127, a3 the next remainder
+// (each level gains >= 7.99 bits, so the represented x is within ~2^-24 of
+// the group's largest element: fp32's own resolution).  A lane's 16 weights
+// share one scale, so their dot is
+//     scale * (s1 D1 + s2 D2 + s3 D3 - bias * G),  D_k = sum_j c_j a_kj
+// with D_k three v_dot4_i32_i8 chains over the byte codes c_j (Q8_0: signed
+// codes, bias 0; Q6_K: 6-bit codes 0..63, bias 32) and G = sum_k s_k sum_j
+// a_kj, the represented group sum.  Instead of a conversion and an fp32 FMA
+// per weight: 3 integer dots per 4 weights.  Equal to sum (scale * q_j) *
+// x_j up to fp32 rounding (the accumulation order differs from the
+// reference's sequential sum in any case; production parity is 1e-3
+// relative; the reference-order mode has its own kernel).
+// LDS: a1[K] | a2[K] | a3[K] | per group {s1, s2, s3, G} | red[64]
+__host__ __device__ inline size_t mvs_split_lds_bytes(int K) { return (size_t)K * 3 + (size_t)(K / 16) * 16 + 64 * 4; }
+
+struct XGrp {
+    v4i_t a[3];
+    v4f_t r;  // s1, s2, s3, G
+    __device__ __forceinline__ void load(const char *smem, int K, int e) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) a[k] = *(const v4i_t *)(smem + (size_t)k * K + e);
+        r = *(const v4f_t *)(smem + (size_t)3 * K + (e >> 4) * 16);
+    }
+    // sum_j c_j x_j - BIAS * sum_j x_j over the group, codes c as 4 words
+    template <int BIAS>
+    __device__ __forceinline__ float dot(const uint32_t (&c)[4]) const {
+        int d[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            d[k] = __builtin_amdgcn_sdot4((int)c[0], a[k].x, 0, false);
+            d[k] = __builtin_amdgcn_sdot4((int)c[1], a[k].y, d[k], false);
+            d[k] = __builtin_amdgcn_sdot4((int)c[2], a[k].z, d[k], false);
+            d[k] = __builtin_amdgcn_sdot4((int)c[3], a[k].w, d[k], false);
+        }
+        float v = r.x * (float)d[0];
+        v = __builtin_fmaf(r.y, (float)d[1], v);
+        v = __builtin_fmaf(r.z, (float)d[2], v);
+        if (BIAS) v = __builtin_fmaf(-(float)BIAS, r.w, v);
+        return v;
+    }
+};
+
+// levels of one 16-element group held as NV values per thread (NV = 16: one
+// thread; NV = 8: the lane pair t, t^1, t even holding the first half)
+template <int NV>
+__device__ __forceinline__ void split_levels(const float *v, char *smem, int K, int e0, bool lead) {
+    float r[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) r[j] = v[j];
+    float sk[3], gs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) m = fmaxf(m, fabsf(r[j]));
+        if (NV == 8) m = fmaxf(m, __int_as_float(xpair(__float_as_int(m))));
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f, sc = m * (1.0f / 127.0f);
+        uint32_t w[NV / 4];
+        int sum = 0;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int c = q8_code(r[j] * inv);
+            r[j] = __builtin_fmaf(-sc, (float)c, r[j]);
+            sum += c;
+            if (j % 4 == 0) w[j / 4] = 0u;
+            w[j / 4] |= ((uint32_t)c & 0xFFu) << (8 * (j % 4));
+        }
+        if (NV == 8) sum += xpair(sum);
+        char *dst = smem + (size_t)k * K + e0;
+        if constexpr (NV == 16) *(v4i_t *)dst = v4i_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        else *(v2i_t *)dst = v2i_t{(int)w[0], (int)w[1]};
+        sk[k] = sc;
+        gs = __builtin_fmaf(sc, (float)sum, gs);
+    }
+    if (lead) *(v4f_t *)(smem + (size_t)3 * K + (e0 >> 4) * 16) = v4f_t{sk[0], sk[1], sk[2], gs};
+}
+
 template <int FMT>
 struct XIn;
 
+// Lane bytes of a Q8_0 piece: 16 codes of elements [off, off + 16), one group.
 template <>
 struct XIn<F_Q8_0> {
-    v4f_t x[4];
-    float g;
+    XGrp g;
     bool ok;
-    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+    __device__ __forceinline__ void load(const WDesc &W, const char *smem, int step, int lane) {
         const int K = W.cols, off0 = step * 1024 + 16 * lane;
-        const int off = min(off0, K - 16);
-#pragma unroll
-        for (int j = 0; j < 4; j++) x[j] = *(const v4f_t *)(lx + off + 4 * j);
-        g = lx[K + (off >> 4)];
+        g.load(smem, K, min(off0, K - 16));
         ok = off0 < K;
     }
 };
 
 __device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q8_0> &P, const XIn<F_Q8_0> &X) {
-    float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t u = (uint32_t)P.q[j] ^ 0x80808080u;  // int8 + 128, per byte
-#pragma unroll
-        for (int k = 0; k < 4; k++) a = __builtin_fmaf((float)((u >> (8 * k)) & 0xFFu), X.x[j][k], a);
-    }
-    return X.ok ? mul_h16lo(P.sc, a - 128.0f * X.g) : 0.0f;
+    const uint32_t c[4] = {(uint32_t)P.q.x, (uint32_t)P.q.y, (uint32_t)P.q.z, (uint32_t)P.q.w};
+    return X.ok ? mul_h16lo(P.sc, X.g.dot<0>(c)) : 0.0f;
 }
 
 // dequant_q6k_block (quantize.rs:343-384, llama.cpp layout): w = d*sc*q.
 // Lane bytes: ql[hf*64 + qq*16 + i]; qq<2 -> q1 (low) / q3 (high), qq>=2 ->
-// q2 / q4; the 2 qh bits sit at shift 2*(qq>>1) and +4.
+// q2 / q4; the 2 qh bits sit at shift 2*(qq>>1) and +4.  The low nibbles are
+// the 16 elements from e_lo, the high nibbles the 16 from e_lo + 64.
 template <>
 struct XIn<F_Q6K> {
-    v4f_t xl[4], xh[4];
-    float glo, ghi;
+    XGrp lo, hi;
     int sh;
     bool ok;
-    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+    __device__ __forceinline__ void load(const WDesc &W, const char *smem, int step, int lane) {
         const int K = W.cols, span = (K >> 8) * 128, off0 = step * 1024 + 16 * lane;
         const int off = min(off0, span - 16);
         const int sb = off >> 7, o = off & 127, hf = o >> 6, qq = (o >> 4) & 3;
         const int e_lo = sb * 256 + hf * 128 + (qq >> 1) * 32 + (qq & 1) * 16;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            xl[j] = *(const v4f_t *)(lx + e_lo + 4 * j);
-            xh[j] = *(const v4f_t *)(lx + e_lo + 64 + 4 * j);
-        }
-        glo = lx[K + (e_lo >> 4)];
-        ghi = lx[K + (e_lo >> 4) + 4];
+        lo.load(smem, K, e_lo);
+        hi.load(smem, K, e_lo + 64);
         sh = 2 * (qq >> 1);
         ok = off0 < span;
     }
 };
 
 __device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q6K> &P, const XIn<F_Q6K> &X) {
-    float slo = 0.0f, shi = 0.0f;
+    uint32_t clo[4], chi[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         // four 6-bit codes per word, assembled byte-wise: nibble | 2 qh bits << 4
         const uint32_t lw = (uint32_t)P.ql[j], hw = (uint32_t)P.qh[j];
         // (the 2 bits at sh / sh + 4 of each qh byte land on bits 4-5 by one
         // shift within the byte, sh <= 2)
-        const uint32_t clo = (lw & 0x0F0F0F0Fu) | ((hw << (4 - X.sh)) & 0x30303030u);
-        const uint32_t chi = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> X.sh) & 0x30303030u);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            slo = __builtin_fmaf((float)((clo >> (8 * k)) & 0xFFu), X.xl[j][k], slo);
-            shi = __builtin_fmaf((float)((chi >> (8 * k)) & 0xFFu), X.xh[j][k], shi);
-        }
+        clo[j] = (lw & 0x0F0F0F0Fu) | ((hw << (4 - X.sh)) & 0x30303030u);
+        chi[j] = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> X.sh) & 0x30303030u);
     }
+    const float slo = X.lo.dot<32>(clo), shi = X.hi.dot<32>(chi);
     const float ds_lo = mul_h16lo(P.d, (float)(int8_t)(P.sc & 0xFF)), ds_hi = mul_h16lo(P.d, (float)(int8_t)(P.sc >> 8));
-    return X.ok ? ds_lo * (slo - 32.0f * X.glo) + ds_hi * (shi - 32.0f * X.ghi) : 0.0f;
+    return X.ok ? ds_lo * slo + ds_hi * shi : 0.0f;
 }
 
+// ---- f32 input, f32 weights: x as floats in LDS ---------------------------
 template <>
 struct XIn<F_F32> {
     v4f_t x;
     bool ok;
-    __device__ __forceinline__ void load(const WDesc &W, const float *lx, int step, int lane) {
+    __device__ __forceinline__ void load(const WDesc &W, const char *smem, int step, int lane) {
+        const float *lx = (const float *)smem;
         const int K = W.cols, off0 = step * 1024 + 16 * lane;
         const int off = min(off0, 4 * K - 16);
         x = *(const v4f_t *)(lx + (off >> 2));
@@ -373,11 +428,77 @@ struct Stage<true, NT, SEQ> {
     }
 };
 
+// prologue of the split form (quantized weights, f32 input): x (pro 0) or
+// rmsnorm(x) * w (pro 1, the same roundings as StageF32) -> the three int8
+// levels and group records in LDS
+template <int NT>
+struct StageSplit {
+    v4f_t xv[4], wv[4];
+    __device__ __forceinline__ void issue(const MvsArgs &a) {
+        const int t = threadIdx.x, n = a.W.cols, E = n / NT;
+        if (n == NT * E && (E == 8 || E == 16)) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int o = min(t * E + 4 * k, n - 4);
+                xv[k] = *(const v4f_t *)(a.x + o);
+                wv[k] = *(const v4f_t *)((a.pro == 1 ? a.nw : a.x) + o);  // nw may be null for pro 0
+            }
+        }
+    }
+    __device__ __forceinline__ void finish(const MvsArgs &a, char *smem, float * = nullptr) {
+        const int t = threadIdx.x, n = a.W.cols, E = n / NT;
+        float *red = (float *)(smem + mvs_split_lds_bytes(n) - 64 * 4);
+        if (n == NT * E && (E == 8 || E == 16)) {
+            float xs[16], ws[16];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                xs[4 * k] = xv[k].x; xs[4 * k + 1] = xv[k].y; xs[4 * k + 2] = xv[k].z; xs[4 * k + 3] = xv[k].w;
+                ws[4 * k] = wv[k].x; ws[4 * k + 1] = wv[k].y; ws[4 * k + 2] = wv[k].z; ws[4 * k + 3] = wv[k].w;
+            }
+            float inv = 1.0f;
+            if (a.pro == 1) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (j < E) ss += xs[j] * xs[j];
+                ss = wg_sum<NT>(ss, red);
+                inv = 1.0f / sqrtf(ss / (float)n + a.eps);
+            }
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = (a.pro == 1) ? (xs[j] * inv) * ws[j] : xs[j];
+            if (E == 16) split_levels<16>(v, smem, n, 16 * t, true);
+            else split_levels<8>(v, smem, n, 8 * t, (t & 1) == 0);
+        } else {
+            const float inv = a.pro == 1 ? wg_inv_rms(a.x, n, a.eps, red) : 1.0f;
+            for (int gi = t; gi < n / 16; gi += NT) {
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const float xj = a.x[16 * gi + j];
+                    v[j] = a.pro == 1 ? (xj * inv) * a.nw[16 * gi + j] : xj;
+                }
+                split_levels<16>(v, smem, n, 16 * gi, true);
+            }
+        }
+        __syncthreads();
+    }
+};
+
+// LDS of k_mvs's activation staging
+template <int FMT, bool F32IN>
+__host__ __device__ inline size_t mvs_lds_fmt(int K) {
+    return (F32IN && FMT != F_F32) ? mvs_split_lds_bytes(K) : mvs_lds_bytes(F32IN, K);
+}
+__host__ __device__ inline size_t mvs_lds_fmt(int fmt, bool f32in, int K) {
+    return (f32in && fmt != F_F32) ? mvs_split_lds_bytes(K) : mvs_lds_bytes(f32in, K);
+}
+
 template <int FMT, bool F32IN>
 __device__ __forceinline__ float pc_dot(const Pc<FMT> &P, const WDesc &W, const char *smem, int step, int lane) {
     if constexpr (F32IN) {
         XIn<FMT> X;
-        X.load(W, (const float *)smem, step, lane);
+        X.load(W, smem, step, lane);
         return pc_dot_f32x(P, X);
     } else {
         const int K = W.cols;
@@ -635,7 +756,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     };
     MV_TS(0);
     MV_TSB(0);
-    Stage<F32IN, kMvsThreads, SEQ> stg;
+    typename std::conditional<F32IN && FMT != F_F32, StageSplit<kMvsThreads>, Stage<F32IN, kMvsThreads, SEQ>>::type stg;
     typename std::conditional<RX == 2, typename std::conditional<FMT == F_Q4K, RegX4L<SU>, RegX8L<SU>>::type,
                               RegX8<RX ? SU : 1, SEQ>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
@@ -643,7 +764,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     FLARE_STAGE_BARRIER();  // keep them ahead of the weight loads (loads complete in order)
     load(ta, 0);                   // 2. first weight pieces (unconditional: clamped rows are valid, and
                                    // the prologue below then waits for the activation loads only)
-    const int qpos = a.epi == EPI_QKV ? *a.qkv.posp : 0;
+    const int qpos = a.epi == EPI_QKV ? ld_uniform(a.qkv.posp) : 0;
     // epilogue operands of the wave's first row group, in flight with the
     // first tile: the residual rows (EPI_ADD, lane r = row r) or lane p's
     // RoPE (cos, sin) (EPI_QKV)
@@ -668,7 +789,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         pre1 = *p1;
     }
     MV_TS(1);
-    float *seqa = (float *)(smem + align16(mvs_lds_bytes(F32IN, K)));  // SEQ areas
+    float *seqa = (float *)(smem + align16(mvs_lds_fmt<FMT, F32IN>(K)));  // SEQ areas
     float *fs = seqa + wave * seq_wave_words(R, SU);
     if constexpr (RX) rx.finish(a, lane, fs);
     else stg.finish(a, smem, seqa);  // 3. prologue arithmetic (ends with a barrier)
@@ -697,7 +818,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
 #pragma unroll
             for (int s = 0; s < SU; s++) {
                 XIn<FMT> X;
-                X.load(W, (const float *)smem, rr * SU + s, lane);
+                X.load(W, smem, rr * SU + s, lane);
 #pragma unroll
                 for (int r = 0; r < R; r++) acc[r] += pc_dot_f32x(T[r][s], X);
                 __builtin_amdgcn_sched_barrier(0);
@@ -749,7 +870,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     }
     MV_TS(4);
     if (a.epi == EPI_ARGMAX) {
-        float *red = (float *)(smem + mvs_lds_bytes(F32IN, K) - 64 * 4 - (F32IN ? 0 : 64));
+        float *red = (float *)(smem + mvs_lds_fmt<FMT, F32IN>(K) - 64 * 4 - (F32IN ? 0 : 64));
         wg_argmax_commit(best, a.slot, (unsigned long long *)red);
     }
     MV_TSB(1);

@@ -53,6 +53,9 @@ hipError_t launch_mvs_q8_0(bool f32in, const MvsPlan &p, hipStream_t st, const M
     }
     if (f32in) {
         C(F_Q8_0, true, 2, 1) C(F_Q8_0, true, 4, 1) C(F_Q8_0, true, 2, 2) C(F_Q8_0, true, 4, 2)
+#ifdef FLARE_MEASURE
+        C(F_Q8_0, true, 1, 2) C(F_Q8_0, true, 1, 4) C(F_Q8_0, true, 2, 4)
+#endif
     } else {
         C(F_Q8_0, false, 4, 1) C(F_Q8_0, false, 4, 2) C(F_Q8_0, false, 2, 1) C(F_Q8_0, false, 2, 2) C(F_Q8_0, false, 2, 4) C(F_Q8_0, false, 1, 4) C(F_Q8_0, false, 1, 8)
     }
