@@ -14,7 +14,7 @@ LIB_PATH = os.environ.get("FLARE_LIB") or os.path.join(os.path.dirname(os.path.a
 
 FL_F32, FL_Q8_0, FL_Q4K, FL_Q6K = 0, 1, 2, 3
 FL_KV_F32, FL_KV_F16, FL_KV_Q8, FL_KV_KIVI2 = 0, 1, 2, 3
-FL_OPT_VERIFY_FUSE, FL_OPT_VERIFY_GRAPH, FL_OPT_EXACT = 1, 2, 3
+FL_OPT_VERIFY_FUSE, FL_OPT_VERIFY_GRAPH, FL_OPT_EXACT, FL_OPT_FUSE_ATTN = 1, 2, 3, 4
 FORMAT_NAMES = {FL_F32: "F32", FL_Q8_0: "Q8_0", FL_Q4K: "Q4_K", FL_Q6K: "Q6_K"}
 
 

@@ -39,7 +39,7 @@ def _run(cmd: list[str]) -> None:
 
 
 HIP_SOURCES = ["flare_hip.hip", "mvs_q8_0.hip", "mvs_q4k.hip", "mvs_f32.hip", "attn.hip", "verify.hip", "mvo.hip", "seq.hip",
-               "sample.hip"]
+               "sample.hip", "fused.hip"]
 HOST_SOURCES = ["synth.cpp", "generate.cpp", "gguf.cpp"]
 
 

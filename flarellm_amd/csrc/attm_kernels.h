@@ -242,8 +242,35 @@ __device__ __forceinline__ void lds_wave_sync() {
 
 // One workgroup = (split s, kv head kvh, query z); waves take 32-token
 // blocks of the split's chunk round-robin.
-template <typename KT, int D, int G, int NTH = kAttmThreads>
-__global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
+// The new token's binary16 K / V row (channels [8c, 8c+8)) from the f32 rows
+// the fused QKV workgroups published (agent-scope loads); the cache slot
+// itself was written by those workgroups.
+struct NewRowH16 {
+    v4i_t k, v;
+    __device__ __forceinline__ void build(const AttnArgs &a, int kvh, int c) {
+        const int D = (int)a.tok_stride;
+        float kx[8], vx[8];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const float2 kk = ld_agent2(a.knew + kvh * D + 8 * c + i), vv = ld_agent2(a.vnew + kvh * D + 8 * c + i);
+            kx[i] = kk.x;
+            kx[i + 1] = kk.y;
+            vx[i] = vv.x;
+            vx[i + 1] = vv.y;
+        }
+        k = f32_to_h8(kx);
+        v = f32_to_h8(vx);
+    }
+    __device__ __forceinline__ void store(const AttnArgs &, int, int, int) const {}
+};
+
+// One workgroup = (split bx, kv head by, query bz).  FUSED (fp16 cache, one
+// query): the first K / V block is issued before the wait on fw, q is read
+// with agent-scope loads after it, and the block holding slot pos takes the
+// new token's K / V from the published rows.
+template <typename KT, int D, int G, int NTH, bool FUSED>
+__device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, int bz, const FuseWait &fw) {
+    static_assert(!FUSED || std::is_same<KT, __half>::value, "fused launch: fp16 cache");
     constexpr int DT = D / 32, NT = D / 16, NW = NTH / 64;
     constexpr int OPT = (G * D + NTH - 1) / NTH;
     static_assert(2 * G <= 16, "query heads (hi/lo rows) exceed the MFMA tile");
@@ -265,11 +292,11 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     // KIVI scores A operand: rows (head, high / residual) x channels of q * K scale
     __shared__ __align__(16) _Float16 akb[KIVI ? NW : 1][KIVI ? 2 * G : 1][KIVI ? D : 8];
     __shared__ float kbias[KIVI ? NW : 1][G], vbias[KIVI ? NW : 1][G][DT];
-    __shared__ uint16_t nkh[KIVI ? D : 1], nvh[KIVI ? D : 1];  // KIVI decode step: the new token in binary16
+    __shared__ uint16_t nkh[KIVI || FUSED ? D : 1], nvh[KIVI || FUSED ? D : 1];  // KIVI / fused decode step: the new token in binary16
     __shared__ __align__(16) float qs[KIVI ? G : 1][KIVI ? D : 1];  // KIVI: the query rows
 
     AttnArgs a = a0;
-    const int zq = (int)blockIdx.z;
+    const int zq = bz;
     const bool qpair = a.qpair != 0;
     const int z0 = qpair ? 2 * zq : zq;  // first query of this workgroup
     if (zq) {
@@ -283,7 +310,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         a.part += (size_t)zq * a.nkv * a.nsplit * G * (D + 2);
         a.counters += (size_t)zq * a.nkv;
     }
-    const int kvh = blockIdx.y, s = blockIdx.x, tid = threadIdx.x;
+    const int kvh = by, s = bx, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, kg = lane >> 4, r = lane & 15;
     ATTN_TS(0);
     using Tile0 = typename std::conditional<KIVI, AttmKiviQ<D>, AttmTile<KT, D>>::type;
@@ -298,19 +325,32 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     constexpr bool spec = std::is_same<KT, KvQ8>::value;
     if constexpr (spec) tile.load(a, kvh, min(t0s + wave * kAttmBlock, a.S - kAttmBlock), a.S - 1, lane);
     v4f_t qv[DT][2];
-    {
+    auto load_q = [&]() {
         const int g = min(r >> 1, G - 1);
         // query pairs: rows g >= G/2 are the second query's heads
         constexpr int GH = G / 2 > 0 ? G / 2 : 1;
         const size_t qo = !qpair ? (size_t)(kvh * G + g) * D
                                  : (g >= GH ? (size_t)a.qstride : 0) + (size_t)(kvh * GH + g % GH) * D;
-        const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
+        if constexpr (FUSED) {
+            // published in this launch: agent-scope loads
+            const float *qf = a.q + qo + 8 * kg;
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            qv[dt][0] = qp[8 * dt];
-            qv[dt][1] = qp[8 * dt + 1];
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const float2 u = ld_agent2(qf + 32 * dt + 4 * h), w = ld_agent2(qf + 32 * dt + 4 * h + 2);
+                    qv[dt][h] = v4f_t{u.x, u.y, w.x, w.y};
+                }
+        } else {
+            const v4f_t *qp = (const v4f_t *)(a.q + qo + 8 * kg);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                qv[dt][0] = qp[8 * dt];
+                qv[dt][1] = qp[8 * dt + 1];
+            }
         }
-    }
+    };
+    if constexpr (!FUSED) load_q();
     const int pos = __hip_atomic_load(a.posp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + (qpair ? z0 + 1 : zq),
               T = pos + 1;
     // query pairs: the first query's heads (rows < G/2) stop before slot pos
@@ -332,7 +372,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     const int nact = (T + CH - 1) / CH;
 
     // the new token (Q8 decode step): quantize, store, and use its codes
-    NewRow<KT> nrow;
+    typename std::conditional<FUSED, NewRowH16, NewRow<KT>>::type nrow;
     const bool has_new = a.knew != nullptr;
 
     const int nblk = (t1 - t0 + kAttmBlock - 1) / kAttmBlock;
@@ -344,6 +384,22 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         if (wave < nqb) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
     } else {
         if ((!spec || t0 != t0s) && wave < nblk) tile.load(a, kvh, t0 + wave * kAttmBlock, t1 - 1, lane);
+    }
+    if constexpr (FUSED) {
+        // the first block is in flight; wait for the QKV workgroups of this
+        // kv head, then read q
+        if (tid == 0) {
+            int n = 0;
+            while (__hip_atomic_load(fw.count + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < fw.target) {
+                if (++n > kFuseSpinLimit) {
+                    __hip_atomic_store(fw.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+        load_q();
     }
 
     // A operand of S: row m = 2g + (hi / lo) of head g (rows >= 2G zero)
@@ -430,7 +486,7 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
             }
         }
         v8h_t ak[KQ ? DT : 1];
-        if constexpr (KIVI) if constexpr (!KQ) {
+        if constexpr (KIVI || FUSED) if constexpr (!KQ) {
             if (has_new && pos >= tb && pos < tb + kAttmBlock) {
                 // decode step: the new token goes into the ring (binary16); the
                 // block holding it patches its K row / V column in registers
@@ -783,6 +839,9 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     float *mo = &red[0][0];  // final output of this kv head (for the Q8 copy)
     if (nact == 1) {
         ATTN_TS(4);
+        // the only workgroup of this kv head: clear its fused-launch count
+        if constexpr (FUSED)
+            if (tid == 0) __hip_atomic_store(fw.count + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();  // red is overwritten below
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
@@ -875,7 +934,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
         if constexpr (OPT == 1) {
             // one output per thread, a 32-block in 32 consecutive lanes: the
             // Q8_0 copy straight from registers (no LDS round trip)
-            if (tid == 0) __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) {
+                __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (FUSED) __hip_atomic_store(fw.count + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             if (tid < G * D) {
                 if (a.out) a.out[oix(tid)] = O[0];
                 if (a.oq) {
@@ -897,7 +959,10 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
                 if (a.out) a.out[oix(i)] = v;
             }
         }
-        if (tid == 0) __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+            __hip_atomic_store(&a.counters[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (FUSED) __hip_atomic_store(fw.count + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         ATTN_TSL(8);
     }
     __syncthreads();
@@ -912,6 +977,11 @@ __global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
     }
     if (nact > 1) ATTN_TSL(9);
     else ATTN_TS(7);
+}
+
+template <typename KT, int D, int G, int NTH = kAttmThreads>
+__global__ __launch_bounds__(NTH) void k_attm(AttnArgs a0) {
+    attm_body<KT, D, G, NTH, false>(a0, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, FuseWait{});
 }
 
 }  // namespace fl

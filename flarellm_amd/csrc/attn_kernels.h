@@ -55,6 +55,17 @@ struct AttnArgs {
     int nq;  // k_attq: queries of the pass (even)
 };
 
+// Fused QKV + attention launch (k_qkv_attm): the attention workgroups of kv
+// head h wait until count[h] reaches target (the QKV workgroups of h have
+// published q and the new K / V rows), with a bounded spin that sets *err
+// and proceeds on timeout, so every wave exits.
+struct FuseWait {
+    int *count;
+    int target;
+    int *err;
+};
+constexpr int kFuseSpinLimit = 1 << 22;
+
 // Offset of (slot t, channel d) in one kv head's transposed V store.
 __host__ __device__ inline size_t vt_off(int t, int d, int D) {
     return ((size_t)(t >> 5) * D + d) * 32 + (t & 31);
@@ -100,21 +111,6 @@ struct KvKivi {};
     do {            \
     } while (0)
 #endif
-
-// Agent-scope relaxed atomic float store / load (cross-XCD visible without
-// a cache write-back fence).
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __uint_as_float(__hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-// two adjacent floats (8-byte aligned) in one agent-scope load
-__device__ __forceinline__ float2 ld_agent2(const float *p) {
-    const unsigned long long u =
-        __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__uint_as_float((unsigned)u), __uint_as_float((unsigned)(u >> 32)));
-}
 
 __device__ __forceinline__ void h8_to_f32(const v4i_t &v, float *o) {
     const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};

@@ -142,6 +142,11 @@ __global__ __launch_bounds__(kThreads) void k_silu_mul(const float *g, const flo
 
 // Decode-step head: choose the token (prompt slot or previous argmax) and
 // dequantize its embedding row into x (token_embedding lookup, model.rs:1964).
+// d_counters: split-merge arrival counters [0, 1024), then the fused
+// QKV + attention launch's per-kv-head arrival counts [1024, 1056) and its
+// wait-timeout flag (1056)
+constexpr int kFuseCount = 1024, kFuseErr = 1056, kCounterWords = 1088;
+
 struct DevState {
     int step;     // next step to run
     int pos;      // position of the step in flight
@@ -243,7 +248,7 @@ struct fl_ctx {
     float *d_rope_row = nullptr;  // [2*256]
     float *d_part = nullptr;
     size_t part_cap = 0;
-    int *d_counters = nullptr;    // [1024]
+    int *d_counters = nullptr;    // [kCounterWords]: split arrivals [0, 1024), fused-launch counts and flag after
     unsigned long long *d_slot = nullptr;
     // model
     bool have_cfg = false, have_weights = false;
@@ -264,6 +269,7 @@ struct fl_ctx {
     size_t kvstage_rows = 0;
     float *rope = nullptr;
     int nsplit = 1, chmin = 1, single = kAttmSingle, attn_waves = 8;
+    bool fuse_attn = false;  // FL_OPT_FUSE_ATTN
     int ncu = 256;  // compute units of the device (fl_model_init)
     // activations
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *logits = nullptr;
@@ -663,13 +669,13 @@ int fl_ctx_create(int device, fl_ctx **out) {
     }
     int rc = dev_alloc(c, (void **)&c->d_pos, 64);
     if (!rc) rc = dev_alloc(c, (void **)&c->d_rope_row, 2 * 512 * 4);
-    if (!rc) rc = dev_alloc(c, (void **)&c->d_counters, 1024 * 4);
+    if (!rc) rc = dev_alloc(c, (void **)&c->d_counters, kCounterWords * 4);
     if (!rc) rc = dev_alloc(c, (void **)&c->d_slot, 64);
     if (rc) {
         fl_ctx_destroy(c);
         return rc;
     }
-    (void)hipMemset(c->d_counters, 0, 1024 * 4);
+    (void)hipMemset(c->d_counters, 0, kCounterWords * 4);
     // this device's copy of the no-alloc scratch array (device current)
     e = hipGetSymbolAddress((void **)&c->scratch, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !c->scratch) {
@@ -677,6 +683,7 @@ int fl_ctx_create(int device, fl_ctx **out) {
         return fail(nullptr, FL_E_HIP, "scratch array address: %s", hipGetErrorString(e));
     }
     c->verify_fuse = measure_env("FLARE_NO_VFUSE") == nullptr;  // initial value of FL_OPT_VERIFY_FUSE
+    c->fuse_attn = measure_env("FLARE_FUSE_ATTN") != nullptr;  // initial value of FL_OPT_FUSE_ATTN
     *out = c;
     return 0;
 }
@@ -687,6 +694,7 @@ int fl_set_option(fl_ctx *ctx, int option, int value) {
     case FL_OPT_VERIFY_FUSE: ctx->verify_fuse = value != 0; break;
     case FL_OPT_VERIFY_GRAPH: ctx->verify_graph = value != 0; break;
     case FL_OPT_EXACT: ctx->exact = value != 0; break;
+    case FL_OPT_FUSE_ATTN: ctx->fuse_attn = value != 0; break;
     default: return fail(ctx, FL_E_INVALID, "unknown option %d", option);
     }
     drop_graphs(ctx);  // captured passes bake the old choice in
@@ -749,10 +757,20 @@ void fl_ctx_destroy(fl_ctx *ctx) {
 
 void *fl_ctx_stream(fl_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
+// The fused QKV + attention launch's wait-timeout flag (set only if its
+// bounded wait ran out: the step's outputs are then invalid).
+static int fuse_check(fl_ctx *ctx) {
+    if (!ctx->d_counters) return 0;
+    int err = 0;
+    HIPCHK(ctx, hipMemcpy(&err, ctx->d_counters + kFuseErr, 4, hipMemcpyDeviceToHost));
+    if (err) return fail(ctx, FL_E_HIP, "fused QKV + attention launch: wait for the QKV workgroups timed out");
+    return 0;
+}
+
 int fl_sync(fl_ctx *ctx) {
     if (!ctx) return fail(nullptr, FL_E_INVALID, "null ctx");
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
-    return 0;
+    return fuse_check(ctx);
 }
 
 int fl_weight_upload(fl_ctx *ctx, const fl_raw_weight *w, fl_weight **out) {
@@ -1070,7 +1088,7 @@ int fl_model_init(fl_ctx *ctx, const fl_model_config *cfg, int kv_format) {
     ALLOC(ctx, ctx->tokens, S * 4);
     HIPCHK(ctx, hipMemset(ctx->st, 0, sizeof(DevState)));
     HIPCHK(ctx, hipMemset(ctx->tokens, 0, S * 4));
-    HIPCHK(ctx, hipMemset(ctx->d_counters, 0, 1024 * 4));
+    HIPCHK(ctx, hipMemset(ctx->d_counters, 0, kCounterWords * 4));
     ctx->have_cfg = true;
     return 0;
 }
@@ -1237,7 +1255,7 @@ int fl_reset(fl_ctx *ctx) {
     // split-merge arrival counters: every launch leaves them at zero (the
     // last arriver resets its counter); cleared here too, so a launch that
     // did not complete cannot leave a stale count behind a reset
-    HIPCHK(ctx, hipMemsetAsync(ctx->d_counters, 0, 1024 * 4, ctx->stream));
+    HIPCHK(ctx, hipMemsetAsync(ctx->d_counters, 0, kCounterWords * 4, ctx->stream));
     if (ctx->vcnt) HIPCHK(ctx, hipMemsetAsync(ctx->vcnt, 0, kVerifyCounters * 4, ctx->stream));
     HIPCHK(ctx, hipStreamSynchronize(ctx->stream));
     return 0;
@@ -1394,6 +1412,38 @@ static int probe_kv(fl_ctx *ctx, int l, const int *posp, int M, const float *sta
     return rc ? rc : probe_copy(ctx, PR_V, stage_v, (size_t)n * 4);
 }
 
+// QKV matvec and decode attention of layer l as one launch (fused.hip), for
+// fp16 caches with a matching instantiation.  Returns 0 when launched, 1 when
+// not applicable (the caller launches the two kernels), -rc on an error.
+static int launch_qkv_attention(fl_ctx *ctx, const fl_weight &w, const float *norm_w, int norm_pro, float eps,
+                                int l, const QkvEpi &qe, float *attn_out) {
+    const fl_model_config &c = ctx->cfg;
+    const int nkv = c.num_kv_heads, D = c.head_dim, G = c.num_heads / nkv;
+    if (!ctx->fuse_attn || ctx->kv_format != FL_KV_F16 || nkv < 1 || nkv > kFuseErr - kFuseCount) return 1;
+    if (w.rows != qe.nq + 2 * qe.nk) return -fail(ctx, FL_E_INVALID, "fused QKV rows %d do not match the heads", w.rows);
+    const MvsPlan p = mvs_plan(w.format, w.rows, w.cols, false, true);
+    if (D % p.r) return 1;
+    const int nt = 64 * ctx->attn_waves;  // workgroup size: the attention kernel's
+    const int rx = w.format == FL_Q8_0 && mvs_steps(F_Q8_0, w.cols) <= p.su ? 1 : 0;
+    MvsArgs m = mvs_args(ctx, w, norm_pro, EPI_QKV, ctx->x, norm_w, eps, nullptr, nullptr, nullptr, ctx->qkv, nullptr);
+    m.qkv = qe;
+    m.qkv.publish = 1;
+    m.trace = nullptr;
+    AttnArgs a = layer_attn_args(ctx, l);
+    a.out = attn_out;
+    a.knew = ctx->qkv + qe.nq;
+    a.vnew = ctx->qkv + qe.nq + qe.nk;
+    // one wave per row group of each kv head's query, key and value rows
+    const int ngrp = (G + 2) * D / p.r, nw = nt / 64;
+    const int nqwg = nkv * ((ngrp + nw - 1) / nw);
+    const FuseWait fw{ctx->d_counters + kFuseCount, nqwg / nkv, ctx->d_counters + kFuseErr};
+    const hipError_t e = launch_qkv_attm(w.format == FL_Q8_0 ? F_Q8_0 : F_Q4K, p, rx, D, G, nt, ctx->stream, m, a,
+                                         nqwg, fw);
+    if (e == hipErrorNotSupported) return 1;
+    if (e != hipSuccess) return -fail(ctx, FL_E_HIP, "fused QKV + attention launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
 // x_given: the caller has put the step's f32 embedding row into ctx->x.
 static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
     const fl_model_config &c = ctx->cfg;
@@ -1420,6 +1470,18 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
         int rc;
         if (probe && (rc = probe_copy(ctx, PR_XIN, ctx->x, H * 4))) return rc;
         const QkvEpi qe = layer_qkv_epi(ctx, l);
+        // one launch for QKV and attention where an instantiation fits
+        float *probe_attn = probe ? (float *)(ctx->probe_dev + poff[PR_ATTN]) : nullptr;
+        const int fused = ctx->exact ? 1 : launch_qkv_attention(ctx, L.qkv, L.attn_norm, norm_pro, eps, l, qe, probe_attn);
+        if (fused < 0) return -fused;
+        if (!fused) {
+            if (probe) {
+                if ((rc = probe_copy(ctx, PR_Q, ctx->qkv, nq * 4))) return rc;
+                if ((rc = probe_kv(ctx, l, &ctx->st->pos, 1, ctx->qkv + nq, ctx->qkv + nq + nk))) return rc;
+                if ((rc = probe_copy(ctx, PR_AQ, ctx->aq, nq))) return rc;
+                if ((rc = probe_copy(ctx, PR_AS, ctx->as, nq / 32 * 4))) return rc;
+            }
+        } else {
         rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
                          ctx->qkv, nullptr, &qe);
         if (rc) return rc;
@@ -1450,13 +1512,14 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
             if (probe && (rc = probe_copy(ctx, PR_ATTN, ctx->attn, nq * 4))) return rc;
         } else {
             AttnArgs a = layer_attn_args(ctx, l);
-            if (probe) a.out = (float *)(ctx->probe_dev + poff[PR_ATTN]);  // also the f32 output
+            if (probe) a.out = probe_attn;  // also the f32 output
             rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
             if (rc) return rc;
         }
         if (probe) {
             if ((rc = probe_copy(ctx, PR_AQ, ctx->aq, nq))) return rc;
             if ((rc = probe_copy(ctx, PR_AS, ctx->as, nq / 32 * 4))) return rc;
+        }
         }
         rc = launch_q8in(ctx, L.wo, PRO_LOADQ, EPI_ADD, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->x,
                          nullptr);

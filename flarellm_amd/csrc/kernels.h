@@ -148,6 +148,21 @@ __device__ __forceinline__ float wg_sum(float v, float *red) {
     return t;
 }
 
+// Agent-scope relaxed atomic float store / load (cross-XCD visible without
+// a cache write-back fence).
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __uint_as_float(__hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// two adjacent floats (8-byte aligned) in one agent-scope load
+__device__ __forceinline__ float2 ld_agent2(const float *p) {
+    const unsigned long long u =
+        __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((unsigned)u), __uint_as_float((unsigned)(u >> 32)));
+}
+
 // A uniform int read through the scalar data cache (s_load_dword): waiting
 // for it does not wait for the vector loads in flight, as the wait for a
 // vector load does (loads complete in order).  Only for data that no kernel

@@ -131,6 +131,10 @@ hipError_t launch_mvs_gu_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a)
 enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2, KV_KIVI = 3 };  // == FL_KV_*
 hipError_t launch_attn(int kvfmt, int D, int G, hipStream_t st, const AttnArgs &a, int nq = 1);
 hipError_t launch_attq(int D, int G, hipStream_t st, const AttnArgs &a);
+// fused QKV matvec + decode attention (fused.hip): nqwg QKV workgroups (a
+// multiple of a.nkv) of nt threads, then a.nsplit * a.nkv attention ones
+hipError_t launch_qkv_attm(int fmt, const MvsPlan &p, int rx, int D, int G, int nt, hipStream_t st,
+                           const struct MvsArgs &m, const AttnArgs &at, int nqwg, const FuseWait &fw);
 // workgroups of the MFMA attention kernel (format, D, G, waves) resident on one CU at once
 int attm_resident_per_cu(int kvfmt, int D, int G, int waves);
 // Write n token rows (device f32 [n][nkv][D]) at positions p0.. into a Q8 or

@@ -24,6 +24,10 @@ struct QkvEpi {
     int kv_f16;         // cache element: 1 = binary16 (RNE), 0 = f32
     int kv_stage;       // 1: K (after RoPE) and V go to the output after q, as f32
     int v_tblk;         // 1: V stored in 32-slot transposed blocks [slot/32][D][32]
+    // 1 (fused QKV + attention launch): q, and K (after RoPE) / V as f32
+    // after q, are stored with agent-scope stores for the attention
+    // workgroups of the same launch; the cache rows are written as usual
+    int publish;
 };
 
 #ifdef FLARE_MV_TRACE
@@ -65,7 +69,10 @@ struct QkvEpi {
 // (n == NT*E with E in {8, 16}); other n take the generic loop of stage_q8.
 // ---------------------------------------------------------------------------
 // SEQ: the sum of squares in the reference's sequential order.
-template <int NT, bool SEQ = false>
+// VT <= NT: only threads [0, VT) stage (the decomposition of a VT-thread
+// workgroup, so the sums are those of that kernel); the others only join
+// the barriers.
+template <int NT, bool SEQ = false, int VT = NT>
 struct StageQ8 {
     v4i_t qv[4];  // PRO_LOADQ: int8 quants (16 B each), scales, sums
     float sv[2];
@@ -77,19 +84,20 @@ struct StageQ8 {
     __device__ __forceinline__ void issue(int pro, int n, const float *x, const float *w, const int8_t *gq,
                                           const float *gs, const int *gsum) {
         const int t = threadIdx.x;
+        if (VT < NT && t >= VT) return;
         if (pro == PRO_LOADQ) {
             const int n16 = n >> 4, nb = n >> 5;
 #pragma unroll
-            for (int k = 0; k < 4; k++) qv[k] = ((const v4i_t *)gq)[min(t + k * NT, n16 - 1)];
+            for (int k = 0; k < 4; k++) qv[k] = ((const v4i_t *)gq)[min(t + k * VT, n16 - 1)];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
-                const int j = min(t + k * NT, nb - 1);
+                const int j = min(t + k * VT, nb - 1);
                 sv[k] = gs[j];
                 sumv[k] = gsum[j];
             }
         } else {
-            const int E = n / NT;
-            if (n == NT * E && (E == 8 || E == 16)) {
+            const int E = n / VT;
+            if (n == VT * E && (E == 8 || E == 16)) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int o = min(t * E + 4 * k, n - 4);
@@ -104,27 +112,30 @@ struct StageQ8 {
                                            int8_t *lq, float *ls, int *lsum, float *red, long long *tr = nullptr,
                                            float *ess = nullptr) {
         const int t = threadIdx.x;
+        const bool act = VT == NT || t < VT;
         ST_TS(7);
         if (pro == PRO_LOADQ) {
             const int n16 = n >> 4, nb = n >> 5;
+            if (act) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = t + k * NT;
-                if (i < n16) ((v4i_t *)lq)[i] = qv[k];
-            }
+                for (int k = 0; k < 4; k++) {
+                    const int i = t + k * VT;
+                    if (i < n16) ((v4i_t *)lq)[i] = qv[k];
+                }
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
-                const int j = t + k * NT;
-                if (j < nb) {
-                    ls[j] = sv[k];
-                    lsum[j] = sumv[k];
+                for (int k = 0; k < 2; k++) {
+                    const int j = t + k * VT;
+                    if (j < nb) {
+                        ls[j] = sv[k];
+                        lsum[j] = sumv[k];
+                    }
                 }
             }
             __syncthreads();
             return;
         }
-        const int E = n / NT;
-        if (!(n == NT * E && (E == 8 || E == 16))) {
+        const int E = n / VT;
+        if (!(n == VT * E && (E == 8 || E == 16))) {
             if (pro == PRO_NORMQ0) stage_q8<PRO_NORMQ0, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red, ess);
             else stage_q8<PRO_NORMQ1, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red, ess);
             return;
@@ -140,9 +151,10 @@ struct StageQ8 {
 #pragma unroll
         for (int j = 0; j < 16; j++)
             if (j < E) ss += xs[j] * xs[j];
+        if (!act) ss = 0.0f;
         ST_TS(8);
         if (SEQ) ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
-        else ss = wg_sum<NT>(ss, red);
+        else ss = wg_sum<VT>(ss, red);  // the first VT / 64 waves' sums
         ST_TS(9);
         const float rms = sqrtf(ss / (float)n + eps);
         const float inv = 1.0f / rms;
@@ -177,19 +189,23 @@ struct StageQ8 {
             }
         }
         if (E == 8) {
-            ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
             qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
             qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-            if ((t & 3) == 0) {
-                ls[t >> 2] = d;
-                lsum[t >> 2] = qsum;
+            if (act) {
+                ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
+                if ((t & 3) == 0) {
+                    ls[t >> 2] = d;
+                    lsum[t >> 2] = qsum;
+                }
             }
         } else {
-            ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
             qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-            if ((t & 1) == 0) {
-                ls[t >> 1] = d;
-                lsum[t >> 1] = qsum;
+            if (act) {
+                ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+                if ((t & 1) == 0) {
+                    ls[t >> 1] = d;
+                    lsum[t >> 1] = qsum;
+                }
             }
         }
         ST_TS(10);
@@ -323,6 +339,11 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
         const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
         if (n < e.nq) {
             const int h = n / D;
+            if (e.publish) {
+                st_agent(q + h * D + i, y0);
+                st_agent(q + h * D + i + half, y1);
+                return;
+            }
             q[h * D + i] = y0;
             q[h * D + i + half] = y1;
         } else if (e.kv_stage) {
@@ -331,6 +352,11 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
             q[e.nq + k0 + i + half] = y1;
         } else {
             const int kvh = (n - e.nq) / D;
+            if (e.publish) {
+                const int k0 = (n - e.nq) - j;
+                st_agent(q + e.nq + k0 + i, y0);
+                st_agent(q + e.nq + k0 + i + half, y1);
+            }
             const size_t off = (size_t)kvh * e.head_stride + (size_t)pos * D;
             if (e.kv_f16) {
                 ((uint16_t *)e.kc)[off + i] = f2h(y0);
@@ -343,6 +369,10 @@ __device__ __forceinline__ void store_qkv_pair(float x0, float x1, int n, const 
     } else {
         // v rows keep their original order
         const int vi = n - e.nq - e.nk, kvh = vi / D, d = vi % D;
+        if (e.publish) {
+            st_agent(q + e.nq + e.nk + vi, x0);
+            st_agent(q + e.nq + e.nk + vi + 1, x1);
+        }
         if (e.kv_stage) {
             q[e.nq + e.nk + vi] = x0;
             q[e.nq + e.nk + vi + 1] = x1;

@@ -394,11 +394,11 @@ __host__ __device__ inline size_t mvs_lds_bytes(bool f32in, int K) {
 }
 
 // prologue staging shared by both kernels: x (Q8 or f32) into LDS
-template <bool F32IN, int NT, bool SEQ = false>
+template <bool F32IN, int NT, bool SEQ = false, int VT = NT>
 struct Stage;
-template <int NT, bool SEQ>
-struct Stage<false, NT, SEQ> {
-    StageQ8<NT, SEQ> s;
+template <int NT, bool SEQ, int VT>
+struct Stage<false, NT, SEQ, VT> {
+    StageQ8<NT, SEQ, VT> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw, a.gq, a.gs, a.gsum); }
     __device__ __forceinline__ void finish(const MvsArgs &a, char *smem, float *ess = nullptr) {
         const int K = a.W.cols;
@@ -409,8 +409,8 @@ struct Stage<false, NT, SEQ> {
         s.finish(a.pro, K, a.eps, a.x, a.nw, lq, ls, lsum, red, a.trace, ess);
     }
 };
-template <int NT, bool SEQ>
-struct Stage<true, NT, SEQ> {
+template <int NT, bool SEQ, int VT>
+struct Stage<true, NT, SEQ, VT> {
     StageF32<NT> s;
     __device__ __forceinline__ void issue(const MvsArgs &a) { s.issue(a.pro, a.W.cols, a.x, a.nw); }
     __device__ __forceinline__ void finish(const MvsArgs &a, char *smem, float * = nullptr) {
@@ -730,23 +730,40 @@ constexpr int kMvsThreads = 256;
 // (RegX8), 2 = pre-quantized input (RegX8L)
 // SEQ: row sums and the norm's sum of squares in the reference's sequential
 // order (SeqFold, seq_sumsq); LDS grows by seq_lds_bytes(4, R, SU)
-template <int FMT, bool F32IN, int R, int SU, int RX = 0, bool SEQ = false>
-__global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
+// Row groups a set of waves walks: every group of the weight (RowsAll), or
+// the groups of one kv head's rows in the fused QKV weight (RowsKvGroup:
+// the G*D query rows of its heads, then its D key rows, then its D value
+// rows; rows are [q (nq) | k (nk) | v (nk)], R divides D).
+struct RowsAll {
+    int ngrp;
+    __device__ __forceinline__ int rg(int i) const { return i; }
+};
+struct RowsKvGroup {
+    int ngrp, h, qg, kg, nq, nk, R;  // qg = G*D/R, kg = D/R row groups
+    __device__ __forceinline__ int rg(int i) const {
+        if (i < qg) return h * qg + i;
+        if (i < qg + kg) return (nq / R) + h * kg + (i - qg);
+        return ((nq + nk) / R) + h * kg + (i - qg - kg);
+    }
+};
+
+// The persistent matvec of one set of waves: global wave gw of tw walks row
+// groups map.rg(gw), map.rg(gw + tw), ...  NT: threads per workgroup.
+template <int FMT, bool F32IN, int R, int SU, int RX, bool SEQ, int NT, typename Map>
+__device__ __forceinline__ void mvs_body(const MvsArgs &a, char *smem, int gw, int tw, const Map &map) {
     static_assert(!RX || ((FMT == F_Q8_0 || (FMT == F_Q4K && RX == 2)) && !F32IN),
                   "register activation: Q8_0 weights (or pre-quantized Q4_K input), Q8 input");
     static_assert(!SEQ || !F32IN, "reference-order sums: Q8 input");
-    extern __shared__ __align__(16) char smem[];
     const WDesc &W = a.W;
     const int K = W.cols;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int S = mvs_steps(FMT, K), NR = (S + SU - 1) / SU;
-    const int ngrp = (W.rows + R - 1) / R;
-    const int gw = blockIdx.x * (kMvsThreads / 64) + wave, tw = gridDim.x * (kMvsThreads / 64);
+    const int ngrp = map.ngrp;
     const int nunits = gw < ngrp ? ((ngrp - 1 - gw) / tw + 1) * NR : 0;
 
     Pc<FMT> ta[R][SU], tb[R][SU];
     auto load = [&](Pc<FMT>(&T)[R][SU], int u) {
-        const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
+        const int k = u / NR, rr = u - k * NR, rg = map.rg(min(gw + k * tw, ngrp - 1));
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = min(rg * R + r, W.rows - 1);
@@ -756,7 +773,10 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     };
     MV_TS(0);
     MV_TSB(0);
-    typename std::conditional<F32IN && FMT != F_F32, StageSplit<kMvsThreads>, Stage<F32IN, kMvsThreads, SEQ>>::type stg;
+    // (the Q8 staging of a wider workgroup keeps the decomposition of a
+    // kMvsThreads one: the same norm sums as k_mvs)
+    typename std::conditional<F32IN && FMT != F_F32, StageSplit<NT>,
+                              Stage<F32IN, NT, SEQ, (NT > kMvsThreads ? kMvsThreads : NT)>>::type stg;
     typename std::conditional<RX == 2, typename std::conditional<FMT == F_Q4K, RegX4L<SU>, RegX8L<SU>>::type,
                               RegX8<RX ? SU : 1, SEQ>>::type rx;
     if constexpr (RX) rx.issue(a, lane);
@@ -773,7 +793,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     // waits for the activation loads only.
     float pre0, pre1;
     {
-        const int row0f = min(gw * R, W.rows - 1);
+        const int row0f = min(map.rg(min(gw, ngrp - 1)) * R, W.rows - 1);
         const float *p0 = (const float *)W.q, *p1 = (const float *)W.q;
         if (a.epi == EPI_ADD) {
             p0 = a.out + min(row0f + min(lane, R - 1), W.rows - 1);
@@ -801,7 +821,7 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
     unsigned long long best = 0;
     SeqFold<FMT, R, SU> fold;
     auto consume = [&](const Pc<FMT>(&T)[R][SU], int u) {
-        const int k = u / NR, rr = u - k * NR, rg = gw + k * tw;
+        const int k = u / NR, rr = u - k * NR, rg = map.rg(gw + k * tw);
         if constexpr (SEQ) {
             float t[R][SU];
 #pragma unroll
@@ -874,6 +894,14 @@ __global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
         wg_argmax_commit(best, a.slot, (unsigned long long *)red);
     }
     MV_TSB(1);
+}
+
+template <int FMT, bool F32IN, int R, int SU, int RX = 0, bool SEQ = false>
+__global__ __launch_bounds__(kMvsThreads) void k_mvs(MvsArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int NW = kMvsThreads / 64;
+    mvs_body<FMT, F32IN, R, SU, RX, SEQ, kMvsThreads>(a, smem, (int)blockIdx.x * NW + (threadIdx.x >> 6),
+                                                      (int)gridDim.x * NW, RowsAll{(a.W.rows + R - 1) / R});
 }
 
 // ---------------------------------------------------------------------------

@@ -127,6 +127,13 @@ const char *fl_backend_name(void);
  * sums in the reference's order.  F32 / F16 KV caches only.  Default:
  * tree-order sums (fast; outputs within 1e-3 relative). */
 #define FL_OPT_EXACT 3
+/* FL_OPT_FUSE_ATTN (default 0): with an fp16 KV cache, the decode step runs
+ * each layer's QKV matvec and attention as one launch whose attention
+ * workgroups stream the K / V cache while the QKV workgroups compute, then
+ * wait for them (outputs identical to the two launches).  Measured slower on
+ * MI355X (the attention role's registers halve the QKV role's occupancy), so
+ * off by default. */
+#define FL_OPT_FUSE_ATTN 4
 int fl_set_option(fl_ctx *ctx, int option, int value);
 
 /* Layer probe (testing surface; no reference counterpart).  With layer >= 0,
