@@ -163,6 +163,21 @@ __device__ __forceinline__ float2 ld_agent2(const float *p) {
     return make_float2(__uint_as_float((unsigned)u), __uint_as_float((unsigned)(u >> 32)));
 }
 
+// f32 product of the f16 in the low (high) half of w and b, rounded once as a
+// plain multiply: v_fma_mix_f32 with the f16 operand selected by op_sel and a
+// -0 addend (x + -0 = x for every x, signed zeros included), one op instead of
+// a conversion and a multiply
+__device__ __forceinline__ float mul_h16lo(uint32_t w, float b) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
+    return r;
+}
+__device__ __forceinline__ float mul_h16hi(uint32_t w, float b) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
+    return r;
+}
+
 // A uniform int read through the scalar data cache (s_load_dword): waiting
 // for it does not wait for the vector loads in flight, as the wait for a
 // vector load does (loads complete in order).  Only for data that no kernel
@@ -194,6 +209,31 @@ __device__ static const uint64_t kExp2Tab[32] = {
     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+// fl_expf with the table read from `tab` (a copy of kExp2Tab, e.g. in LDS)
+__device__ __forceinline__ float fl_expf_t(float x, const uint64_t *tab) {
+    if (x != x) return x + x;                   // NaN
+    if (x == -INFINITY) return 0.0f;
+    if (x > 0x1.62e42ep6f) return INFINITY;     // above log(2^128)
+    if (x < -0x1.9fe368p6f) return 0.0f;        // below log(2^-150)
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
+    const double s = __longlong_as_double((long long)t);
+    const double p = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}
 
 __device__ __forceinline__ float fl_expf(float x) {
     if (x != x) return x + x;                   // NaN

@@ -48,21 +48,6 @@ __device__ __forceinline__ void i8x4_to_f32(int w, float *q) {
 // lanes l and l^1 exchange a value (quad_perm [1,0,3,2])
 __device__ __forceinline__ int xpair(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true); }
 
-// f32 product of the f16 in the low (high) half of w and b, rounded once as a
-// plain multiply: v_fma_mix_f32 with the f16 operand selected by op_sel and a
-// -0 addend (x + -0 = x for every x, signed zeros included), one op instead of
-// a conversion and a multiply
-__device__ __forceinline__ float mul_h16lo(uint32_t w, float b) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
-    return r;
-}
-__device__ __forceinline__ float mul_h16hi(uint32_t w, float b) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(b), "v"(-0.0f));
-    return r;
-}
-
 // bytes of one row in the streamed plane
 __host__ __device__ inline int mvs_span(int fmt, int K) {
     return fmt == F_Q8_0 ? K : (fmt == F_F32 ? 4 * K : K / 2);

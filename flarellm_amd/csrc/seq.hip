@@ -77,6 +77,21 @@ __global__ __launch_bounds__(64) void k_attn_scores_exact(SeqAttnArgs a) {
     for (int i = threadIdx.x; i < G * D; i += blockDim.x) lq[i] = a.q[(size_t)kvh * G * D + i];
     __syncthreads();
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (F16 && blockIdx.x * 64 < T) {
+        // the V blocks of these 64 slots, read once here so that the chain
+        // kernel's V loads find them in the memory-side cache: up to 2 blocks
+        // of [D][32] binary16 (4 D 16-byte pieces each), D / 8 pieces per lane
+        const v4i_t *vb = (const v4i_t *)((const uint16_t *)a.vc + (size_t)kvh * a.head_stride +
+                                           (size_t)blockIdx.x * 2 * D * 32);
+        const int nb = min(2, (T - (int)blockIdx.x * 64 + 31) / 32);
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const int e = threadIdx.x + 64 * i;  // piece e of nb * D * 4 pieces
+            if (e < nb * D * 4) acc ^= vb[e].x;
+        }
+        asm volatile("" ::"v"(acc));
+    }
     if (t >= T) return;
     const size_t hbase = (size_t)kvh * a.head_stride + (size_t)t * D;
     const float scale = 1.0f / sqrtf((float)D);
@@ -106,25 +121,51 @@ __global__ __launch_bounds__(64) void k_attn_scores_exact(SeqAttnArgs a) {
 }
 
 constexpr int kChainBlk = 32;
-constexpr int kChainRing = 8;  // fp16 V blocks in flight per lane
+constexpr int kChainRing = 8;        // fp16 V blocks in flight per chain lane
+constexpr int kChainThreads = 512;   // prologue parallelism; D chain lanes + the sum lane
 
-// 32 fp16 V values of lane d for one 32-slot block ([slot/32][D][32] layout)
+// 32 fp16 V values of lane d for one 32-slot block ([slot/32][D][32] layout):
+// value j in word j / 2 (q[j / 8][(j / 2) % 4]), half j % 2
 struct VBlk {
     v4i_t q[4];
 };
 
+// the products w_t * v_t of one block, each one v_fma_mix (the exact binary16
+// operand times w plus -0: rounded once, as (float)v * w); the weights in 8
+// b128 LDS reads
+__device__ __forceinline__ void chain_products(const VBlk &v, const float *w, float (&p)[kChainBlk]) {
+    const v4f_t *wp = (const v4f_t *)w;
+#pragma unroll
+    for (int q = 0; q < kChainBlk / 4; q++) {
+        const v4f_t wq = wp[q];
+        const uint32_t w0 = (uint32_t)v.q[q >> 1][2 * (q & 1)], w1 = (uint32_t)v.q[q >> 1][2 * (q & 1) + 1];
+        p[4 * q] = mul_h16lo(w0, wq.x);
+        p[4 * q + 1] = mul_h16hi(w0, wq.y);
+        p[4 * q + 2] = mul_h16lo(w1, wq.z);
+        p[4 * q + 3] = mul_h16hi(w1, wq.w);
+    }
+}
+
+
 template <bool F16>
-__global__ __launch_bounds__(256) void k_attn_chain_exact(SeqAttnArgs a) {
-    extern __shared__ float sm[];  // w[slots] | old[slots] | flags[slots/32] | wave maxima[4] | sum
+__global__ __launch_bounds__(kChainThreads) void k_attn_chain_exact(SeqAttnArgs a) {
+    extern __shared__ float sm[];  // w[slots] | old[slots] | flags[slots/32] | wave maxima[8] | sum
+    __shared__ uint64_t etab[32];  // the exp table of fl_expf
+    constexpr int NW = kChainThreads / 64;
     const int h = blockIdx.x, kvh = h / a.group, D = a.D;
-    const int T = *a.posp + 1, nt = blockDim.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int T = *a.posp + 1, nt = kChainThreads, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nblk = (T + kChainBlk - 1) / kChainBlk;
     float *w = sm, *old = sm + a.slots;
     int *flag = (int *)(old + a.slots);
     float *wmax = (float *)(flag + (a.slots + kChainBlk - 1) / kChainBlk);
-    float *ssum = wmax + 4;
+    float *ssum = wmax + NW;
     const size_t hb = (size_t)kvh * a.head_stride;
-    // the chain lanes' first V blocks, in flight during the prologue
+    // scores into LDS first (vector loads complete in order), flags cleared
+    const float *sc = a.scores + (size_t)h * a.slots;
+    for (int t = tid; t < T; t += nt) w[t] = sc[t];
+    for (int b = tid; b < nblk; b += nt) flag[b] = 0;
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    // then the chain lanes' first V blocks, in flight during the prologue
     VBlk ring[kChainRing];
     if (F16 && tid < D) {
 #pragma unroll
@@ -134,9 +175,6 @@ __global__ __launch_bounds__(256) void k_attn_chain_exact(SeqAttnArgs a) {
             for (int i = 0; i < 4; i++) ring[r].q[i] = p[i];
         }
     }
-    // scores into LDS
-    const float *sc = a.scores + (size_t)h * a.slots;
-    for (int t = tid; t < T; t += nt) w[t] = sc[t];
     __syncthreads();
     // running maximum: contiguous chunks; exclusive max of the earlier chunks
     // by a wave scan and the wave maxima (max is exact in any order)
@@ -154,62 +192,79 @@ __global__ __launch_bounds__(256) void k_attn_chain_exact(SeqAttnArgs a) {
     if (lane == 0) m = -INFINITY;
     __syncthreads();
     for (int i = 0; i < wv; i++) m = fmaxf(m, wmax[i]);
+    // the running maximum m_t of the chunk into old[] (a cheap serial pass),
+    // then the weights exp(s_t - m_t) and rescales exp(m_{t-1} - m_t) as
+    // independent iterations (table in LDS; exp(0) = 1 exactly); a block
+    // with a rescale other than 1 is flagged
+    const float m_in = m;
     for (int t = c0; t < c1; t++) {
-        const float s = w[t];
-        const float nm = fmaxf(m, s);
-        old[t] = fl_expf(m - nm);
-        w[t] = fl_expf(s - nm);
-        m = nm;
+        m = fmaxf(m, w[t]);
+        old[t] = m;
     }
-    __syncthreads();
-    for (int b = tid; b < nblk; b += nt) {
-        int f = 0;
-        for (int t = b * kChainBlk; t < min(T, (b + 1) * kChainBlk); t++) f |= old[t] != 1.0f;
-        flag[b] = f;
+    float pm = m_in;
+    for (int t = c0; t < c1; t++) {
+        const float s = w[t], nm = old[t];
+        w[t] = fl_expf_t(s - nm, etab);
+        const float r = pm == nm ? 1.0f : fl_expf_t(pm - nm, etab);
+        old[t] = r;
+        if (r != 1.0f) flag[t / kChainBlk] = 1;
+        pm = nm;
     }
     __syncthreads();
     if (tid < D) {
         float o = 0.0f;
-        auto step_block = [&](int b, const float (&v)[kChainBlk]) {
-            const int t0 = b * kChainBlk, n = min(kChainBlk, T - t0);
-            if (n == kChainBlk && !flag[b]) {
-#pragma unroll
-                for (int i = 0; i < kChainBlk; i++) o = o + w[t0 + i] * v[i];
-            } else {
-#pragma unroll
-                for (int i = 0; i < kChainBlk; i++)
-                    if (i < n) o = o * old[t0 + i] + w[t0 + i] * v[i];
-            }
-        };
         if (F16) {
-            for (int b0 = 0; b0 < nblk; b0 += kChainRing) {
+            // per block: its 32 products first (independent), then the
+            // dependent adds (between changes of the maximum the rescale is
+            // exactly 1 and o * 1 = o: one dependent add per slot).  A wave64
+            // VALU instruction holds the SIMD for 4 cycles, so the chain is
+            // issue-bound (~26 cycles per slot measured with every schedule
+            // tried: products interleaved with the adds, or formed a block
+            // ahead; the V stream costs ~10 % of it).
+            auto block = [&](int b, VBlk &slot) {
+                const int t0 = b * kChainBlk, n = min(kChainBlk, T - t0);
+                float p[kChainBlk];
+                chain_products(slot, w + t0, p);
+                // refill the slot with block b + kChainRing
+                const v4i_t *q = (const v4i_t *)((const uint16_t *)a.vc + hb +
+                                                 ((size_t)min(b + kChainRing, nblk - 1) * D + tid) * 32);
 #pragma unroll
-                for (int r = 0; r < kChainRing; r++) {
-                    const int b = b0 + r;
-                    if (b < nblk) {
-                        float v[kChainBlk];
+                for (int i = 0; i < 4; i++) slot.q[i] = q[i];
+                if (n == kChainBlk && !flag[b]) {
 #pragma unroll
-                        for (int i = 0; i < 4; i++)
+                    for (int i = 0; i < kChainBlk; i++) o = o + p[i];
+                } else {
 #pragma unroll
-                            for (int e = 0; e < 8; e++)
-                                v[8 * i + e] = h2f((uint16_t)((uint32_t)ring[r].q[i][e >> 1] >> (16 * (e & 1))));
-                        // refill this ring slot with block b + kChainRing
-                        const v4i_t *p = (const v4i_t *)((const uint16_t *)a.vc + hb +
-                                                         ((size_t)min(b + kChainRing, nblk - 1) * D + tid) * 32);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) ring[r].q[i] = p[i];
-                        step_block(b, v);
-                    }
+                    for (int i = 0; i < kChainBlk; i++)
+                        if (i < n) o = o * old[t0 + i] + p[i];
                 }
+            };
+            // whole rounds of the ring without conditions (so the compiler's
+            // wait counts stay exact: each slot waits for its own loads only),
+            // then the remaining blocks
+            int b0 = 0;
+            for (; b0 + kChainRing <= nblk; b0 += kChainRing) {
+#pragma unroll
+                for (int r = 0; r < kChainRing; r++) block(b0 + r, ring[r]);
             }
+#pragma unroll
+            for (int r = 0; r < kChainRing; r++)
+                if (b0 + r < nblk) block(b0 + r, ring[r]);
         } else {
             for (int b = 0; b < nblk; b++) {
-                const int t0 = b * kChainBlk;
+                const int t0 = b * kChainBlk, n = min(kChainBlk, T - t0);
                 float v[kChainBlk];
 #pragma unroll
                 for (int i = 0; i < kChainBlk; i++)
                     v[i] = ((const float *)a.vc)[hb + (size_t)min(t0 + i, T - 1) * D + tid];
-                step_block(b, v);
+                if (n == kChainBlk && !flag[b]) {
+#pragma unroll
+                    for (int i = 0; i < kChainBlk; i++) o = o + w[t0 + i] * v[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kChainBlk; i++)
+                        if (i < n) o = o * old[t0 + i] + w[t0 + i] * v[i];
+                }
             }
         }
         __syncthreads();
@@ -221,15 +276,30 @@ __global__ __launch_bounds__(256) void k_attn_chain_exact(SeqAttnArgs a) {
         a.out[(size_t)h * D + tid] = o;
     } else {
         if (tid == D) {
+            // the weights' sum in the same order; the next block's weights
+            // are read while this block's adds run
             float sum = 0.0f;
+            v4f_t wq[kChainBlk / 4], wqn[kChainBlk / 4];
+#pragma unroll
+            for (int q = 0; q < kChainBlk / 4; q++) wq[q] = ((const v4f_t *)w)[q];
             for (int b = 0; b < nblk; b++) {
                 const int t0 = b * kChainBlk, n = min(kChainBlk, T - t0);
+                const v4f_t *wn = (const v4f_t *)(w + (size_t)min(b + 1, nblk) * kChainBlk);
+#pragma unroll
+                for (int q = 0; q < kChainBlk / 4; q++) wqn[q] = wn[q];
                 if (n == kChainBlk && !flag[b]) {
 #pragma unroll
-                    for (int i = 0; i < kChainBlk; i++) sum = sum + w[t0 + i];
+                    for (int q = 0; q < kChainBlk / 4; q++) {
+                        sum = sum + wq[q].x;
+                        sum = sum + wq[q].y;
+                        sum = sum + wq[q].z;
+                        sum = sum + wq[q].w;
+                    }
                 } else {
                     for (int i = 0; i < n; i++) sum = sum * old[t0 + i] + w[t0 + i];
                 }
+#pragma unroll
+                for (int q = 0; q < kChainBlk / 4; q++) wq[q] = wqn[q];
             }
             *ssum = sum;
         }
@@ -382,8 +452,11 @@ __global__ __launch_bounds__(256) void k_out_exact(WDesc W, const float *xn, flo
     if ((threadIdx.x & 63) == 0 && best) atomicMax(slot, best);
 }
 
-hipError_t launch_attn_seq(bool f16, hipStream_t st, const SeqAttnArgs &a, int num_heads) {
-    const size_t chain_lds = (size_t)a.slots * 8 + (size_t)((a.slots + kChainBlk - 1) / kChainBlk) * 4 + 32;
+hipError_t launch_attn_seq(bool f16, hipStream_t st, const SeqAttnArgs &a0, int num_heads) {
+    const SeqAttnArgs &a = a0;
+    // w / old of every slot, the block flags, 8 wave maxima, the sum, and one
+    // block of slack (the pipelined chain reads block nblk's weights, unused)
+    const size_t chain_lds = (size_t)a.slots * 8 + (size_t)((a.slots + kChainBlk - 1) / kChainBlk) * 4 + 64 + kChainBlk * 4;
     // the chain kernel: whole waves of chain lanes (D a multiple of 64) plus
     // one wave for the sum, at most 4 waves; w / old of every slot in LDS
     if (a.group > 8 || (a.D != 64 && a.D != 128) || chain_lds > 64 * 1024) {
@@ -395,7 +468,7 @@ hipError_t launch_attn_seq(bool f16, hipStream_t st, const SeqAttnArgs &a, int n
     const int nkv = num_heads / a.group;
     const dim3 sg((a.slots + 63) / 64, nkv);
     const size_t qlds = (size_t)a.group * a.D * 4;
-    const int nt = ((a.D + 64 + 63) / 64) * 64;  // D chain lanes + the sum wave
+    const int nt = kChainThreads;  // D chain lanes + the sum lane + prologue threads
     if (f16) {
         if (a.D == 64) hipLaunchKernelGGL((k_attn_scores_exact<true, 64>), sg, dim3(64), qlds, st, a);
         else hipLaunchKernelGGL((k_attn_scores_exact<true, 128>), sg, dim3(64), qlds, st, a);
