@@ -12,18 +12,26 @@ hipError_t launch_vgemm(int fmt, hipStream_t st, const VgArgs &a) {
     if (a.M > kVerifyMaxTokens && a.W.cols % 256 == 0 && !a.post) {
         // prefill batches: activations staged per 256-value step (chunk = steps)
         // Q4_K: the int8-MFMA form, whose MFMAs form the reference's exact
-        // per-block integer dots (FLARE_PGEMM_H: the f16-MFMA form, 3.5 %
-        // faster on the C3 prefill but with no integer dots; a measurement
-        // switch)
+        // per-block integer dots (C3 4096-token prefill 395 ms).
+        // FLARE_PGEMM_H: the f16-MFMA form (sub-block scales folded into the
+        // weight operand, activation scales into the activation operand, so
+        // the MFMAs apply the block terms; 381 ms), whose MFMAs accumulate
+        // scaled products rather than integer dots; a measurement switch
         static const bool f16 = measure_env("FLARE_PGEMM_H") != nullptr;
         if (fmt == F_Q4K && f16 && !a.dots) {
             const dim3 gh((tiles + 7) / 8, a.ksplit);
             static const bool db = measure_env("FLARE_PGEMM_DB") != nullptr;  // measurement switch
             if (db) hipLaunchKernelGGL((k_pgemm_h<8, 2>), gh, dim3(512), 0, st, a);
             else hipLaunchKernelGGL((k_pgemm_h<8, 1>), gh, dim3(512), 0, st, a);
-        } else if (fmt == F_Q4K) hipLaunchKernelGGL(k_pgemm<F_Q4K>, grid, dim3(256), 0, st, a);
-        else if (fmt == F_Q8_0) hipLaunchKernelGGL(k_pgemm<F_Q8_0>, grid, dim3(256), 0, st, a);
-        else return hipErrorNotSupported;
+        } else if (fmt == F_Q4K) {
+            if (a.dots) hipLaunchKernelGGL((k_pgemm<F_Q4K, true>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_pgemm<F_Q4K, false>), grid, dim3(256), 0, st, a);
+        } else if (fmt == F_Q8_0) {
+            if (a.dots) hipLaunchKernelGGL((k_pgemm<F_Q8_0, true>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_pgemm<F_Q8_0, false>), grid, dim3(256), 0, st, a);
+        } else {
+            return hipErrorNotSupported;
+        }
         return hipGetLastError();
     }
     if (a.W.cols % 32) return hipErrorInvalidValue;

@@ -299,7 +299,10 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls
 //   Q8_0  acc += (s * d_w) * dot
 // (the same terms as the reference's s * (d*sc*dot - dmin*mn*sum q), in
 // another rounding order).
-template <int FMT>
+// DOTS: also write each per-block integer dot to a.dots (the readback of
+// fl_op_batched_block_dots; a separate instantiation, so the product's has
+// no trace of it)
+template <int FMT, bool DOTS = false>
 __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
     __shared__ __align__(16) int8_t lx[2][64 * kPgStride];
     __shared__ __align__(16) float lsc[2][8 * 64];  // [block][token] activation scales
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++)
                     dd[tt] = vg_mfma(*(const i64x1_t *)(bx + (tA + 16 * tt) * kPgStride + 32 * j + 8 * kg), wb);
-                if (a.dots)
+                if constexpr (DOTS)
 #pragma unroll
                     for (int tt = 0; tt < 4; tt++)
 #pragma unroll
