@@ -8,7 +8,7 @@ from what those published.  The values and the order of every operation are
 those of the two separate kernels, so the decode step's outputs must be
 bit-identical with the option on and off -- logits, greedy tokens, and the
 cache the following steps read.  Checked at the C2 and C3 model widths
-(2 layers), at contexts that exercise one split and several (the split merge),
+(2 layers), at contexts of one split, a few, and more than 8 per kv head,
 through the graph-replayed greedy loop and the logits-returning step.
 
 The reference path: forward_layers (flare-core/src/model.rs:1955-2561),
@@ -40,7 +40,10 @@ def _run(backend, prompt, n_gen, n_logit, fuse):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("width,n_prompt", [("c2", 5), ("c2", 300), ("c3", 7), ("c3", 600)])
+# contexts: one split, a few, and more than 8 per kv head (the split merge's
+# batched form; C2 128-slot and C3 256-slot chunks)
+@pytest.mark.parametrize("width,n_prompt", [("c2", 5), ("c2", 300), ("c2", 1100), ("c3", 7), ("c3", 600),
+                                            ("c3", 2200)])
 def test_fused_step_identical(backend, width, n_prompt):
     base = S.LLAMA32_1B if width == "c2" else S.LLAMA3_8B
     spec = S.replace(base, layers=2, max_seq=n_prompt + 48)
