@@ -106,24 +106,11 @@ __device__ __forceinline__ float row_max(float v) {
     if (W >= 16) v = fmaxf(v, FL_DPP(v, 0x140));
     return v;
 }
-// Sum / max over all 64 lanes (DPP within rows, then two cross-row shuffles).
-__device__ __forceinline__ float wave_sum(float v) {
-    v = row_sum<16>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = row_max<16>(v);
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
-}
-
-// Sum over the 64 lanes, every lane with the same value: DPP sums inside the
+// Sum over all 64 lanes, every lane with the same value: DPP sums inside the
 // 16-lane rows, then the four row sums read into scalars (v_readlane: no LDS
-// round trips) and added in a fixed order.  The whole wave must be active.
-__device__ __forceinline__ float wave_sum_rl(float v) {
+// round trips) and added as (r0 + r1) + (r2 + r3), the order of the
+// cross-row shuffle form (xor 16, then xor 32).  The whole wave must be active.
+__device__ __forceinline__ float wave_sum(float v) {
     v = row_sum<16>(v);
     const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
     const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
@@ -131,13 +118,20 @@ __device__ __forceinline__ float wave_sum_rl(float v) {
     const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return (a + b) + (c + d);
 }
+// Max over all 64 lanes (DPP within rows, then two cross-row shuffles).
+__device__ __forceinline__ float wave_max(float v) {
+    v = row_max<16>(v);
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
 
 // Workgroup-wide sum with a fixed combination order (deterministic).  NT:
 // the workgroup's thread count when known at compile time (0: blockDim.x,
 // which is read from the dispatch packet).
 template <int NT = 0>
 __device__ __forceinline__ float wg_sum(float v, float *red) {
-    v = wave_sum_rl(v);
+    v = wave_sum(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     __syncthreads();
     if (lane == 0) red[w] = v;
