@@ -924,7 +924,38 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
                 }
             }
         };
-        if (nact <= 8) merge(std::integral_constant<int, 8>{});
+        // one output per thread (one query head per wave): lane j of every
+        // wave loads split j's (m, l) and forms its weight e^(m_j - M) once;
+        // each lane folds its head's o_j * w_j in split order, w_j read from
+        // lane j.  Two (m, l) loads per wave instead of two per split.
+        auto wmerge = [&](auto mbc) {
+            constexpr int MB = decltype(mbc)::value;
+            const int i = min(tid, G * D - 1), g = i / D;
+            float mj = -INFINITY, lj = 0.0f;
+            if (lane < nact) {
+                const float *pm = pb + (size_t)lane * P + G * D + 2 * g;
+                mj = ld_agent(pm);
+                lj = ld_agent(pm + 1);
+            }
+            float ov[MB];
+#pragma unroll
+            for (int k2 = 0; k2 < MB; k2++) ov[k2] = ld_agent(pb + (size_t)min(k2, nact - 1) * P + i);
+            const float Mw = wave_max(mj);
+            const float wj = (mj == -INFINITY) ? 0.0f : __expf(mj - Mw);
+            L[0] = wave_sum(lj * wj);
+            float o = 0.0f;
+#pragma unroll
+            for (int k2 = 0; k2 < MB; k2++)
+                if (k2 < nact) o = fmaf(ov[k2], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), k2)), o);
+            O[0] = o;
+        };
+        if (OPT == 1 && nact <= 64) {
+            if (nact <= 8) wmerge(std::integral_constant<int, 8>{});
+            else if (nact <= 16) wmerge(std::integral_constant<int, 16>{});
+            else if (nact <= 24) wmerge(std::integral_constant<int, 24>{});
+            else if (nact <= 32) wmerge(std::integral_constant<int, 32>{});
+            else wmerge(std::integral_constant<int, 64>{});
+        } else if (nact <= 8) merge(std::integral_constant<int, 8>{});
         else if (nact <= 16) merge(std::integral_constant<int, 16>{});
         else if (OPT > 1 || nact <= 24) merge(std::integral_constant<int, OPT == 1 ? 24 : 16>{});
         else merge(std::integral_constant<int, 32>{});

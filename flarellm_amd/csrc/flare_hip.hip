@@ -484,6 +484,11 @@ static int upload_concat(fl_ctx *ctx, const fl_raw_weight *const *ws_in, int n, 
 
 // ---- launches ---------------------------------------------------------------
 
+#ifdef FLARE_MV_TRACE
+// trace builds: FLARE_MV_TRACE_LAYER = l records the QKV launch of layer l of
+// the decode step only (graph replays included)
+static bool g_trace_off = false;
+#endif
 static MvsArgs mvs_args(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const float *x, const float *nw,
                         float eps, const int8_t *q, const float *s, const int *sums, float *out,
                         unsigned long long *slot) {
@@ -500,6 +505,9 @@ static MvsArgs mvs_args(fl_ctx *ctx, const fl_weight &w, int pro, int epi, const
     a.out = out;
     a.slot = slot;
     a.trace = ctx->bench_trace;
+#ifdef FLARE_MV_TRACE
+    if (g_trace_off) a.trace = nullptr;
+#endif
     return a;
 }
 
@@ -1482,8 +1490,22 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
                 if ((rc = probe_copy(ctx, PR_AS, ctx->as, nq / 32 * 4))) return rc;
             }
         } else {
+        // measurement: QKV on pre-quantized codes (wrong values, the time of
+        // a QKV without its norm prologue)
+#ifdef FLARE_MV_TRACE
+        static const int trace_layer = measure_env("FLARE_MV_TRACE_LAYER") ? atoi(measure_env("FLARE_MV_TRACE_LAYER")) : -1;
+        g_trace_off = trace_layer >= 0 && l != trace_layer;
+#endif
+        static const bool qkv_preq = measure_env("FLARE_QKV_PREQ") != nullptr;
+        if (qkv_preq && !ctx->exact)
+            rc = launch_q8in(ctx, L.qkv, PRO_LOADQ, EPI_QKV, nullptr, nullptr, 0.f, ctx->hq, ctx->hs, ctx->hsum,
+                             ctx->qkv, nullptr, &qe);
+        else
         rc = launch_q8in(ctx, L.qkv, norm_pro, EPI_QKV, ctx->x, L.attn_norm, eps, nullptr, nullptr, nullptr,
                          ctx->qkv, nullptr, &qe);
+#ifdef FLARE_MV_TRACE
+        g_trace_off = trace_layer >= 0;
+#endif
         if (rc) return rc;
         if (probe) {
             if ((rc = probe_copy(ctx, PR_Q, ctx->qkv, nq * 4))) return rc;
@@ -1525,6 +1547,11 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
                          nullptr);
         if (rc) return rc;
         if (probe && (rc = probe_copy(ctx, PR_XMID, ctx->x, H * 4))) return rc;
+        static const bool gu_preq = measure_env("FLARE_GU_PREQ") != nullptr;
+        if (gu_preq && !ctx->exact)
+            rc = launch_gateup(ctx, L.gu, PRO_LOADQ, nullptr, nullptr, 0.f, ctx->aq, ctx->as, ctx->asum, ctx->hq,
+                               ctx->hs, ctx->hsum, nullptr);
+        else
         rc = launch_gateup(ctx, L.gu, norm_pro, ctx->x, L.ffn_norm, eps, nullptr, nullptr, nullptr, ctx->hq, ctx->hs,
                            ctx->hsum, nullptr);
         if (rc) return rc;

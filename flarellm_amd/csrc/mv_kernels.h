@@ -140,74 +140,78 @@ struct StageQ8 {
             else stage_q8<PRO_NORMQ1, SEQ>(x, w, eps, n, nullptr, nullptr, nullptr, lq, ls, lsum, red, ess);
             return;
         }
-        float xs[16], ws[16];
+        // E (8 or 16) as a compile-time constant: no per-element guards
+        auto body = [&](auto ec) {
+            constexpr int EC = decltype(ec)::value;
+            float xs[EC], ws[EC];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            xs[4 * k] = xv[k].x; xs[4 * k + 1] = xv[k].y; xs[4 * k + 2] = xv[k].z; xs[4 * k + 3] = xv[k].w;
-            ws[4 * k] = wv[k].x; ws[4 * k + 1] = wv[k].y; ws[4 * k + 2] = wv[k].z; ws[4 * k + 3] = wv[k].w;
-        }
-        // sum of squares: per-thread sequential, then the workgroup tree
-        float ss = 0.0f;
+            for (int k = 0; k < EC / 4; k++) {
+                xs[4 * k] = xv[k].x; xs[4 * k + 1] = xv[k].y; xs[4 * k + 2] = xv[k].z; xs[4 * k + 3] = xv[k].w;
+                ws[4 * k] = wv[k].x; ws[4 * k + 1] = wv[k].y; ws[4 * k + 2] = wv[k].z; ws[4 * k + 3] = wv[k].w;
+            }
+            // sum of squares: per-thread sequential, then the workgroup tree
+            float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            if (j < E) ss += xs[j] * xs[j];
-        if (!act) ss = 0.0f;
-        ST_TS(8);
-        if (SEQ) ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
-        else ss = wg_sum<VT>(ss, red);  // the first VT / 64 waves' sums
-        ST_TS(9);
-        const float rms = sqrtf(ss / (float)n + eps);
-        const float inv = 1.0f / rms;
-        float v[16];
-        // rmsnorm_quantize_q8_0_scalar (x*w)*inv (model.rs:5615) or
-        // rmsnorm_scalar_into (x*inv)*w (model.rs:7474): one branch on the
-        // uniform prologue kind
-        if (pro == PRO_NORMQ0) {
+            for (int j = 0; j < EC; j++) ss += xs[j] * xs[j];
+            if (!act) ss = 0.0f;
+            ST_TS(8);
+            if (SEQ) ss = ess ? ess_sumsq_wg(x, n, ess) : seq_sumsq(x, n);
+            else ss = wg_sum<VT>(ss, red);  // the first VT / 64 waves' sums
+            ST_TS(9);
+            const float rms = sqrtf(ss / (float)n + eps);
+            const float inv = 1.0f / rms;
+            float v[EC];
+            // rmsnorm_quantize_q8_0_scalar (x*w)*inv (model.rs:5615) or
+            // rmsnorm_scalar_into (x*inv)*w (model.rs:7474): one branch on the
+            // uniform prologue kind
+            if (pro == PRO_NORMQ0) {
 #pragma unroll
-            for (int j = 0; j < 16; j++) v[j] = j < E ? xs[j] * ws[j] * inv : 0.0f;
-        } else {
+                for (int j = 0; j < EC; j++) v[j] = xs[j] * ws[j] * inv;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 16; j++) v[j] = j < E ? (xs[j] * inv) * ws[j] : 0.0f;
-        }
-        float amax = 0.0f;
+                for (int j = 0; j < EC; j++) v[j] = (xs[j] * inv) * ws[j];
+            }
+            float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            if (j < E) amax = fmaxf(amax, fabsf(v[j]));
-        // a 32-block spans 32/E consecutive lanes of one row
-        if (E == 8) amax = row_max<4>(amax);
-        else amax = row_max<2>(amax);
-        const float d = amax / 127.0f;
-        const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
-        int qsum = 0;
-        uint32_t packed[4] = {0, 0, 0, 0};
+            for (int j = 0; j < EC; j++) amax = fmaxf(amax, fabsf(v[j]));
+            // a 32-block spans 32/E consecutive lanes of one row
+            if (EC == 8) amax = row_max<4>(amax);
+            else amax = row_max<2>(amax);
+            const float d = amax / 127.0f;
+            const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+            int qsum = 0;
+            uint32_t packed[EC / 4];
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            if (j < E) {
+            for (int k = 0; k < EC / 4; k++) packed[k] = 0;
+#pragma unroll
+            for (int j = 0; j < EC; j++) {
                 const int8_t qq = q8_code(v[j] * id);
                 qsum += qq;
                 packed[j >> 2] |= (uint32_t)(uint8_t)qq << (8 * (j & 3));
             }
-        }
-        if (E == 8) {
-            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-            if (act) {
-                ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
-                if ((t & 3) == 0) {
-                    ls[t >> 2] = d;
-                    lsum[t >> 2] = qsum;
+            if constexpr (EC == 8) {
+                qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+                qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+                if (act) {
+                    ((v2i_t *)lq)[t] = v2i_t{(int)packed[0], (int)packed[1]};
+                    if ((t & 3) == 0) {
+                        ls[t >> 2] = d;
+                        lsum[t >> 2] = qsum;
+                    }
+                }
+            } else {
+                qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+                if (act) {
+                    ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+                    if ((t & 1) == 0) {
+                        ls[t >> 1] = d;
+                        lsum[t >> 1] = qsum;
+                    }
                 }
             }
-        } else {
-            qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-            if (act) {
-                ((v4i_t *)lq)[t] = v4i_t{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
-                if ((t & 1) == 0) {
-                    ls[t >> 1] = d;
-                    lsum[t >> 1] = qsum;
-                }
-            }
-        }
+        };
+        if (E == 8) body(std::integral_constant<int, 8>{});
+        else body(std::integral_constant<int, 16>{});
         ST_TS(10);
         __syncthreads();
     }
