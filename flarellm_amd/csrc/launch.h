@@ -104,7 +104,7 @@ inline MvsPlan mvs_gu_plan(int fmt, int F, int cols) {
     if (const char *e = measure_env("FLARE_GU_NW")) p.r = atoi(e);
     if (const char *e = measure_env("FLARE_GU_SU")) p.su = atoi(e);
     p.grid = std::max(1, std::min(nblk, 1024));
-    p.lds = mvs_lds_bytes(false, cols) + 32 * 4;
+    p.lds = mvs_lds_gu(cols, p.r);
     return p;
 }
 

@@ -86,7 +86,11 @@ struct Pc<F_Q4K> {
 template <>
 struct Pc<F_Q6K> {
     v4i_t ql, qh;
-    uint32_t sc;  // scale of the low-nibble weights | high-nibble weights << 8
+    // scales of the low- and high-nibble weights, each kept as loaded: a
+    // combining shift right after the loads would make the wave wait for
+    // them (and, completing in order, for every load before them) when the
+    // tile is issued instead of when it is consumed
+    uint32_t sc0, sc1;
     uint32_t d;
     __device__ __forceinline__ void load(const WDesc &W, int row, int step, int lane) {
         const int nsb = W.cols >> 8, span = nsb * 128;
@@ -97,7 +101,8 @@ struct Pc<F_Q6K> {
         qh = *(const v4i_t *)(W.h + rs * 64 + hf * 32 + (q & 1) * 16);  // 2 lanes share it
         const int si = hf * 8 + (q & 1) + 2 * (q >> 1);
         const uint8_t *scp = W.h2 + rs * 16;
-        sc = (uint32_t)scp[si] | ((uint32_t)scp[si + 4] << 8);
+        sc0 = scp[si];
+        sc1 = scp[si + 4];
         d = W.s[rs];
     }
 };
@@ -111,6 +116,30 @@ struct Pc<F_F32> {
         w = ld_stream_f(W.q + (size_t)row * K * 4 + off);
     }
 };
+
+// The persistent loops: unit u + 1's loads are in flight while unit u is
+// consumed (ta holds unit 0 on entry).  The steady-state loop issues its
+// loads unconditionally and the last one or two units are consumed after it:
+// with a load under a branch the compiler must assume the path that issued
+// none, and the consume of a tile would then wait for the next tile's loads
+// too (loads complete in order), losing the overlap.
+template <typename T, typename L, typename C>
+__device__ __forceinline__ void pingpong(int nunits, T &ta, T &tb, const L &load, const C &consume) {
+    int u = 0;
+    for (; u + 2 < nunits; u += 2) {
+        load(tb, u + 1);
+        consume(ta, u);
+        load(ta, u + 2);
+        consume(tb, u + 1);
+    }
+    if (u + 1 < nunits) {
+        load(tb, u + 1);
+        consume(ta, u);
+        consume(tb, u + 1);
+    } else if (u < nunits) {
+        consume(ta, u);
+    }
+}
 
 // ---- Q8 input (int8 activations in LDS) -----------------------------------
 // matvec_q8_0_preq_into per-block term (model.rs:8082-8099):
@@ -326,7 +355,7 @@ __device__ __forceinline__ float pc_dot_f32x(const Pc<F_Q6K> &P, const XIn<F_Q6K
         chi[j] = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> X.sh) & 0x30303030u);
     }
     const float slo = X.lo.dot<32>(clo), shi = X.hi.dot<32>(chi);
-    const float ds_lo = mul_h16lo(P.d, (float)(int8_t)(P.sc & 0xFF)), ds_hi = mul_h16lo(P.d, (float)(int8_t)(P.sc >> 8));
+    const float ds_lo = mul_h16lo(P.d, (float)(int8_t)P.sc0), ds_hi = mul_h16lo(P.d, (float)(int8_t)P.sc1);
     return X.ok ? ds_lo * slo + ds_hi * shi : 0.0f;
 }
 
@@ -377,6 +406,9 @@ struct MvsArgs {
 __host__ __device__ inline size_t mvs_lds_bytes(bool f32in, int K) {
     return f32in ? (size_t)K * 4 + (size_t)(K / 16) * 4 + 64 * 4 : (size_t)K + (size_t)(K / 32) * 8 + 64 * 4 + 64;
 }
+// gate/up: the Q8 input area, the 32 SiLU*up values of the current block,
+// then one 256-byte exp table per wave
+__host__ __device__ inline size_t mvs_lds_gu(int K, int nw) { return mvs_lds_bytes(false, K) + 32 * 4 + (size_t)nw * 256; }
 
 // prologue staging shared by both kernels: x (Q8 or f32) into LDS
 template <bool F32IN, int NT, bool SEQ = false, int VT = NT>
@@ -865,14 +897,8 @@ __device__ __forceinline__ void mvs_body(const MvsArgs &a, char *smem, int gw, i
         }
     };
     // ping-pong: the next unit's pieces are in flight while this one is
-    // consumed (a wave with no next unit issues nothing)
-    for (int u = 0; u < nunits; u += 2) {
-        if (u + 1 < nunits) load(tb, u + 1);
-        consume(ta, u);
-        if (u + 1 >= nunits) break;
-        if (u + 2 < nunits) load(ta, u + 2);
-        consume(tb, u + 1);
-    }
+    // consumed
+    pingpong(nunits, ta, tb, load, consume);
     MV_TS(4);
     if (a.epi == EPI_ARGMAX) {
         float *red = (float *)(smem + mvs_lds_fmt<FMT, F32IN>(K) - 64 * 4 - (F32IN ? 0 : 64));
@@ -934,12 +960,18 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
     MV_TSB(0);
     Stage<false, NT, SEQ> stg;
     typename std::conditional<RX == 2, RegX8L<SU>, RegX8<RX ? SU : 1, SEQ>>::type rx;
+    // the SiLU's exp table, one copy per wave in LDS: a global table load in
+    // the epilogue would wait for the next tile's loads (loads complete in
+    // order); an LDS read does not
+    uint64_t *etab = (uint64_t *)(hb + 32) + wave * 32;
+    const uint64_t etv = kExp2Tab[lane & 31];
     if constexpr (RX) rx.issue(a, lane);
     else stg.issue(a);
     FLARE_STAGE_BARRIER();
     load(ta, 0);  // unconditional, so the prologue waits for the activation loads only
+    if (lane < 32) etab[lane] = etv;
     MV_TS(1);
-    float *seqa = (float *)(smem + align16(mvs_lds_bytes(false, K) + 32 * 4));  // SEQ areas
+    float *seqa = (float *)(smem + align16(mvs_lds_gu(K, NW)));  // SEQ areas
     float *fs = seqa + wave * seq_wave_words(R, SU);
     if constexpr (RX) rx.finish(a, lane, fs);
     else stg.finish(a, smem, seqa);
@@ -978,7 +1010,7 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
             if (lane < 2) {
                 // silu_mul_into: g / (1 + exp(-g)) * u
                 const float g = lane ? acc[1] : acc[0], up = lane ? acc[3] : acc[2];
-                hb[wave * HU + item * 2 + lane] = (g / (1.0f + fl_expf(-g))) * up;
+                hb[wave * HU + item * 2 + lane] = (g / (1.0f + fl_expf_t(-g, etab))) * up;
             }
 #pragma unroll
             for (int r = 0; r < R; r++) acc[r] = 0.0f;
@@ -995,13 +1027,7 @@ __global__ __launch_bounds__(NW * 64) void k_mvs_gu(MvsArgs a) {
             }
         }
     };
-    for (int u = 0; u < nunits; u += 2) {
-        if (u + 1 < nunits) load(tb, u + 1);
-        consume(ta, u);
-        if (u + 1 >= nunits) break;
-        if (u + 2 < nunits) load(ta, u + 2);
-        consume(tb, u + 1);
-    }
+    pingpong(nunits, ta, tb, load, consume);
     MV_TS(5);
     MV_TSB(1);
 }
