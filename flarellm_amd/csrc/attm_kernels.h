@@ -756,23 +756,18 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
         // (Q8 at D = 128: 248 VGPRs with both tiles, no spills; 128k slots
         // 74 -> 71 us against reloading each half as it is consumed)
         AttmTile<KT, D> tile2;
-        for (int bi = wave; bi < nblk; bi += 2 * NW) {
-            if (bi + NW < nblk) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi);
-            if (bi + NW >= nblk) break;
-            if (bi + 2 * NW < nblk) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW);
-        }
+        const int nbw = wave < nblk ? (nblk - wave + NW - 1) / NW : 0;  // blocks wave, wave + NW, ...
+        pingpong(
+            nbw, tile, tile2,
+            [&](AttmTile<KT, D> &T, int j) { T.load(a, kvh, t0 + (wave + j * NW) * kAttmBlock, t1 - 1, lane); },
+            [&](AttmTile<KT, D> &T, int j) { process(T, wave + j * NW); });
     } else if constexpr (KIVI) {
         // 2-bit blocks ping-pong (small tiles), then the ring blocks
         Tile0 tile2;
-        for (int bi = wave; bi < nqb; bi += 2 * NW) {
-            if (bi + NW < nqb) tile2.load(a, kvh, t0 + (bi + NW) * kAttmBlock, t1 - 1, lane);
-            process(tile, bi);
-            if (bi + NW >= nqb) break;
-            if (bi + 2 * NW < nqb) tile.load(a, kvh, t0 + (bi + 2 * NW) * kAttmBlock, t1 - 1, lane);
-            process(tile2, bi + NW);
-        }
+        const int nbw = wave < nqb ? (nqb - wave + NW - 1) / NW : 0;
+        pingpong(
+            nbw, tile, tile2, [&](Tile0 &T, int j) { T.load(a, kvh, t0 + (wave + j * NW) * kAttmBlock, t1 - 1, lane); },
+            [&](Tile0 &T, int j) { process(T, wave + j * NW); });
         AttmTile<KvKivi, D> rt;
         const int bi0 = nqb > wave ? wave + (nqb - wave + NW - 1) / NW * NW : wave;
         for (int bi = bi0; bi < nblk; bi += NW) {

@@ -142,6 +142,30 @@ __device__ __forceinline__ float wg_sum(float v, float *red) {
     return t;
 }
 
+// Double-buffered streaming loops: unit u + 1's loads are in flight while
+// unit u is consumed (ta holds unit 0 on entry).  The steady-state loop issues its
+// loads unconditionally and the last one or two units are consumed after it:
+// with a load under a branch the compiler must assume the path that issued
+// none, and the consume of a tile would then wait for the next tile's loads
+// too (loads complete in order), losing the overlap.
+template <typename T, typename L, typename C>
+__device__ __forceinline__ void pingpong(int nunits, T &ta, T &tb, const L &load, const C &consume) {
+    int u = 0;
+    for (; u + 2 < nunits; u += 2) {
+        load(tb, u + 1);
+        consume(ta, u);
+        load(ta, u + 2);
+        consume(tb, u + 1);
+    }
+    if (u + 1 < nunits) {
+        load(tb, u + 1);
+        consume(ta, u);
+        consume(tb, u + 1);
+    } else if (u < nunits) {
+        consume(ta, u);
+    }
+}
+
 // Agent-scope relaxed atomic float store / load (cross-XCD visible without
 // a cache write-back fence).
 __device__ __forceinline__ void st_agent(float *p, float v) {

@@ -117,30 +117,6 @@ struct Pc<F_F32> {
     }
 };
 
-// The persistent loops: unit u + 1's loads are in flight while unit u is
-// consumed (ta holds unit 0 on entry).  The steady-state loop issues its
-// loads unconditionally and the last one or two units are consumed after it:
-// with a load under a branch the compiler must assume the path that issued
-// none, and the consume of a tile would then wait for the next tile's loads
-// too (loads complete in order), losing the overlap.
-template <typename T, typename L, typename C>
-__device__ __forceinline__ void pingpong(int nunits, T &ta, T &tb, const L &load, const C &consume) {
-    int u = 0;
-    for (; u + 2 < nunits; u += 2) {
-        load(tb, u + 1);
-        consume(ta, u);
-        load(ta, u + 2);
-        consume(tb, u + 1);
-    }
-    if (u + 1 < nunits) {
-        load(tb, u + 1);
-        consume(ta, u);
-        consume(tb, u + 1);
-    } else if (u < nunits) {
-        consume(ta, u);
-    }
-}
-
 // ---- Q8 input (int8 activations in LDS) -----------------------------------
 // matvec_q8_0_preq_into per-block term (model.rs:8082-8099):
 // (f16(w_scale) * x_scale) * (int dot as f32), counted once (even lane).
