@@ -129,56 +129,58 @@ __global__ __launch_bounds__(kMvoThreads) void k_mvo(MvoArgs a) {
         float acc[2] = {0.0f, 0.0f};  // tokens 2kg, 2kg+1
         if constexpr (FMT == F_Q6K) {
             const int nsb = K >> 8;
-            Q6Lane cur, nxt;
-            cur.load(W, row, 0, kg);
-            for (int sb = 0; sb < nsb; sb++) {
-                if (sb + 1 < nsb) nxt.load(W, row, sb + 1, kg);
-                const float d = h2f(cur.d);
-                const uint32_t scw[4] = {(uint32_t)cur.sc.x, (uint32_t)cur.sc.y, (uint32_t)cur.sc.z, (uint32_t)cur.sc.w};
+            Q6Lane ta, tb;
+            ta.load(W, row, 0, kg);
+            pingpong(
+                nsb, ta, tb, [&](Q6Lane &T, int sb) { T.load(W, row, sb, kg); },
+                [&](Q6Lane &cur, int sb) {
+                    const float d = h2f(cur.d);
+                    const uint32_t scw[4] = {(uint32_t)cur.sc.x, (uint32_t)cur.sc.y, (uint32_t)cur.sc.z,
+                                             (uint32_t)cur.sc.w};
 #pragma unroll
-                for (int hf = 0; hf < 2; hf++)
+                    for (int hf = 0; hf < 2; hf++)
 #pragma unroll
-                    for (int g = 0; g < 4; g++)
+                        for (int g = 0; g < 4; g++)
 #pragma unroll
-                        for (int h16 = 0; h16 < 2; h16++) {
-                            const uint32_t qlw = cur.ql[hf][g & 1][h16], qhw = cur.qh[hf][h16];
-                            const uint32_t codes = ((qlw >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
-                                                   (((qhw >> (2 * g)) & 0x03030303u) << 4);
-                            const v4h_t b = q6_codes_to_h4(codes);
-                            const int col = sb * 256 + hf * 128 + g * 32 + h16 * 16 + 4 * kg;
-                            v4h_t av = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-                            if (arow) av = *(const v4h_t *)(xrow + col);
-                            const v4fm_t dd = mfma_k16(av, b, v4fm_t{0.f, 0.f, 0.f, 0.f});
-                            const int si = hf * 8 + h16 + 2 * g;
-                            const float s = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFFu);
-                            acc[0] += s * (dd[0] + dd[1]);
-                            acc[1] += s * (dd[2] + dd[3]);
-                        }
-                cur = nxt;
-            }
+                            for (int h16 = 0; h16 < 2; h16++) {
+                                const uint32_t qlw = cur.ql[hf][g & 1][h16], qhw = cur.qh[hf][h16];
+                                const uint32_t codes = ((qlw >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
+                                                       (((qhw >> (2 * g)) & 0x03030303u) << 4);
+                                const v4h_t b = q6_codes_to_h4(codes);
+                                const int col = sb * 256 + hf * 128 + g * 32 + h16 * 16 + 4 * kg;
+                                v4h_t av = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                                if (arow) av = *(const v4h_t *)(xrow + col);
+                                const v4fm_t dd = mfma_k16(av, b, v4fm_t{0.f, 0.f, 0.f, 0.f});
+                                const int si = hf * 8 + h16 + 2 * g;
+                                const float s = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFFu);
+                                acc[0] += s * (dd[0] + dd[1]);
+                                acc[1] += s * (dd[2] + dd[3]);
+                            }
+                });
         } else {  // Q8_0
             const int nb = K >> 5;
             const int8_t *wq = (const int8_t *)W.q + (size_t)row * K + 8 * kg;
             const uint16_t *ws = W.s + (size_t)row * nb;
-            v2i_t cw = *(const v2i_t *)wq, nw2;
-            uint16_t cs = ws[0], ns = 0;
-            for (int b = 0; b < nb; b++) {
-                if (b + 1 < nb) {
-                    nw2 = *(const v2i_t *)(wq + 32 * (b + 1));
-                    ns = ws[b + 1];
-                }
-                const v8h2_t bv = i8_codes_to_h8((uint32_t)cw.x, (uint32_t)cw.y);
+            struct Q8Blk {
+                v2i_t w;
+                uint16_t s;
+            } ta, tb;
+            auto ld = [&](Q8Blk &T, int b) {
+                T.w = *(const v2i_t *)(wq + 32 * b);
+                T.s = ws[b];
+            };
+            ld(ta, 0);
+            pingpong(nb, ta, tb, ld, [&](Q8Blk &T, int b) {
+                const v8h2_t bv = i8_codes_to_h8((uint32_t)T.w.x, (uint32_t)T.w.y);
                 v8h2_t av;
 #pragma unroll
                 for (int i = 0; i < 8; i++) av[i] = (_Float16)0.0f;
                 if (arow) av = *(const v8h2_t *)(xrow + 32 * b + 8 * kg);
                 const v4fm_t dd = mfma_k32(av, bv, v4fm_t{0.f, 0.f, 0.f, 0.f});
-                const float s = h2f(cs);
+                const float s = h2f(T.s);
                 acc[0] += s * (dd[0] + dd[1]);
                 acc[1] += s * (dd[2] + dd[3]);
-                cw = nw2;
-                cs = ns;
-            }
+            });
         }
         // epilogue for row n, tokens 2kg + e
 #pragma unroll
