@@ -446,7 +446,10 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
         if constexpr (std::is_same<KT, KvQ8>::value) {
             // Q8 decode step: the block holding slot pos quantizes the new
             // token, stores it, and patches its K row / V column in registers
-            if (has_new && pos >= tb && pos < tb + kAttmBlock) {
+            // a wave-uniform branch (the position is a vector load: without
+            // readfirstlane the compiler lowers this as a divergent region and
+            // its waits land on every block)
+            if (__builtin_amdgcn_readfirstlane((int)(has_new && pos >= tb && pos < tb + kAttmBlock))) {
                 const int c = lane % (D / 8);  // lanes >= D/8 duplicate a chunk
                 nrow.build(a, kvh, c);
                 if (lane < D / 8) {
@@ -458,8 +461,7 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
                         nvs[c >> 2] = (uint16_t)(nrow.sc >> 16);
                     }
                 }
-                __builtin_amdgcn_s_waitcnt(0);
-                __builtin_amdgcn_wave_barrier();
+                lds_wave_sync();  // the codes / halves written to LDS above (the cache stores stay in flight)
                 const int pi = pos - tb, th = pi >> 4;
                 if ((pi & 15) == r) {
 #pragma unroll
@@ -487,7 +489,10 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
         }
         v8h_t ak[KQ ? DT : 1];
         if constexpr (KIVI || FUSED) if constexpr (!KQ) {
-            if (has_new && pos >= tb && pos < tb + kAttmBlock) {
+            // a wave-uniform branch (the position is a vector load: without
+            // readfirstlane the compiler lowers this as a divergent region and
+            // its waits land on every block)
+            if (__builtin_amdgcn_readfirstlane((int)(has_new && pos >= tb && pos < tb + kAttmBlock))) {
                 // decode step: the new token goes into the ring (binary16); the
                 // block holding it patches its K row / V column in registers
                 const int c = lane % (D / 8);
@@ -497,8 +502,7 @@ __device__ __forceinline__ void attm_body(const AttnArgs &a0, int bx, int by, in
                     *(v4i_t *)(nkh + 8 * c) = nrow.k;
                     *(v4i_t *)(nvh + 8 * c) = nrow.v;
                 }
-                __builtin_amdgcn_s_waitcnt(0);
-                __builtin_amdgcn_wave_barrier();
+                lds_wave_sync();  // the codes / halves written to LDS above (the cache stores stay in flight)
                 const int pi = pos - tb, th = pi >> 4;
                 if ((pi & 15) == r) {
 #pragma unroll
