@@ -59,8 +59,15 @@ inline void mvs_shape(int fmt, bool f32in, int S, bool pairs, int &r, int &su) {
     if (fmt == F_Q6K && f32in) { r = 2; su = 1; return; }
     if (S <= 1) { r = 4; su = 1; return; }
     // Q4_K with Q8 input, measured on MI355X (Llama-3-8B): QKV 4 rows x 1 KiB
-    // (9.8 vs 10.1 us for 2 x 2 KiB), wo / down 1 row x 2 KiB
-    if (fmt == F_Q4K) { r = pairs ? 4 : 1; su = pairs ? 1 : 2; return; }
+    // (8.0 vs 8.6-8.9 us for 2-row tiles); rows of one or two steps (wo) 2 x
+    // 2 KiB with the codes in registers (4.3 vs 4.7 us for 1 x 2 KiB), longer
+    // rows (down) 4 x 1 KiB (7.6 vs 8.4 us for 1 x 2 KiB, 7.9 for 2 x 1 KiB)
+    if (fmt == F_Q4K) {
+        if (pairs) { r = 4; su = 1; }
+        else if (S <= 2) { r = 2; su = 2; }
+        else { r = 4; su = 1; }
+        return;
+    }
     if (fmt == F_Q6K) { r = 2; su = 2; return; }
     if (S == 2 || S == 3) { r = 4; su = 2; return; }
     // long Q8_0 rows (Llama-3.2-1B down, 8 KiB): 1 row x 4 KiB measured best

@@ -23,7 +23,7 @@ namespace fl {
 
 hipError_t launch_mvs_q4k(const MvsPlan &p, hipStream_t st, const MvsArgs &a) {
     if (a.seq) {
-        SX(4, 1) SX(2, 1) SX(1, 2)
+        SX(4, 1) SX(2, 1) SX(2, 2) SX(1, 2)
         return hipErrorNotSupported;
     }
     // pre-quantized input whose row fits one unit: the lane's activation runs
