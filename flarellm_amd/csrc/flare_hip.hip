@@ -1535,6 +1535,11 @@ static int enqueue_step(fl_ctx *ctx, bool want_logits, bool x_given = false) {
         } else {
             AttnArgs a = layer_attn_args(ctx, l);
             if (probe) a.out = probe_attn;  // also the f32 output
+#ifdef FLARE_ATTN_TRACE
+            // trace builds: FLARE_ATTN_TRACE_LAYER = l records layer l's launch
+            if (measure_env("FLARE_ATTN_TRACE_LAYER") && l == atoi(measure_env("FLARE_ATTN_TRACE_LAYER")))
+                a.trace = ctx->bench_trace;
+#endif
             rc = launch_attention(ctx, ctx->kv_format, hd, G, a);
             if (rc) return rc;
         }
