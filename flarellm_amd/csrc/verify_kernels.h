@@ -242,7 +242,12 @@ __global__ __launch_bounds__(256) void k_vgemm_q4k(VgArgs a) {
 // step's loads in flight while this one is consumed, so the LDS footprint
 // does not grow with K.  Same per-block terms as k_vgemm_q8_0 / k_vgemm_q4k.
 // ---------------------------------------------------------------------------
-constexpr int kPgStride = 256 + 32;  // LDS row stride of one step's codes (bank spread)
+// LDS row stride of one step's codes: 68 dwords, so the 8-byte MFMA operand
+// reads of 16 token rows (dword 68 t + 2 kg) fall on distinct banks
+constexpr int kPgStride = 256 + 16;
+// plane stride of the [block][token] scale arrays: 80 floats, so the min-term
+// reads (block kg, token tA) and the staging stores spread over the banks
+constexpr int kPgPlane = 80;
 
 // One step's activation pieces in registers: 4 x 16 B of the 64 x 256 codes
 // and 2 of the 64 x 8 (scale, scale * code sum) pairs per thread.
@@ -279,7 +284,7 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const int i = t + 256 * u, o = (i & 7) * 64 + (i >> 3);
+        const int i = t + 256 * u, o = (i & 7) * kPgPlane + (i >> 3);
         ls[o] = r.sc[u].x;
         lq[o] = r.sc[u].x * r.sc[u].y;
     }
@@ -305,8 +310,8 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls
 template <int FMT, bool DOTS = false>
 __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
     __shared__ __align__(16) int8_t lx[2][64 * kPgStride];
-    __shared__ __align__(16) float lsc[2][8 * 64];  // [block][token] activation scales
-    __shared__ __align__(16) float lsq[2][8 * 64];  // [block][token] scale * code sum
+    __shared__ __align__(16) float lsc[2][8 * kPgPlane];  // [block][token] activation scales
+    __shared__ __align__(16) float lsq[2][8 * kPgPlane];  // [block][token] scale * code sum
     const WDesc &W = a.W;
     const int K = W.cols, nst = K >> 8;  // 256-value steps
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
                     const int t0 = 16 * tt + 4 * kg;  // tokens t0 .. t0+3 of this lane
-                    const v4f_t xs = *(const v4f_t *)&lsc[cur][j * 64 + t0];
+                    const v4f_t xs = *(const v4f_t *)&lsc[cur][j * kPgPlane + t0];
                     const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(xv[i] * dsc, (float)dd[tt][i], acc[tt][i]);
@@ -412,8 +417,8 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
                     v4f32_t c = {acc[tt][0], acc[tt][1], acc[tt][2], acc[tt][3]};
-                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][kg * 64 + tA + 16 * tt], nm0, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][(4 + kg) * 64 + tA + 16 * tt], nm1, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][kg * kPgPlane + tA + 16 * tt], nm0, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lsq[cur][(4 + kg) * kPgPlane + tA + 16 * tt], nm1, c, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[tt][i] = c[i];
                 }
