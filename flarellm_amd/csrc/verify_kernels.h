@@ -249,24 +249,28 @@ constexpr int kPgStride = 256 + 16;
 // reads (block kg, token tA) and the staging stores spread over the banks
 constexpr int kPgPlane = 80;
 
-// One step's activation pieces in registers: 4 x 16 B of the 64 x 256 codes
-// and 2 of the 64 x 8 (scale, scale * code sum) pairs per thread.
+// One step's activation pieces in registers, staged by NT threads: 1024
+// pieces of 16 code bytes (token i / 16, bytes 16 (i % 16)) and 512
+// (scale, scale * code sum) pairs (token i / 8, block i % 8).
+template <int NT>
 struct PgStage {
-    v4i_t q[4];
-    float2 sc[2];
+    static constexpr int QN = 1024 / NT, SN = 512 / NT;
+    v4i_t q[QN];
+    float2 sc[SN];
 };
 
-__device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage &r) {
+template <int NT>
+__device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage<NT> &r) {
     const int K = a.W.cols, t = threadIdx.x;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int i = t + 256 * u;  // 1024 pieces of 16 B: token i / 16, bytes 16 (i % 16)
+    for (int u = 0; u < PgStage<NT>::QN; u++) {
+        const int i = t + NT * u;
         const int tok = min(i >> 4, a.M - 1);
         r.q[u] = *(const v4i_t *)(a.xq + (size_t)tok * K + k0 + 16 * (i & 15));
     }
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int i = t + 256 * u;  // 512 pairs: token i / 8, block i % 8
+    for (int u = 0; u < PgStage<NT>::SN; u++) {
+        const int i = t + NT * u;
         const int tok = min(i >> 3, a.M - 1);
         const size_t o = (size_t)tok * (K >> 5) + (k0 >> 5) + (i & 7);
         r.sc[u] = make_float2(a.xs[o], (float)a.xsum[o]);
@@ -275,16 +279,17 @@ __device__ __forceinline__ void pg_load(const VgArgs &a, int k0, PgStage &r) {
 
 // codes [token][kPgStride]; scales and scale * code sums as [block][token]
 // planes, so the four tokens of an MFMA output lane are one 16-B read each
-__device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls, float *lq) {
+template <int NT>
+__device__ __forceinline__ void pg_store(const PgStage<NT> &r, int8_t *lx, float *ls, float *lq) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int i = t + 256 * u;
+    for (int u = 0; u < PgStage<NT>::QN; u++) {
+        const int i = t + NT * u;
         *(v4i_t *)(lx + (i >> 4) * kPgStride + 16 * (i & 15)) = r.q[u];
     }
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int i = t + 256 * u, o = (i & 7) * kPgPlane + (i >> 3);
+    for (int u = 0; u < PgStage<NT>::SN; u++) {
+        const int i = t + NT * u, o = (i & 7) * kPgPlane + (i >> 3);
         ls[o] = r.sc[u].x;
         lq[o] = r.sc[u].x * r.sc[u].y;
     }
@@ -307,8 +312,11 @@ __device__ __forceinline__ void pg_store(const PgStage &r, int8_t *lx, float *ls
 // DOTS: also write each per-block integer dot to a.dots (the readback of
 // fl_op_batched_block_dots; a separate instantiation, so the product's has
 // no trace of it)
-template <int FMT, bool DOTS = false>
-__global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
+// NW waves (16 rows each) share the staged activations; NW = 8 runs with at
+// most 128 VGPRs, so two workgroups (16 waves) fit on a CU beside their LDS.
+template <int FMT, bool DOTS = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 1)))
+void k_pgemm(VgArgs a) {
     __shared__ __align__(16) int8_t lx[2][64 * kPgStride];
     __shared__ __align__(16) float lsc[2][8 * kPgPlane];  // [block][token] activation scales
     __shared__ __align__(16) float lsq[2][8 * kPgPlane];  // [block][token] scale * code sum
@@ -317,7 +325,7 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int s0 = blockIdx.y * a.chunk, s1 = min(nst, s0 + a.chunk);
     if (s0 >= s1) return;
-    const int tile = blockIdx.x * 4 + wave;
+    const int tile = blockIdx.x * NW + wave;
     const int n = tile * 16 + (lane & 15), kg = lane >> 4, tA = lane & 15;
     const int row = min(n, W.rows - 1);
     float acc[4][4];
@@ -344,7 +352,7 @@ __global__ __launch_bounds__(256) void k_pgemm(VgArgs a) {
             for (int jj = 0; jj < 8; jj++) sn[jj] = W.s[(size_t)row * (K >> 5) + 8 * st + jj];
         }
     };
-    PgStage xr;
+    PgStage<NW * 64> xr;
     wload(s0);
     pg_load(a, s0 * 256, xr);
     pg_store(xr, lx[0], lsc[0], lsq[0]);
