@@ -371,7 +371,7 @@ def run_decode(args, config: str, with_cpu: bool) -> dict:
                 "kernel": f"{dom} ({d['kernel']})", "bytes_per_launch": d["bytes"],
                 "avg_launch_us": d["us"]}
 
-    # time to first token through fl_prefill (16-token int8-MFMA passes) of
+    # time to first token through fl_prefill (64-token int8-MFMA passes) of
     # the same prompt, against the decode-step path above
     prefill = None
     if n_prompt > 1:
